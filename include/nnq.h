@@ -1,0 +1,206 @@
+/*
+ * nnq — MI355X (gfx950) quantized-linear hot path: C ABI.
+ *
+ * Drop-in boundary for alabsystems/nn's dequant-fused matmul over GGUF block
+ * formats (Q8_0, Q4_K, Q6_K) and the GPT-OSS MXFP4 mixture-of-experts layer.
+ * A Rust backend crate binds these symbols with `extern "C"` (the binding is
+ * shown in INTEGRATION.md) the way nn-cuda binds libamdhip64
+ * (crates/nn-cuda/src/hip_runtime_ffi_linux.rs:17-47): plain pointers, sizes
+ * and i32 status codes, no C++ or torch types.
+ *
+ * Conventions
+ *  - Every call returns an nnq_status; on failure nnq_last_error() returns a
+ *    thread-local message.
+ *  - Device pointers (x, y, bias, logits, outputs) live on the current HIP
+ *    device; `stream` is a hipStream_t (NULL = the null stream).  Compute calls
+ *    are asynchronous on `stream` and never synchronize the host.
+ *  - Weight handles are immutable after creation and may be shared across
+ *    threads and streams.
+ *  - Weights are row-major W[n, k] (out_features x in_features) with blocks
+ *    along k, as QuantizedStorage / QuantizedWeight store them
+ *    (crates/nn-core/src/dyn_tensor/quantized.rs:109-172,
+ *     crates/nn-core/src/layers/quantized/linear.rs:260-264).
+ */
+#ifndef NNQ_H
+#define NNQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The quantized-matmul kinds mirror QuantizedMatmulError
+ * (crates/nn-core/src/dyn_tensor/quantized_matmul.rs:30-82); the tensor and
+ * backend kinds mirror TensorError / BackendErrorKind
+ * (crates/nn-core/src/error.rs:48-93,171). */
+typedef enum nnq_status {
+    NNQ_OK = 0,
+    NNQ_ERR_INVALID_ARGUMENT = 1,  /* null pointer, negative or zero size where not allowed */
+    NNQ_ERR_SHAPE_MISMATCH = 2,    /* QuantizedMatmulError::ShapeMismatch (input K != weight K) */
+    NNQ_ERR_WRONG_FORMAT = 3,      /* QuantizedMatmulError::WrongQuantType / unsupported layout */
+    NNQ_ERR_NOT_QUANTIZED = 4,     /* QuantizedMatmulError::NotQuantized */
+    NNQ_ERR_WEIGHT_RANK = 5,       /* QuantizedMatmulError::WeightRank */
+    NNQ_ERR_BIAS_MISMATCH = 6,     /* QuantizedMatmulError::BiasMismatch */
+    NNQ_ERR_DATA_LENGTH = 7,       /* TensorError::DataLengthMismatch */
+    NNQ_ERR_INVALID_SHAPE = 8,     /* TensorError::InvalidShape (element count not a block multiple) */
+    NNQ_ERR_NON_FINITE = 9,        /* TensorError::NonFiniteData / ValueOutOfRange */
+    NNQ_ERR_NO_DEVICE = 10,        /* no HIP device */
+    NNQ_ERR_OUT_OF_MEMORY = 11,    /* BackendErrorKind::OutOfMemory */
+    NNQ_ERR_DISPATCH_FAILED = 12,  /* BackendErrorKind::DispatchFailed */
+    NNQ_ERR_UNSUPPORTED = 13       /* TensorError::Unsupported */
+} nnq_status;
+
+/* Block formats; values are the GGUF type ids (GgufDType,
+ * crates/nn-gguf/src/dequant.rs:14-45).  MXFP4 uses ggml's id 39. */
+typedef enum nnq_format {
+    NNQ_FMT_Q8_0 = 8,
+    NNQ_FMT_Q4_K = 12,
+    NNQ_FMT_Q6_K = 14,
+    NNQ_FMT_MXFP4 = 39
+} nnq_format;
+
+/* Byte layouts.  The reference carries more than one decoder per format:
+ *  NNQ_LAYOUT_GGUF    Q8_0 (crates/nn-core/src/dyn_tensor/quantized.rs:237-253) and
+ *                     Q4_K as nn-core BlockQ4K (crates/nn-core/src/layers/quantized/linear.rs:49-92,166-176).
+ *  NNQ_LAYOUT_NN_GGUF nn-gguf's own decoders: Q4_K (crates/nn-gguf/src/dequant.rs:335-398),
+ *                     Q6_K (crates/nn-gguf/src/dequant.rs:415-459, the only Q6_K decoder), Q8_0 (:178-196).
+ *  NNQ_LAYOUT_GPTOSS  GPT-OSS Mxfp4Tensor (crates/nn-gptoss/src/quantize.rs:122-188): packed bytes with
+ *                     the HIGH nibble = even element, E8M0 scales in a separate array, byte 0 -> 2^-126. */
+typedef enum nnq_layout {
+    NNQ_LAYOUT_GGUF = 0,
+    NNQ_LAYOUT_NN_GGUF = 1,
+    NNQ_LAYOUT_GPTOSS = 2
+} nnq_layout;
+
+typedef enum nnq_dtype {
+    NNQ_F32 = 0,
+    NNQ_F16 = 1,
+    NNQ_BF16 = 2
+} nnq_dtype;
+
+typedef struct nnq_weight nnq_weight;   /* opaque: device-resident, repacked block weight */
+typedef struct nnq_moe nnq_moe;         /* opaque: device-resident MXFP4 expert weights + biases */
+
+/* ---- device ------------------------------------------------------------------- */
+
+/* Count HIP devices (0 when none).  Replaces the device probe of nn-cuda's HIP
+ * runtime (crates/nn-cuda/src/hip_runtime.rs:191). */
+int nnq_device_count(int *count);
+
+/* Make `device` current for this thread and initialise per-device state.
+ * NNQ_ERR_NO_DEVICE when no HIP device exists.  Counterpart of
+ * register_gpu_backend (crates/nn-core/src/dyn_tensor/gpu.rs:156-162). */
+int nnq_init(int device);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char *nnq_last_error(void);
+
+/* ---- weights ------------------------------------------------------------------ */
+
+/* Upload host block bytes for W[n, k] to the current device, repacked into the
+ * device layout.  The caller keeps ownership of `bytes`.  Validation follows
+ * QuantizedStorage::new (crates/nn-core/src/dyn_tensor/quantized.rs:121-140):
+ * NNQ_ERR_INVALID_SHAPE when k is not a multiple of the block size (32 for Q8_0,
+ * 256 for Q4_K/Q6_K), NNQ_ERR_DATA_LENGTH when nbytes != n*k/block*block_bytes.
+ * Replaces DynTensor::from_quantized (:270-278) and QLinear::from_linear's
+ * block storage (crates/nn-core/src/layers/quantized/linear.rs:309-346). */
+int nnq_weight_create(nnq_format fmt, nnq_layout layout, const uint8_t *bytes, size_t nbytes, int64_t n,
+                      int64_t k, nnq_weight **out);
+
+int nnq_weight_destroy(nnq_weight *w);
+
+/* Shape / format queries (QuantizedStorage::shape / quant_type, quantized.rs:142-152). */
+int nnq_weight_info(const nnq_weight *w, int *fmt, int *layout, int64_t *n, int64_t *k, size_t *device_bytes);
+
+/* Decode the whole weight to f32 W[n, k] at device pointer `out` — bit-exact with
+ * QuantizedStorage::dequantize / BlockQ4K::dequantize / dequantize_q6_k
+ * (crates/nn-core/src/dyn_tensor/quantized.rs:155-165,
+ *  crates/nn-core/src/layers/quantized/linear.rs:268-281,
+ *  crates/nn-gguf/src/dequant.rs:178-196,335-459). */
+int nnq_dequant(const nnq_weight *w, float *out, void *stream);
+
+/* ---- quantized linear ----------------------------------------------------------- */
+
+/* y[m, n] = x[m, k] @ W^T (+ bias[n]).  `m` folds every leading batch dimension
+ * (rank folding as in quantized_matmul_core, quantized_matmul.rs:232-272); m = 0
+ * is a no-op.  `k` is the input's last dimension: k != weight k gives
+ * NNQ_ERR_SHAPE_MISMATCH (validate_input, :121-145).  bias: f32 [bias_len] or
+ * NULL; bias_len != n gives NNQ_ERR_BIAS_MISMATCH (:391-401).
+ * x: NNQ_F32 or NNQ_BF16 (bf16 is widened exactly to f32, ops/matmul.rs:20-21);
+ * y: NNQ_F32, or NNQ_BF16 (f32 accumulate, rounded to bf16 once, ops/matmul.rs:37-38).
+ * Replaces quantized_linear / quantized_matmul_q8_0 (quantized_matmul.rs:335-406)
+ * and QLinear::forward (crates/nn-core/src/layers/quantized/linear.rs:366-400). */
+int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m, int64_t k, const float *bias,
+               int64_t bias_len, void *y, nnq_dtype y_dtype, void *stream);
+
+/* First index of the maximum of logits[n] (strict `>`), written as u32 to
+ * `idx` (device).  NaN input -> *status_dev = NNQ_ERR_NON_FINITE (device int,
+ * may be NULL).  Replaces DynTensor::argmax on the last dim
+ * (crates/nn-core/src/dyn_tensor/ops_ext/argreduce.rs:19,94-118). */
+int nnq_argmax_f32(const float *logits, int64_t n, uint32_t *idx, int32_t *status_dev, void *stream);
+
+/* LM head: logits[n] = x[k] @ W^T (+bias) fused with the first-index argmax.
+ * Replaces lm_head Linear + argmax (crates/nn-qwen3/src/lib.rs:124-133,
+ * crates/nn-core/src/dyn_tensor/ops_ext/argreduce.rs:105-118). */
+int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const float *bias, int64_t bias_len,
+                      float *logits, uint32_t *idx, int32_t *status_dev, void *stream);
+
+/* ---- GPT-OSS MXFP4 mixture of experts ----------------------------------------- */
+
+/* Upload one layer's expert weights in the GPT-OSS convention:
+ *  gate_up: Mxfp4Tensor of the flat [E, hidden, 2*inter] f32 tensor
+ *           (packed bytes E*hidden*2*inter/2, scales E*hidden*2*inter/32),
+ *  down:    Mxfp4Tensor of the flat [E, inter, hidden] tensor,
+ *  biases:  f32 [E, 2*inter] and [E, hidden] (host).
+ * Replaces QuantizedDecoderLayer::load's expert tensors
+ * (crates/nn-gptoss/src/quantized_model.rs:70-78). */
+int nnq_moe_create(int64_t num_experts, int64_t hidden, int64_t inter, const uint8_t *gu_packed,
+                   const uint8_t *gu_scales, const float *gu_bias, const uint8_t *dn_packed,
+                   const uint8_t *dn_scales, const float *dn_bias, nnq_moe **out);
+
+int nnq_moe_destroy(nnq_moe *moe);
+
+/* y[t, hidden] (f32) = MoE(x[t, hidden]) with router logits [t, E] (f32):
+ * softmax -> top_k -> renormalise -> per expert clamp(silu(x@Wg+bg), -limit, limit)
+ * * (x@Wu+bu) -> @Wd + bd -> weighted sum.  x: NNQ_F32 or NNQ_BF16.  Routing,
+ * permutation and combine run on the device (no host synchronisation).
+ * Optional outputs topk_idx [t, top_k] u32 and topk_w [t, top_k] f32 (device).
+ * Replaces QuantizedDecoderLayer::moe_forward / expert_forward
+ * (crates/nn-gptoss/src/quantized_model.rs:99-194). */
+int nnq_moe_forward(const nnq_moe *moe, const void *x, nnq_dtype x_dtype, int64_t tokens,
+                    const float *router_logits, int top_k, float swiglu_limit, float *y, uint32_t *topk_idx,
+                    float *topk_w, void *stream);
+
+/* Decode expert e's weights to f32 (device): gate_up [hidden, 2*inter] and down
+ * [inter, hidden] — bit-exact with Mxfp4Tensor::dequantize
+ * (crates/nn-gptoss/src/quantize.rs:167-188). Either output may be NULL. */
+int nnq_moe_dequant_expert(const nnq_moe *moe, int64_t expert, float *gate_up, float *down, void *stream);
+
+/* ---- host encoders (CPU, no device needed) --------------------------------------- */
+
+/* BlockQ4K::quantize over a flat f32 buffer, zero-padded to 256 as
+ * QLinear::from_linear does (crates/nn-core/src/layers/quantized/linear.rs:95-162,
+ * 309-346).  `out` holds ceil(n/256)*144 bytes.  NNQ_ERR_NON_FINITE on NaN/inf. */
+int nnq_quantize_q4_k(const float *v, size_t n, uint8_t *out);
+
+/* Mxfp4Tensor::quantize (crates/nn-gptoss/src/quantize.rs:122-163): `packed`
+ * holds ceil(n/32)*16 bytes, `scales` ceil(n/32) bytes. */
+int nnq_quantize_mxfp4(const float *v, size_t n, uint8_t *packed, uint8_t *scales);
+
+/* Q8_0 and nn-gguf-layout Q6_K encoders.  The reference ships no encoder for
+ * either (its tests hand-build blocks, quantized_matmul_tests.rs:37-46); these
+ * are this library's own input generators.  n must be a block multiple. */
+int nnq_quantize_q8_0(const float *v, size_t n, uint8_t *out);
+int nnq_quantize_q6_k(const float *v, size_t n, uint8_t *out);
+
+/* Seeded N(0, sigma) f32 generator: splitmix64 (crates/nn-core/src/test_prng.rs:18-22)
+ * keyed by (seed, tensor_id, index), uniform from the top 53 bits (:31-33),
+ * Box-Muller in f64, cast to f32. */
+int nnq_synth_normal(uint64_t seed, uint64_t tensor_id, size_t n, double sigma, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NNQ_H */

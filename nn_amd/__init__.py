@@ -1,0 +1,13 @@
+"""nn_amd — MI355X (gfx950) quantized-linear hot path for alabsystems/nn.
+
+Hand-written HIP kernels behind a C ABI (``include/nnq.h``, ``libnnq.so``) for
+the dequant-fused matmul over GGUF Q8_0 / Q4_K / Q6_K blocks and the GPT-OSS
+MXFP4 mixture-of-experts layer; ``nn_amd.quantized`` mirrors the reference's
+operator surface in Python.
+"""
+from .quantized import (  # noqa: F401
+    BiasMismatch, DataLengthMismatch, InvalidShape, Layout, NonFiniteData, NotQuantized, QuantizedMatmulError,
+    QuantizedMoE, QuantizedWeight, QuantType, RankMismatch, ShapeMismatch, TensorError, Unsupported, WeightRank,
+    WrongQuantType, argmax, device_count, init, linear_argmax, quantize_mxfp4, quantize_q4_k, quantize_q6_k,
+    quantize_q8_0, quantized_linear, quantized_matmul_q4_k, quantized_matmul_q6_k, quantized_matmul_q8_0,
+    synth_normal)

@@ -1,0 +1,420 @@
+// C ABI of the nnq library (include/nnq.h): validation, device memory, repack
+// upload and kernel dispatch.  Error semantics follow the reference's
+// quantized-matmul / tensor errors; messages are kept per thread.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "nnq_internal.h"
+
+using namespace nnq;
+
+struct nnq_weight {
+    Layout L;
+    uint8_t *dev = nullptr;
+    int device = 0;
+};
+
+struct nnq_moe {
+    MoeDev d;
+    int device = 0;
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+        return fail(NNQ_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+    return fail(NNQ_ERR_DISPATCH_FAILED, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                       \
+    do {                                          \
+        hipError_t _e = (expr);                   \
+        if (_e != hipSuccess) return hip_fail(_e, what); \
+    } while (0)
+
+size_t block_elems(int fmt) { return fmt == NNQ_FMT_Q8_0 ? 32 : 256; }
+size_t block_bytes(int fmt) {
+    switch (fmt) {
+    case NNQ_FMT_Q8_0: return 34;
+    case NNQ_FMT_Q4_K: return 144;
+    case NNQ_FMT_Q6_K: return 210;
+    }
+    return 0;
+}
+
+// Stream-ordered scratch owned by one call.
+struct Scratch {
+    void *p = nullptr;
+    hipStream_t s = nullptr;
+    ~Scratch() {
+        if (p) (void)hipFreeAsync(p, s);
+    }
+    hipError_t alloc(size_t n, hipStream_t st) {
+        s = st;
+        return hipMallocAsync(&p, n ? n : 16, st);
+    }
+};
+
+template <class F>
+void parallel_for(int64_t n, F &&fn) {
+    int64_t nt = std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), std::max<int64_t>(1, n / 64));
+    if (nt <= 1) {
+        fn(0, n);
+        return;
+    }
+    std::vector<std::thread> th;
+    int64_t per = (n + nt - 1) / nt;
+    for (int64_t t = 0; t < nt; t++) {
+        int64_t lo = t * per, hi = std::min(n, lo + per);
+        if (lo < hi) th.emplace_back([&fn, lo, hi] { fn(lo, hi); });
+    }
+    for (auto &x : th) x.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *nnq_last_error(void) { return g_err.c_str(); }
+
+int nnq_device_count(int *count) {
+    if (!count) return fail(NNQ_ERR_INVALID_ARGUMENT, "count is null");
+    int c = 0;
+    hipError_t e = hipGetDeviceCount(&c);
+    *count = (e == hipSuccess) ? c : 0;
+    return NNQ_OK;
+}
+
+int nnq_init(int device) {
+    int c = 0;
+    if (hipGetDeviceCount(&c) != hipSuccess || c == 0) return fail(NNQ_ERR_NO_DEVICE, "no HIP device");
+    if (device < 0 || device >= c) return fail(NNQ_ERR_INVALID_ARGUMENT, "device %d out of range (%d)", device, c);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (!std::strstr(prop.gcnArchName, "gfx950"))
+        return fail(NNQ_ERR_UNSUPPORTED, "kernels are built for gfx950, device is %s", prop.gcnArchName);
+    return NNQ_OK;
+}
+
+int nnq_weight_create(nnq_format fmt, nnq_layout layout, const uint8_t *bytes, size_t nbytes, int64_t n, int64_t k,
+                      nnq_weight **out) {
+    if (!out) return fail(NNQ_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (fmt != NNQ_FMT_Q8_0 && fmt != NNQ_FMT_Q4_K && fmt != NNQ_FMT_Q6_K)
+        return fail(NNQ_ERR_WRONG_FORMAT, "format %d is not a linear-weight block format", (int)fmt);
+    if (n <= 0 || k <= 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "weight shape [%lld, %lld]", (long long)n, (long long)k);
+    if ((size_t)k % block_elems(fmt))
+        return fail(NNQ_ERR_INVALID_SHAPE, "in_features %lld is not a multiple of the block size %zu", (long long)k,
+                    block_elems(fmt));
+    size_t expect = (size_t)n * ((size_t)k / block_elems(fmt)) * block_bytes(fmt);
+    if (nbytes != expect)
+        return fail(NNQ_ERR_DATA_LENGTH, "data length mismatch: expected %zu bytes, got %zu", expect, nbytes);
+    if (!bytes) return fail(NNQ_ERR_INVALID_ARGUMENT, "bytes is null");
+    Layout L;
+    const char *err = nullptr;
+    if (!make_layout(fmt, layout, n, k, &L, &err)) return fail(NNQ_ERR_WRONG_FORMAT, "%s", err);
+    std::vector<uint8_t> host(L.total());
+    // repack tile by tile in parallel (disjoint output ranges)
+    switch (fmt) {
+    case NNQ_FMT_Q4_K:
+    case NNQ_FMT_Q6_K: {
+        // each tile's rows map to disjoint destination ranges; run the whole-weight repack
+        // on row-tile slices of a sub-layout to parallelise.
+        parallel_for(L.ntile, [&](int64_t lo, int64_t hi) {
+            Layout S = L;
+            S.n = std::min<int64_t>(L.n - lo * kTile, (hi - lo) * kTile);
+            S.ntile = hi - lo;
+            size_t per_q = L.qs_bytes / L.ntile, per_h = L.hdr_bytes / L.ntile;
+            S.qs_bytes = per_q * S.ntile;
+            S.hdr_bytes = per_h * S.ntile;
+            std::vector<uint8_t> tmp(S.total());
+            const uint8_t *src = bytes + (size_t)lo * kTile * (k / 256) * block_bytes(fmt);
+            if (fmt == NNQ_FMT_Q4_K)
+                repack_q4k(src, layout == NNQ_LAYOUT_NN_GGUF, S, tmp.data());
+            else
+                repack_q6k(src, S, tmp.data());
+            std::memcpy(host.data() + per_q * lo, tmp.data(), S.qs_bytes);
+            std::memcpy(host.data() + L.qs_bytes + per_h * lo, tmp.data() + S.qs_bytes, S.hdr_bytes);
+        });
+        break;
+    }
+    case NNQ_FMT_Q8_0:
+        repack_q8_0(bytes, L, host.data());
+        break;
+    }
+    nnq_weight *w = new nnq_weight;
+    w->L = L;
+    hipGetDevice(&w->device);
+    hipError_t e = hipMalloc(&w->dev, L.total());
+    if (e != hipSuccess) {
+        delete w;
+        return hip_fail(e, "hipMalloc(weight)");
+    }
+    e = hipMemcpy(w->dev, host.data(), L.total(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(w->dev);
+        delete w;
+        return hip_fail(e, "hipMemcpy(weight)");
+    }
+    *out = w;
+    return NNQ_OK;
+}
+
+int nnq_weight_destroy(nnq_weight *w) {
+    if (!w) return NNQ_OK;
+    if (w->dev) hipFree(w->dev);
+    delete w;
+    return NNQ_OK;
+}
+
+int nnq_weight_info(const nnq_weight *w, int *fmt, int *layout, int64_t *n, int64_t *k, size_t *device_bytes) {
+    if (!w) return fail(NNQ_ERR_NOT_QUANTIZED, "weight handle is null");
+    if (fmt) *fmt = w->L.fmt;
+    if (layout) *layout = w->L.layout;
+    if (n) *n = w->L.n;
+    if (k) *k = w->L.k;
+    if (device_bytes) *device_bytes = w->L.total();
+    return NNQ_OK;
+}
+
+int nnq_dequant(const nnq_weight *w, float *out, void *stream) {
+    if (!w) return fail(NNQ_ERR_NOT_QUANTIZED, "weight handle is null");
+    if (!out) return fail(NNQ_ERR_INVALID_ARGUMENT, "out is null");
+    int e = launch_dequant(w->L.fmt, w->dev, w->dev + w->L.qs_bytes, w->L.n, w->L.k, w->L.ntile, w->L.nblk, out,
+                           stream);
+    if (e) return hip_fail((hipError_t)e, "dequant launch");
+    return NNQ_OK;
+}
+
+static int check_linear(const nnq_weight *w, const void *x, nnq_dtype xd, int64_t m, int64_t k, const float *bias,
+                        int64_t bias_len, void *y, nnq_dtype yd) {
+    if (!w) return fail(NNQ_ERR_NOT_QUANTIZED, "weight tensor is not quantized (null handle)");
+    if (m < 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "m = %lld", (long long)m);
+    if (k != w->L.k)
+        return fail(NNQ_ERR_SHAPE_MISMATCH,
+                    "quantized matmul shape mismatch: input last dim %lld != weight in_features %lld", (long long)k,
+                    (long long)w->L.k);
+    if (bias && bias_len != w->L.n)
+        return fail(NNQ_ERR_BIAS_MISMATCH, "bias shape mismatch: expected [%lld], got [%lld]", (long long)w->L.n,
+                    (long long)bias_len);
+    if (m > 0 && (!x || !y)) return fail(NNQ_ERR_INVALID_ARGUMENT, "x or y is null");
+    if (xd != NNQ_F32 && xd != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d (f32 or bf16)", (int)xd);
+    if (yd != NNQ_F32 && yd != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "output dtype %d (f32 or bf16)", (int)yd);
+    if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(NNQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    return NNQ_OK;
+}
+
+int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m, int64_t k, const float *bias,
+               int64_t bias_len, void *y, nnq_dtype y_dtype, void *stream) {
+    int rc = check_linear(w, x, x_dtype, m, k, bias, bias_len, y, y_dtype);
+    if (rc) return rc;
+    if (m == 0) return NNQ_OK;
+    const Layout &L = w->L;
+    const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, ye = y_dtype == NNQ_BF16 ? 2 : 4;
+    if (L.fmt == NNQ_FMT_Q4_K && m > 8) {
+        // prefill: LDS-staged MFMA GEMM
+        GemmArgs g{};
+        g.qs = w->dev;
+        g.hdr = w->dev + L.qs_bytes;
+        g.x = x;
+        g.x_bf16 = x_dtype == NNQ_BF16;
+        g.bias = bias;
+        g.y = y;
+        g.y_bf16 = y_dtype == NNQ_BF16;
+        g.n = L.n;
+        g.k = L.k;
+        g.m = m;
+        g.ntile = L.ntile;
+        g.nblk = L.nblk;
+        Scratch s;
+        HIP_TRY(s.alloc(gemm_scratch_bytes(m, L.k), (hipStream_t)stream), "scratch alloc");
+        uint8_t *base = (uint8_t *)s.p;
+        g.xs = (uint16_t *)base;
+        g.rowscale = (float *)(base + (size_t)m * L.k * 2);
+        g.xsum = (float *)(base + (size_t)m * L.k * 2 + (size_t)m * 4 + 256 - ((size_t)m * 4) % 256);
+        int e = launch_gemm_q4k(g, stream);
+        if (e) return hip_fail((hipError_t)e, "gemm launch");
+        return NNQ_OK;
+    }
+    const int64_t mmax = L.fmt == NNQ_FMT_Q6_K ? 4 : 8;
+    for (int64_t m0 = 0; m0 < m; m0 += mmax) {
+        GemvArgs a{};
+        a.qs = w->dev;
+        a.hdr = w->dev + L.qs_bytes;
+        a.x = (const uint8_t *)x + (size_t)m0 * k * xe;
+        a.x_bf16 = x_dtype == NNQ_BF16;
+        a.bias = bias;
+        a.y = (uint8_t *)y + (size_t)m0 * L.n * ye;
+        a.y_bf16 = y_dtype == NNQ_BF16;
+        a.n = L.n;
+        a.k = L.k;
+        a.m = std::min(mmax, m - m0);
+        a.ntile = L.ntile;
+        a.nblk = L.nblk;
+        int e = launch_gemv(L.fmt, a, stream);
+        if (e) return hip_fail((hipError_t)e, "gemv launch");
+    }
+    return NNQ_OK;
+}
+
+int nnq_argmax_f32(const float *logits, int64_t n, uint32_t *idx, int32_t *status_dev, void *stream) {
+    if (!logits || !idx) return fail(NNQ_ERR_INVALID_ARGUMENT, "null pointer");
+    if (n <= 0) return fail(NNQ_ERR_INVALID_SHAPE, "argmax over a zero-length dimension");
+    if (n > 0xFFFFFFFFll) return fail(NNQ_ERR_INVALID_SHAPE, "argmax dim exceeds u32::MAX");
+    Scratch s;
+    const size_t bytes = 1024 * sizeof(unsigned long long);
+    HIP_TRY(s.alloc(bytes, (hipStream_t)stream), "scratch alloc");
+    int e = launch_argmax_reduce(logits, n, idx, status_dev, s.p, bytes, stream);
+    if (e) return hip_fail((hipError_t)e, "argmax launch");
+    return NNQ_OK;
+}
+
+int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const float *bias, int64_t bias_len,
+                      float *logits, uint32_t *idx, int32_t *status_dev, void *stream) {
+    int rc = check_linear(w, x, NNQ_F32, 1, k, bias, bias_len, logits, NNQ_F32);
+    if (rc) return rc;
+    if (!idx) return fail(NNQ_ERR_INVALID_ARGUMENT, "idx is null");
+    const Layout &L = w->L;
+    Scratch s;
+    HIP_TRY(s.alloc((size_t)L.ntile * sizeof(unsigned long long), (hipStream_t)stream), "scratch alloc");
+    GemvArgs a{};
+    a.qs = w->dev;
+    a.hdr = w->dev + L.qs_bytes;
+    a.x = x;
+    a.bias = bias;
+    a.y = logits;
+    a.n = L.n;
+    a.k = L.k;
+    a.m = 1;
+    a.ntile = L.ntile;
+    a.nblk = L.nblk;
+    a.argmax_partial = (unsigned long long *)s.p;
+    int e = launch_gemv(L.fmt, a, stream);
+    if (e) return hip_fail((hipError_t)e, "gemv launch");
+    e = launch_argmax_final(a.argmax_partial, L.ntile, idx, status_dev, stream);
+    if (e) return hip_fail((hipError_t)e, "argmax launch");
+    return NNQ_OK;
+}
+
+// ---- MoE ---------------------------------------------------------------------------
+
+int nnq_moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, const uint8_t *gu_scales,
+                   const float *gu_bias, const uint8_t *dn_packed, const uint8_t *dn_scales, const float *dn_bias,
+                   nnq_moe **out) {
+    if (!out) return fail(NNQ_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (E <= 0 || H <= 0 || I <= 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "bad MoE shape");
+    if (!gu_packed || !gu_scales || !gu_bias || !dn_packed || !dn_scales || !dn_bias)
+        return fail(NNQ_ERR_INVALID_ARGUMENT, "null weight pointer");
+    if ((2 * I) % 32 || H % 32 || H % 16 || I % 16)
+        return fail(NNQ_ERR_INVALID_SHAPE, "MoE dims must be multiples of 32 along the output dimension");
+    const size_t gu_el = (size_t)E * H * 2 * I, dn_el = (size_t)E * I * H;
+    nnq_moe *m = new nnq_moe;
+    hipGetDevice(&m->device);
+    auto dalloc = [&](size_t bytes, void **p) -> hipError_t {
+        hipError_t e = hipMalloc(p, bytes);
+        if (e == hipSuccess) m->allocs.push_back(*p);
+        return e;
+    };
+    std::vector<uint8_t> rq;
+    void *p[8] = {};
+    hipError_t e = hipSuccess;
+    // repacked codes for the grouped GEMMs
+    rq.resize(gu_el / 2);
+    moe_repack(gu_packed, E, H, 2 * I, rq.data());
+    if ((e = dalloc(gu_el / 2, &p[0])) == hipSuccess) e = hipMemcpy(p[0], rq.data(), gu_el / 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        rq.resize(dn_el / 2);
+        moe_repack(dn_packed, E, I, H, rq.data());
+        if ((e = dalloc(dn_el / 2, &p[1])) == hipSuccess)
+            e = hipMemcpy(p[1], rq.data(), dn_el / 2, hipMemcpyHostToDevice);
+    }
+    if (e == hipSuccess && (e = dalloc(gu_el / 32, &p[2])) == hipSuccess)
+        e = hipMemcpy(p[2], gu_scales, gu_el / 32, hipMemcpyHostToDevice);
+    if (e == hipSuccess && (e = dalloc(dn_el / 32, &p[3])) == hipSuccess)
+        e = hipMemcpy(p[3], dn_scales, dn_el / 32, hipMemcpyHostToDevice);
+    if (e == hipSuccess && (e = dalloc((size_t)E * 2 * I * 4, &p[4])) == hipSuccess)
+        e = hipMemcpy(p[4], gu_bias, (size_t)E * 2 * I * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess && (e = dalloc((size_t)E * H * 4, &p[5])) == hipSuccess)
+        e = hipMemcpy(p[5], dn_bias, (size_t)E * H * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess && (e = dalloc(gu_el / 2, &p[6])) == hipSuccess)
+        e = hipMemcpy(p[6], gu_packed, gu_el / 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess && (e = dalloc(dn_el / 2, &p[7])) == hipSuccess)
+        e = hipMemcpy(p[7], dn_packed, dn_el / 2, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        for (void *q : m->allocs) hipFree(q);
+        delete m;
+        return hip_fail(e, "MoE upload");
+    }
+    m->d.E = E;
+    m->d.H = H;
+    m->d.I = I;
+    m->d.gu_q = (const uint8_t *)p[0];
+    m->d.dn_q = (const uint8_t *)p[1];
+    m->d.gu_s = (const uint8_t *)p[2];
+    m->d.dn_s = (const uint8_t *)p[3];
+    m->d.gu_b = (const float *)p[4];
+    m->d.dn_b = (const float *)p[5];
+    m->d.gu_raw_q = (const uint8_t *)p[6];
+    m->d.dn_raw_q = (const uint8_t *)p[7];
+    *out = m;
+    return NNQ_OK;
+}
+
+int nnq_moe_destroy(nnq_moe *m) {
+    if (!m) return NNQ_OK;
+    for (void *q : m->allocs) hipFree(q);
+    delete m;
+    return NNQ_OK;
+}
+
+int nnq_moe_forward(const nnq_moe *m, const void *x, nnq_dtype x_dtype, int64_t tokens, const float *router_logits,
+                    int top_k, float swiglu_limit, float *y, uint32_t *topk_idx, float *topk_w, void *stream) {
+    if (!m) return fail(NNQ_ERR_INVALID_ARGUMENT, "MoE handle is null");
+    if (tokens < 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "tokens < 0");
+    if (top_k <= 0 || top_k > m->d.E || top_k > 8)
+        return fail(NNQ_ERR_INVALID_SHAPE, "topk k=%d out of range for %lld experts", top_k, (long long)m->d.E);
+    if (x_dtype != NNQ_F32 && x_dtype != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d", (int)x_dtype);
+    if (tokens == 0) return NNQ_OK;
+    if (!x || !router_logits || !y) return fail(NNQ_ERR_INVALID_ARGUMENT, "null pointer");
+    if (m->d.E > 256) return fail(NNQ_ERR_UNSUPPORTED, "at most 256 experts");
+    Scratch s;
+    HIP_TRY(s.alloc(moe_scratch_bytes(tokens, m->d.E, m->d.H, m->d.I, top_k), (hipStream_t)stream), "scratch alloc");
+    int e = launch_moe(m->d, x, x_dtype == NNQ_BF16, tokens, router_logits, top_k, swiglu_limit, y, topk_idx, topk_w,
+                       s.p, stream);
+    if (e) return hip_fail((hipError_t)e, "moe launch");
+    return NNQ_OK;
+}
+
+int nnq_moe_dequant_expert(const nnq_moe *m, int64_t expert, float *gate_up, float *down, void *stream) {
+    if (!m) return fail(NNQ_ERR_INVALID_ARGUMENT, "MoE handle is null");
+    if (expert < 0 || expert >= m->d.E) return fail(NNQ_ERR_INVALID_ARGUMENT, "expert %lld", (long long)expert);
+    int e = launch_moe_dequant(m->d, expert, gate_up, down, stream);
+    if (e) return hip_fail((hipError_t)e, "moe dequant launch");
+    return NNQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// Internal declarations shared by the C-ABI implementation, the host repack
+// code and the HIP kernels.  Not part of the public ABI.
+//
+// Device weight layout ("tile16"): rows are grouped in tiles of 16 (the N side
+// of a 16x16xK MFMA).  For every (tile, K-chunk) the quantized bytes of the 16
+// rows are stored so that one wave-wide 16-byte load puts exactly the MFMA
+// B-operand bytes of lane l = 16*p + n (row n of the tile, k-group p) into that
+// lane, and each 4-byte word is byte-permuted (e0,e2,e1,e3) so that masking
+// yields packed-f16 pairs in natural k order.  Scale/header bytes live in a
+// separate plane per (tile, block).  The repack is a bijection on the block
+// bytes: device bytes == host bytes except for zero padding of the last tile.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/nnq.h"
+
+namespace nnq {
+
+constexpr int kTile = 16;  // rows per tile
+
+// ---- per-format device layout geometry --------------------------------------------
+struct Layout {
+    int fmt = 0;        // nnq_format
+    int layout = 0;     // nnq_layout of the source bytes
+    int64_t n = 0, k = 0;
+    int64_t ntile = 0;  // ceil(n/16)
+    int64_t nblk = 0;   // format blocks per row after padding (Q8_0: padded to a multiple of 8)
+    size_t qs_bytes = 0;   // bytes of the quant plane
+    size_t hdr_bytes = 0;  // bytes of the scale/header plane
+    size_t total() const { return qs_bytes + hdr_bytes; }
+};
+
+// Q4_K: per (tile, block of 256): qs 2048 B (two 1 KB halves: groups {0,1}, {2,3}),
+//       header 16 rows x 16 B (d, dmin, scales[12] in GGUF-spec packing).
+// Q8_0: per (tile, block pair): qs 1024 B; per (tile, 8 blocks): 16 rows x 8 f16 scales.
+// Q6_K: per (tile, block of 256): qs 3072 B (four 64-k chunks x 64 lanes x 12 B),
+//       header 16 rows x 16 int8 scales + 16 rows x f16 d (288 B).
+bool make_layout(int fmt, int layout, int64_t n, int64_t k, Layout *out, const char **err);
+
+// Host repack: source block bytes (format/layout as given) -> device image (Layout::total bytes).
+void repack_q4k(const uint8_t *src, int legacy, const Layout &L, uint8_t *dst);
+void repack_q8_0(const uint8_t *src, const Layout &L, uint8_t *dst);
+void repack_q6k(const uint8_t *src, const Layout &L, uint8_t *dst);
+
+// nn-gguf legacy Q4_K block -> GGUF-spec (BlockQ4K) block with identical decoded values.
+void q4k_legacy_to_gguf(const uint8_t *legacy, uint8_t *gguf);
+
+// ---- kernel launch parameters ------------------------------------------------------
+struct GemvArgs {
+    const uint8_t *qs;    // quant plane
+    const uint8_t *hdr;   // header plane
+    const void *x;        // [m, k] f32 or bf16
+    int x_bf16;
+    const float *bias;    // [n] or null
+    void *y;              // [m, n] f32 or bf16
+    int y_bf16;
+    int64_t n, k, m;
+    int64_t ntile, nblk;
+    int kc;               // K elements staged in LDS per chunk (multiple of 256)
+    float *logits_out;    // optional copy (argmax fusion)
+    unsigned long long *argmax_partial;  // optional per-tile (orderable value, index) keys
+};
+
+int launch_gemv(int fmt, const GemvArgs &a, void *stream);      // returns hipError_t
+int launch_dequant(int fmt, const uint8_t *qs, const uint8_t *hdr, int64_t n, int64_t k, int64_t ntile,
+                   int64_t nblk, float *out, void *stream);
+int launch_argmax_reduce(const float *v, int64_t n, uint32_t *idx, int32_t *status, void *scratch,
+                         size_t scratch_bytes, void *stream);
+int launch_argmax_final(const unsigned long long *partial, int64_t count, uint32_t *idx, int32_t *status,
+                        void *stream);
+
+// GEMM (prefill) for Q4_K: x bf16/f32 [m, k] -> y [m, n]
+struct GemmArgs {
+    const uint8_t *qs;
+    const uint8_t *hdr;
+    const void *x;
+    int x_bf16;
+    const float *bias;
+    void *y;
+    int y_bf16;
+    int64_t n, k, m;
+    int64_t ntile, nblk;
+    uint16_t *xs;      // scratch: x converted to f16 * 2^s_row [m, k]
+    float *rowscale;   // scratch: per-row 2^-s factors [m]
+    float *xsum;       // scratch: per-row sums over 32-element sub-blocks [m, k/32]
+};
+int launch_gemm_q4k(const GemmArgs &a, void *stream);
+size_t gemm_scratch_bytes(int64_t m, int64_t k);
+
+// MoE (GPT-OSS MXFP4)
+struct MoeDev {
+    int64_t E, H, I;
+    const uint8_t *gu_q;    // repacked gate_up codes
+    const uint8_t *gu_s;    // gate_up scales
+    const float *gu_b;      // [E, 2I]
+    const uint8_t *dn_q;
+    const uint8_t *dn_s;
+    const float *dn_b;      // [E, H]
+    const uint8_t *gu_raw_q;  // original packed bytes (for bit-exact dequant)
+    const uint8_t *dn_raw_q;
+};
+size_t moe_scratch_bytes(int64_t T, int64_t E, int64_t H, int64_t I, int top_k);
+int launch_moe(const MoeDev &m, const void *x, int x_bf16, int64_t T, const float *logits, int top_k, float limit,
+               float *y, uint32_t *topk_idx, float *topk_w, void *scratch, void *stream);
+int launch_moe_dequant(const MoeDev &m, int64_t e, float *gate_up, float *down, void *stream);
+void moe_repack(const uint8_t *packed, int64_t E, int64_t K, int64_t N, uint8_t *dst);
+
+}  // namespace nnq

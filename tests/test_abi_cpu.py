@@ -1,0 +1,117 @@
+"""C-ABI checks that need no GPU: libnnq.so loads, exports every symbol that
+include/nnq.h declares, its host encoders agree byte-for-byte with the oracle's
+restatement of the reference quantizers, and argument validation reports the
+reference's error kinds before any device work."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from nn_amd import _lib
+    return _lib.load()
+
+
+def header_symbols():
+    txt = open(os.path.join(ROOT, "include", "nnq.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(nnq_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_exports_every_declared_symbol(lib):
+    from nn_amd import _lib
+    syms = header_symbols()
+    assert len(syms) >= 19
+    for s in syms:
+        assert hasattr(lib, s), s
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+
+
+def test_q4k_encoder_matches_oracle(O):
+    import nn_amd
+    rng = np.random.default_rng(0)
+    for scale in (0.02, 1.0, 1e-3):
+        v = (rng.standard_normal(256 * 37 + 100) * scale).astype(np.float32)
+        assert np.array_equal(nn_amd.quantize_q4_k(v), O.quantize_q4_k(v))
+    v = np.full(256, -1.0, np.float32)
+    v[0] = 0.0
+    assert np.array_equal(nn_amd.quantize_q4_k(v), O.quantize_q4_k(v))
+    for c in (0.5, -0.5, 0.0):
+        v = np.full(512, c, np.float32)
+        assert np.array_equal(nn_amd.quantize_q4_k(v), O.quantize_q4_k(v))
+
+
+def test_q4k_encoder_rejects_non_finite():
+    import nn_amd
+    v = np.full(256, 0.5, np.float32)
+    v[128] = np.nan
+    with pytest.raises(nn_amd.NonFiniteData):
+        nn_amd.quantize_q4_k(v)
+
+
+def test_other_encoders_match_oracle(O):
+    import nn_amd
+    rng = np.random.default_rng(1)
+    v = (rng.standard_normal(256 * 64) * 0.02).astype(np.float32)
+    assert np.array_equal(nn_amd.quantize_q8_0(v), O.quantize_q8_0(v))
+    assert np.array_equal(nn_amd.quantize_q6_k(v), O.quantize_q6_k(v))
+    v2 = np.concatenate([v, np.float32([np.nan, np.inf, -7.0, 1e-40, 6.0])])
+    a, b = nn_amd.quantize_mxfp4(v2), O.mxfp4_quantize(v2)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_synth_generator(O):
+    import nn_amd
+    a = nn_amd.synth_normal(42, 3, (1 << 16,), 0.02)
+    b = nn_amd.synth_normal(42, 3, (1 << 16,), 0.02)
+    c = nn_amd.synth_normal(42, 4, (1 << 16,), 0.02)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    assert abs(a.mean()) < 5e-4 and abs(a.std() - 0.02) < 5e-4
+    # the generator's words are splitmix64 of the keyed counter (test_prng.rs:18-22)
+    u = (O.splitmix64((42 + 3 * 0xD1B54A32D192ED03) % 2**64) >> 11) * 2.0 ** -53
+    u2 = (O.splitmix64((42 + 3 * 0xD1B54A32D192ED03 + 0x9E3779B97F4A7C15) % 2**64) >> 11) * 2.0 ** -53
+    v0 = np.float32(0.02 * np.sqrt(-2 * np.log(1 - u)) * np.cos(2 * np.pi * u2))
+    assert abs(a[0] - v0) <= 1e-9
+
+
+def test_weight_create_validation_without_device(lib):
+    from nn_amd import _lib
+    h = ctypes.c_void_p()
+    buf = np.zeros(144 * 4, np.uint8)
+    vp = buf.ctypes.data_as(ctypes.c_void_p)
+    # k not a multiple of the block size -> InvalidShape (QuantizedStorage::new)
+    assert lib.nnq_weight_create(12, 0, vp, buf.size, 4, 100, ctypes.byref(h)) == _lib.ERR_INVALID_SHAPE
+    # wrong byte count -> DataLengthMismatch
+    assert lib.nnq_weight_create(12, 0, vp, buf.size - 1, 4, 256, ctypes.byref(h)) == _lib.ERR_DATA_LENGTH
+    assert "expected 576" in _lib.last_error()
+    # not a linear block format
+    assert lib.nnq_weight_create(39, 0, vp, buf.size, 4, 256, ctypes.byref(h)) == _lib.ERR_WRONG_FORMAT
+    # a null weight handle is "not quantized"
+    assert lib.nnq_linear(None, None, 0, 1, 256, None, 0, None, 0, None) == _lib.ERR_NOT_QUANTIZED
+
+
+def test_python_mirror_validation_without_device():
+    import nn_amd
+    with pytest.raises(nn_amd.WeightRank):
+        nn_amd.QuantizedWeight.from_quantized(np.zeros(144, np.uint8), nn_amd.QuantType.Q4_K, (1, 1, 256))
+    with pytest.raises(nn_amd.InvalidShape):
+        nn_amd.QuantizedWeight.from_quantized(np.zeros(34, np.uint8), nn_amd.QuantType.Q8_0, (1, 30))
+    with pytest.raises(nn_amd.DataLengthMismatch):
+        nn_amd.QuantizedWeight.from_quantized(np.zeros(33, np.uint8), nn_amd.QuantType.Q8_0, (1, 32))
+    assert nn_amd.QuantType.Q4_K.expected_bytes(512) == 288 and nn_amd.QuantType.Q4_K.expected_bytes(100) is None
+
+
+def test_no_device_is_reported(lib):
+    import torch
+    from nn_amd import _lib
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    c = ctypes.c_int(-1)
+    assert lib.nnq_device_count(ctypes.byref(c)) == 0 and c.value == 0
+    assert lib.nnq_init(0) == _lib.ERR_NO_DEVICE

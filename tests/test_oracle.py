@@ -1,0 +1,482 @@
+"""Pin the CPU oracle (oracle/nnq_oracle.c) before trusting it as the checker.
+
+Each test restates a known-answer test of the reference (cited), an invariant its
+Kani harnesses prove, a closed form fixed by IEEE arithmetic, or an independent
+brute-force computation (numpy / f64) on small inputs.
+"""
+import numpy as np
+import pytest
+
+
+def f16b(v):
+    return int(np.float16(v).view(np.uint16))
+
+
+def block_bytes(*pairs, size):
+    b = np.zeros(size, np.uint8)
+    for off, val in pairs:
+        b[off] = val
+    return b
+
+
+# ---------------------------------------------------------------------------------
+# half precision (the `half` crate: IEEE 754 binary16, RNE)
+# ---------------------------------------------------------------------------------
+
+def test_f16_to_f32_exhaustive_matches_numpy(O):
+    bits = np.arange(65536, dtype=np.uint16)
+    a = O.f16_bits_to_f32(bits)
+    b = bits.view(np.float16).astype(np.float32)
+    fin = ~np.isnan(b)
+    assert np.array_equal(a[fin].view(np.uint32), b[fin].view(np.uint32))
+    assert np.isnan(a[~fin]).all()
+
+
+def test_f32_to_f16_rne_matches_numpy(O):
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(200_000) * 10.0 ** rng.integers(-9, 6, 200_000)).astype(np.float32)
+    edge = np.array([65504, 65519.99, 65520, 65536, 2.98e-8, 2.9802322e-08, 5.96e-8, 6.1e-5, -0.0, np.inf, -np.inf,
+                     1e-45, 3.0e-5], np.float32)
+    raw = rng.integers(0, 2**32, 200_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = np.concatenate([x, edge, raw[~np.isnan(raw)]])
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.f32_to_f16_bits(x), ref)
+
+
+def test_bf16_round_trip(O):
+    x = np.array([1.0, 1.00390625, 1.005859375, -3.5, 1e-40, 3.3e38], np.float32)
+    b = O.f32_to_bf16_bits(x)
+    # RNE: 1.00390625 = 1 + 2^-8 is a tie -> even (1.0); 1.005859375 rounds up
+    assert list(b[:3]) == [0x3F80, 0x3F80, 0x3F81]
+    assert np.array_equal(O.bf16_bits_to_f32(b)[[0, 3]], np.float32([1.0, -3.5]))
+
+
+def test_splitmix64_published_vector(O):
+    # SplitMix64 seeded with 0: the first output mixes 0x9E3779B97F4A7C15 (Vigna 2015)
+    assert O.splitmix64(0x9E3779B97F4A7C15) == 0xE220A8397B1DCDAF
+    assert O.splitmix64(2 * 0x9E3779B97F4A7C15 % 2**64) == 0x6E789E6AA1B965F4
+
+
+# ---------------------------------------------------------------------------------
+# Q8_0
+# ---------------------------------------------------------------------------------
+
+def test_q8_0_zero_scale(O):
+    # crates/nn-gguf/src/dequant.rs:699-715
+    blk = np.zeros(34, np.uint8)
+    blk[2:] = 42
+    assert np.all(O.dequant_q8_0(blk, 32) == 0.0)
+
+
+def test_q8_0_cross_crate_block(O):
+    # crates/nn-import/src/gguf_expanded_tests.rs:894-925: scale 0.25, values -10..21
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    blk[2:] = (np.arange(32) - 10).astype(np.int8).view(np.uint8)
+    assert np.array_equal(O.dequant_q8_0(blk, 32), 0.25 * (np.arange(32) - 10).astype(np.float32))
+
+
+def test_q8_0_decode_closed_form(O):
+    rng = np.random.default_rng(1)
+    raw = rng.integers(0, 256, 34 * 64, dtype=np.uint8)
+    d = raw.reshape(64, 34)[:, :2].copy().view(np.uint16).ravel()
+    d = d & 0x7BFF  # finite scales
+    raw.reshape(64, 34)[:, :2] = d.view(np.uint8).reshape(64, 2)
+    got = O.dequant_q8_0(raw, 64 * 32)
+    q = raw.reshape(64, 34)[:, 2:].view(np.int8).astype(np.float64)
+    exact = d.view(np.float16).astype(np.float64)[:, None] * q  # exact in binary32 (<= 19 bits)
+    assert np.array_equal(got, exact.astype(np.float32).ravel())
+
+
+def test_q8_0_short_buffer_clamps(O):
+    # crates/nn-gguf/src/security_tests.rs:693-700
+    assert O.dequant_q8_0(np.zeros(20, np.uint8), 32).size == 0
+
+
+def make_q8_0_weight(n, k, scale, values):
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(scale).tobytes(), np.uint8)
+    blk[2:] = np.asarray(values, np.int8).view(np.uint8)
+    return np.tile(blk, n * (k // 32))
+
+
+def test_q8_0_matmul_known_values(O):
+    # crates/nn-core/src/dyn_tensor/quantized_matmul_tests.rs:150-163 and :166-200
+    w = make_q8_0_weight(2, 32, 0.5, [2] * 32)
+    assert np.all(np.abs(O.q8_0_matmul(np.ones((1, 32), np.float32), w, 2) - 32.0) < 0.5)
+    w = make_q8_0_weight(1, 32, 1.0, [1] * 32)
+    x = np.stack([np.ones(32, np.float32), 2 * np.ones(32, np.float32)])
+    y = O.q8_0_matmul(x, w, 1)
+    assert abs(y[0, 0] - 32.0) < 0.5 and abs(y[1, 0] - 64.0) < 1.0
+
+
+def test_q8_0_matmul_batch_4d_and_multiblock(O):
+    # quantized_matmul_tests.rs:296-318 (4-D batch) and :528-545 (two blocks)
+    w = make_q8_0_weight(3, 32, 1.0, [1] * 32)
+    y = O.q8_0_matmul(np.full((2, 2, 1, 32), 2.0, np.float32), w, 3)
+    assert y.shape == (2, 2, 1, 3) and np.all(np.abs(y - 64.0) < 1.0)
+    w = make_q8_0_weight(2, 64, 1.0, [1] * 32)
+    assert np.all(np.abs(O.q8_0_matmul(np.ones((1, 64), np.float32), w, 2) - 64.0) < 1.0)
+
+
+def test_q8_0_matmul_bias_values(O):
+    # quantized_matmul_tests.rs:323-350 and :383-418 (bias added after the fused matmul)
+    w = make_q8_0_weight(2, 32, 1.0, [1] * 32)
+    y = O.q8_0_matmul(np.ones((1, 32), np.float32), w, 2) + np.float32([10, 20])
+    assert np.allclose(y, [[42, 52]], atol=1.0)
+    w = make_q8_0_weight(3, 32, 1.0, [1] * 32)
+    y = O.q8_0_matmul(np.full((2, 1, 32), 0.5, np.float32), w, 3) + np.float32([100, 200, 300])
+    assert np.allclose(y[0, 0], [116, 216, 316], atol=1.0)
+
+
+def test_q8_0_fused_matches_dequant_then_matmul(O):
+    # quantized_matmul_tests.rs:457-491: fused vs dequant+matmul within 1e-3
+    w = make_q8_0_weight(4, 64, 0.25, [4] * 32)
+    x = ((np.arange(128) % 64) * 0.1 - 3.0).astype(np.float32).reshape(2, 64)
+    fused = O.q8_0_matmul(x, w, 4)
+    ref = O.matmul_xwt(x, O.dequant_q8_0(w, 4 * 64).reshape(4, 64))
+    assert np.max(np.abs(fused - ref)) < 1e-3
+
+
+def test_q8_0_fused_against_f64_bruteforce(O):
+    rng = np.random.default_rng(3)
+    n, k = 37, 320
+    w = O.quantize_q8_0(rng.standard_normal(n * k).astype(np.float32) * 0.02)
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    wf = O.dequant_q8_0(w, n * k).reshape(n, k).astype(np.float64)
+    exact = x.astype(np.float64) @ wf.T
+    got = O.q8_0_matmul(x, w, n)
+    assert np.max(np.abs(got - exact)) <= 1e-5 * np.max(np.abs(exact))
+
+
+# ---------------------------------------------------------------------------------
+# Q4_K, GGUF-spec layout (nn-core BlockQ4K)
+# ---------------------------------------------------------------------------------
+
+def pack_scale_min(sc, mn):
+    """The packing written by BlockQ4K::quantize (linear.rs:121-133)."""
+    s = np.zeros(12, np.uint8)
+    for j in range(8):
+        ls, lm = sc[j], mn[j]
+        if j < 4:
+            s[j] = ls
+            s[j + 4] = lm
+        else:
+            s[j + 4] = (ls & 0xF) | ((lm & 0xF) << 4)
+            s[j - 4] |= (ls >> 4) << 6
+            s[j] |= (lm >> 4) << 6
+    return s
+
+
+def test_q4k_scale_min_pack_roundtrip_exhaustive(O):
+    # Kani harnesses q4k_scale_pack_roundtrip_low/high (linear.rs:633-668): every j and 6-bit pair
+    for j in range(8):
+        for sc in range(64):
+            for mn in range(0, 64, 3 if j % 2 else 1):
+                q = np.zeros(12, np.uint8)
+                if j < 4:
+                    q[j], q[j + 4] = sc, mn
+                else:
+                    q[j + 4] = (sc & 0xF) | ((mn & 0xF) << 4)
+                    q[j - 4] |= (sc >> 4) << 6
+                    q[j] |= (mn >> 4) << 6
+                assert O.q4k_get_scale_min(j, q) == (sc, mn)
+
+
+def q4k_block(d, dmin, sc, mn, q):
+    """BlockQ4K bytes from scales/mins and 256 4-bit values (GGUF element order)."""
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    b[2:4] = np.frombuffer(np.float16(dmin).tobytes(), np.uint8)
+    b[4:16] = pack_scale_min(sc, mn)
+    q = np.asarray(q, np.uint8)
+    for g in range(4):
+        b[16 + 32 * g:16 + 32 * g + 32] = q[64 * g:64 * g + 32] | (q[64 * g + 32:64 * g + 64] << 4)
+    return b
+
+
+def test_q4k_gguf_decode_known_block(O):
+    # element e of sub-block j = e // 32 decodes to d*sc_j*q_e - dmin*m_j (linear.rs:63-92)
+    sc = [1, 2, 3, 4, 63, 33, 17, 0]
+    mn = [0, 5, 9, 62, 1, 63, 20, 7]
+    q = np.arange(256) % 16
+    blk = q4k_block(0.5, 0.25, sc, mn, q)
+    got = O.dequant_q4_k(blk, 256)
+    exp = np.array([0.5 * sc[e // 32] * q[e] - 0.25 * mn[e // 32] for e in range(256)], np.float64)
+    assert np.array_equal(got, exp.astype(np.float32))
+
+
+def test_q4k_gguf_decode_closed_form_random(O):
+    # F13: d*sc and dmin*m are exact, so each output is round_f32(d*sc*q - dmin*m) of the exact value
+    rng = np.random.default_rng(11)
+    nb = 200
+    raw = rng.integers(0, 256, 144 * nb, dtype=np.uint8).reshape(nb, 144)
+    dd = raw[:, :4].copy().view(np.uint16) & 0x7BFF
+    raw[:, :4] = dd.view(np.uint8)
+    got = O.dequant_q4_k(raw.ravel(), 256 * nb).reshape(nb, 256)
+    for b in range(nb):
+        d, dmin = dd[b].view(np.float16).astype(np.float64)
+        for e in range(0, 256, 7):
+            j = e // 32
+            sc, mn = O.q4k_get_scale_min(j, raw[b, 4:16])
+            g, i = e // 64, e % 64
+            byte = raw[b, 16 + 32 * g + (i % 32)]
+            qv = (byte & 0xF) if i < 32 else (byte >> 4)
+            assert got[b, e] == np.float32(d * sc * qv - dmin * mn)
+
+
+def test_q4k_quantize_round_trip_bounds(O):
+    # crates/nn-core/src/layers/quantized/linear_tests.rs:33-99
+    cases = [(np.zeros(256, np.float32), 0.01), (np.arange(256, dtype=np.float32) / 255.0, 0.1),
+             (np.arange(256, dtype=np.float32) / 127.5 - 1.0, 0.2), (np.full(256, 0.5, np.float32), 0.1)]
+    for v, tol in cases:
+        r = O.dequant_q4_k(O.quantize_q4_k(v), 256)
+        assert np.max(np.abs(r - v)) < tol
+
+
+def test_q4k_quantize_clustered_at_min_and_nan(O):
+    # linear_tests.rs:300-332
+    v = np.full(256, -1.0, np.float32)
+    v[0] = 0.0
+    assert np.isfinite(O.dequant_q4_k(O.quantize_q4_k(v), 256)).all()
+    v = np.full(256, 0.5, np.float32)
+    v[128] = np.nan
+    with pytest.raises(O.OracleError):
+        O.quantize_q4_k(v)
+
+
+def test_q4k_nearest_int_cases(O):
+    # linear_tests.rs:258-298 (f32::round: half away from zero)
+    assert [O.q4k_nearest_int(v) for v in (0.0, 1.5, -1.5, 0.4, -0.4, 2.5)] == [0, 2, -2, 0, 0, 3]
+    for bad in (np.nan, np.inf, -np.inf):
+        with pytest.raises(O.OracleError):
+            O.q4k_nearest_int(bad)
+
+
+def test_q4k_qlinear_round_trip_weight_tolerance(O):
+    # linear_tests.rs:118-142: from_linear -> dequantize within 0.1 for small weights
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((8, 512)) * 0.1).astype(np.float32)
+    r = O.dequant_q4_k(O.quantize_q4_k(w), w.size).reshape(w.shape)
+    assert np.max(np.abs(r - w)) < 0.1
+
+
+def test_q4k_padding_non_aligned(O):
+    # QLinear::from_linear pads the flattened weight to a multiple of 256 (linear.rs:323-328)
+    v = np.arange(300, dtype=np.float32) / 300.0
+    b = O.quantize_q4_k(v)
+    assert b.size == 2 * 144
+    assert np.max(np.abs(O.dequant_q4_k(b, 512)[:300] - v)) < 0.1
+
+
+# ---------------------------------------------------------------------------------
+# Q4_K, nn-gguf layout
+# ---------------------------------------------------------------------------------
+
+def test_q4k_legacy_known_values_and_divergence(O):
+    # crates/nn-gguf/src/dequant.rs:764-818: d=1, scales[0]=2, q=3 -> 6.0 for sub-block 0
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[4] = 0x02
+    blk[16:32] = 0x33
+    leg = O.dequant_q4_k_legacy(blk, 256)
+    assert np.all(np.abs(leg[:32] - 6.0) < 1e-4) and np.all(np.abs(leg[32:]) < 1e-6)
+    # the same bytes under the GGUF layout: elements 16..31 are 0
+    gg = O.dequant_q4_k(blk, 256)
+    assert np.all(gg[:16] == 6.0) and np.all(gg[16:32] == 0.0)
+
+
+def test_q4k_legacy_with_dmin_and_zero(O):
+    # dequant.rs:820-852 and :748-762
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    blk[4] = 0x01
+    blk[8] = 0x04
+    assert np.all(np.abs(O.dequant_q4_k_legacy(blk, 256)[:32] + 2.0) < 1e-3)
+    z = np.zeros(144, np.uint8)
+    z[4:16] = 0xFF
+    z[16:] = 0xAB
+    assert np.all(O.dequant_q4_k_legacy(z, 256) == 0.0)
+    assert O.dequant_q4_k_legacy(np.zeros(100, np.uint8), 256).size == 0  # security_tests.rs:702-709
+
+
+# ---------------------------------------------------------------------------------
+# Q6_K, nn-gguf layout (crates/nn-gguf/src/dequant.rs:1158-1399)
+# ---------------------------------------------------------------------------------
+
+def q6(d, scales=(), ql=(), qh=()):
+    b = np.zeros(210, np.uint8)
+    b[208:210] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    for i, v in scales:
+        b[192 + i] = np.uint8(np.int8(v).view(np.uint8))
+    for i, v in ql:
+        b[i] = v
+    for i, v in qh:
+        b[128 + i] = v
+    return b
+
+
+def test_q6k_zero_d_and_zero_scales(O):
+    b = q6(0.0)
+    b[:192] = 0xAB
+    b[192:208] = 0x7F
+    assert np.all(O.dequant_q6_k(b, 256) == 0.0)
+    b = q6(1.0)
+    b[:192] = 0xFF
+    assert np.all(O.dequant_q6_k(b, 256) == 0.0)
+
+
+def test_q6k_known_values(O):
+    # centered q=32 -> 0; d=0.5 sc=2 q=35 -> 3.0; sc=-3 q=33 -> -3.0; q=63 -> 62.0; q=0 -> -64.0
+    b = q6(1.0, scales=[(i, 1) for i in range(16)], qh=[(i, 0xAA) for i in range(64)])
+    assert np.all(np.abs(O.dequant_q6_k(b, 256)) < 1e-4)
+    b = q6(0.5, scales=[(0, 2)], ql=[(i, 0x33) for i in range(8)], qh=[(i, 0xAA) for i in range(4)])
+    r = O.dequant_q6_k(b, 256)
+    assert np.all(np.abs(r[:16] - 3.0) < 1e-3) and np.all(np.abs(r[16:]) < 1e-4)
+    b = q6(1.0, scales=[(0, -3)], ql=[(i, 0x11) for i in range(8)], qh=[(i, 0xAA) for i in range(4)])
+    assert np.all(np.abs(O.dequant_q6_k(b, 256)[:16] + 3.0) < 1e-3)
+    b = q6(0.5, scales=[(0, 4)], ql=[(i, 0xFF) for i in range(8)], qh=[(i, 0xFF) for i in range(4)])
+    r = O.dequant_q6_k(b, 256)
+    assert np.all(np.abs(r[:16] - 62.0) < 1e-2) and np.all(np.abs(r[16:]) < 1e-4)
+    b = q6(1.0, scales=[(0, 2)])
+    assert np.all(np.abs(O.dequant_q6_k(b, 256)[:16] + 64.0) < 1e-2)
+
+
+def test_q6k_two_blocks_length_finite_short(O):
+    data = np.zeros(420, np.uint8)
+    data[208:210] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    data[418:420] = np.frombuffer(np.float16(2.0).tobytes(), np.uint8)
+    assert np.all(O.dequant_q6_k(data, 512) == 0.0)
+    assert O.dequant_q6_k(np.zeros(840, np.uint8), 1024).size == 1024  # gguf_expanded_tests.rs:465-470
+    pat = ((np.arange(210) * 17) % 256).astype(np.uint8)  # gguf_expanded_tests.rs:472-480
+    assert np.isfinite(O.dequant_q6_k(pat, 256)).all()
+    assert O.dequant_q6_k(np.zeros(100, np.uint8), 256).size == 0  # security_tests.rs:711-717
+
+
+def test_q6k_element_mapping_closed_form(O):
+    rng = np.random.default_rng(9)
+    raw = rng.integers(0, 256, 210 * 20, dtype=np.uint8).reshape(20, 210)
+    dd = raw[:, 208:210].copy().view(np.uint16) & 0x7BFF
+    raw[:, 208:210] = dd.view(np.uint8)
+    got = O.dequant_q6_k(raw.ravel(), 20 * 256).reshape(20, 256)
+    idx = np.arange(256)
+    lo = (raw[:, idx // 2] >> (4 * (idx % 2))) & 0xF
+    hi = (raw[:, 128 + idx // 4] >> (2 * (idx % 4))) & 3
+    q = (lo | (hi << 4)).astype(np.float64) - 32
+    sc = raw[:, 192:208].view(np.int8).astype(np.float64)[:, idx // 16]
+    exact = dd.view(np.float16).astype(np.float64) * sc * q  # exact (<= 23 significant bits)
+    assert np.array_equal(got, exact.astype(np.float32))
+
+
+# ---------------------------------------------------------------------------------
+# GPT-OSS MXFP4 (crates/nn-gptoss/src/quantize.rs:270-404, tests/integration.rs:125-160)
+# ---------------------------------------------------------------------------------
+
+def test_mxfp4_lut_and_e8m0(O):
+    assert [O.lib().orc_mxfp4_lut(i) for i in range(16)] == [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                                                             -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+    dec = O.lib().orc_mxfp4_decode_e8m0
+    assert (dec(127), dec(128), dec(126)) == (1.0, 2.0, 0.5)
+    assert dec(0) == 2.0 ** -126 and dec(1) == 2.0 ** -126
+    enc = O.lib().orc_mxfp4_e8m0_from_max
+    assert (enc(0.0), enc(float("nan")), enc(6.0), enc(1e-40)) == (0, 0, 127, 0)
+
+
+def test_mxfp4_round_trips(O):
+    v = np.float32([0.0, 1.0, -1.0, 2.0, -2.0, 3.0, -3.0, 4.0])
+    p, s = O.mxfp4_quantize(v)
+    assert np.all(np.abs(O.mxfp4_dequantize(p, s, 8) - v) < 1e-6)
+    v = ((np.arange(64) - 32.0) * 0.1).astype(np.float32)
+    p, s = O.mxfp4_quantize(v)
+    r = O.mxfp4_dequantize(p, s, 64)
+    for i in range(64):
+        assert abs(v[i] - r[i]) <= O.lib().orc_mxfp4_decode_e8m0(int(s[i // 32])) + 1e-6
+    p, s = O.mxfp4_quantize(np.zeros(64, np.float32))
+    assert np.all(O.mxfp4_dequantize(p, s, 64) == 0.0)
+    v = np.float32([0.5, -0.25, 1.0, 0.0, -1.0, 0.75, -0.5, 0.125])
+    p, s = O.mxfp4_quantize(v)
+    assert np.all(np.abs(O.mxfp4_dequantize(p, s, 8) - v) < 2.0)
+
+
+def test_mxfp4_sizes_large_subnormal(O):
+    p, s = O.mxfp4_quantize(np.arange(50, dtype=np.float32))
+    assert s.size == 2 and O.mxfp4_dequantize(p, s, 50).size == 50
+    p, s = O.mxfp4_quantize(np.ones(128, np.float32))
+    assert s.size == 4 and p.size == 64
+    p, s = O.mxfp4_quantize(np.float32([1000.0, -500.0, 250.0, -125.0]))
+    assert np.isfinite(O.mxfp4_dequantize(p, s, 4)).all()
+    p, s = O.mxfp4_quantize(np.full(32, np.finfo(np.float32).tiny / 100, np.float32))
+    assert np.all(np.abs(O.mxfp4_dequantize(p, s, 32)) < 1e-30)
+
+
+def test_mxfp4_nibble_order_and_ties(O):
+    # pair p: HIGH nibble = element 2p (quantize.rs:147-155); ties keep the lower magnitude (strict <)
+    v = np.zeros(32, np.float32)
+    v[0], v[1] = 6.0, -0.5
+    p, s = O.mxfp4_quantize(v)
+    assert s[0] == 127 and p[0] == (0x7 << 4 | 0x9)
+    enc = O.lib().orc_mxfp4_quantize_fp4
+    assert enc(1.25, 1.0) == 2 and enc(2.5, 1.0) == 4 and enc(5.0, 1.0) == 6 and enc(0.25, 1.0) == 0
+    assert enc(float("inf"), 1.0) == 0 and enc(-1.75, 1.0) == 0xB
+
+
+# ---------------------------------------------------------------------------------
+# argmax / softmax / topk / MoE
+# ---------------------------------------------------------------------------------
+
+def test_argmax_semantics(O):
+    assert O.argmax(np.float32([1, 3, 3, 2])) == 1  # first maximum (strict >)
+    assert O.argmax(np.float32([-np.inf, -np.inf])) == 0
+    with pytest.raises(O.OracleError):
+        O.argmax(np.float32([1, np.nan, 2]))
+
+
+def test_softmax_topk_small(O):
+    x = np.float32([[1.0, 2.0, 3.0, 0.5], [0.0, 0.0, -np.inf, 1.0]])
+    p = O.softmax_rows(x)
+    e = np.exp(x.astype(np.float64) - x.max(1, keepdims=True))
+    assert np.allclose(p, e / e.sum(1, keepdims=True), rtol=1e-6, atol=0)
+    v, i = O.topk_rows(p, 2)
+    assert i.tolist() == [[2, 1], [3, 0]]
+    assert O.softmax_rows(np.full((1, 3), -np.inf, np.float32)).tolist() == [[0.0, 0.0, 0.0]]
+
+
+def moe_f64(x, logits, k, Wg, bg, Wd, bd, inter, limit):
+    """Independent f64 restatement of moe_forward (quantized_model.rs:132-194)."""
+    T, H = x.shape
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    out = np.zeros((T, H))
+    for t in range(T):
+        order = sorted(range(logits.shape[1]), key=lambda e: (-p[t, e], e))[:k]
+        w = p[t, order] / p[t, order].sum()
+        for e, we in sorted(zip(order, w)):
+            gu = x[t] @ Wg[e] + bg[e]
+            g, u = gu[:inter], gu[inter:]
+            sg = np.clip(g / (1 + np.exp(-g)), -limit, limit)
+            out[t] += we * ((sg * u) @ Wd[e] + bd[e])
+    return out
+
+
+def test_moe_matches_f64_bruteforce(O):
+    rng = np.random.default_rng(21)
+    E, K, T, H, I = 4, 2, 6, 64, 32
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    gu = (rng.standard_normal(E * H * 2 * I) * 0.1).astype(np.float32)
+    dn = (rng.standard_normal(E * I * H) * 0.1).astype(np.float32)
+    gb = (rng.standard_normal(E * 2 * I) * 0.1).astype(np.float32)
+    db = (rng.standard_normal(E * H) * 0.1).astype(np.float32)
+    gp, gs = O.mxfp4_quantize(gu)
+    dp, ds = O.mxfp4_quantize(dn)
+    y, ti, tw = O.moe_forward(x, logits, K, gp, gs, gb, dp, ds, db, I, 7.0)
+    y2, _, _ = O.moe_forward(x, logits, K, gp, gs, gb, dp, ds, db, I, 7.0, faithful=True)
+    assert np.array_equal(y, y2)
+    Wg = O.mxfp4_dequantize(gp, gs, E * H * 2 * I).reshape(E, H, 2 * I).astype(np.float64)
+    Wd = O.mxfp4_dequantize(dp, ds, E * I * H).reshape(E, I, H).astype(np.float64)
+    ref = moe_f64(x.astype(np.float64), logits.astype(np.float64), K, Wg, gb.reshape(E, 2 * I), Wd,
+                  db.reshape(E, H), I, 7.0)
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+    assert np.allclose(tw.sum(1), 1.0, atol=1e-6)
