@@ -47,17 +47,26 @@ __device__ __forceinline__ void split_f16(float x, uint32_t &hi, uint32_t &lo) {
     lo = __builtin_bit_cast(uint16_t, (_Float16)r);
 }
 
-// Power-of-two prescale that maps max|x| into [2^14, 2^15): returns 2^s as float
-// (1.0 for an all-zero row); non-finite max -> NaN (propagates NaN to outputs).
-__device__ __forceinline__ float f16_prescale(float amax) {
-    if (!(amax <= 3.0e38f)) return __uint_as_float(0x7FC00000u);
-    if (amax == 0.0f) return 1.0f;
-    int e = (int)((__float_as_uint(amax) >> 23) & 0xFF);  // biased exponent (0 for subnormal)
-    if (e == 0) e = 1;
-    int s = 14 - (e - 127);  // scale exponent
-    if (s > 127) s = 127;
-    if (s < -126) s = -126;
-    return __uint_as_float((uint32_t)(s + 127) << 23);
+// Power-of-two prescale: s = 2^e with amax * s in [2^14, 2^15) (s = 1 for amax = 0)
+// and back = 1 / s exactly, both normal f32; a non-finite amax gives NaN for both, so
+// NaN / inf activations propagate to the outputs.
+__device__ __forceinline__ void f16_prescale(float amax, float &s, float &back) {
+    const int eb = (int)((__float_as_uint(amax) >> 23) & 0xFF);  // biased exponent (0 for subnormal)
+    int se = 141 - (eb > 1 ? eb : 1);                             // 14 - (eb - 127)
+    se = se > 126 ? 126 : (se < -126 ? -126 : se);
+    s = __uint_as_float((uint32_t)(127 + se) << 23);
+    back = __uint_as_float((uint32_t)(127 - se) << 23);
+    if (amax == 0.0f) s = back = 1.0f;
+    if (!(amax <= 3.0e38f)) s = back = __uint_as_float(0x7FC00000u);
+}
+
+// DPP quad permutations: the value of lane (l ^ 1) / (l ^ 2) within each group of 4.
+// All lanes of the wave must be active.
+__device__ __forceinline__ float dpp_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -69,11 +78,19 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Non-temporal-free 16-byte global loads (kept as plain vector loads).
-__device__ __forceinline__ u32x4 ldg128(const uint8_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
+// Weight loads: every weight byte is read once per call, so they are issued as
+// non-temporal (streaming) loads that do not displace the activations in the caches.
+__device__ __forceinline__ u32x4 ldg128(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
 __device__ __forceinline__ u32x3 ldg96(const uint8_t *p) {
     const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
-    return u32x3{q[0], q[1], q[2]};
+    return u32x3{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1), __builtin_nontemporal_load(q + 2)};
+}
+
+// DPP row_half_mirror: the value of lane 7 - (l % 8) within each group of 8.
+__device__ __forceinline__ float dpp_half_mirror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
 }
 
 }  // namespace nnq

@@ -1,16 +1,17 @@
 // Decode GEMV (m <= 8 tokens) for Q4_K / Q8_0 / Q6_K weights on gfx950.
 //
 // One workgroup owns a tile of 16 weight rows and all of K.  Its waves split K
-// into 256-element units (unit u goes to wave u % WAVES).  Per unit a wave
-// issues coalesced 16-byte loads whose bytes are, lane by lane, the B operand
-// of a 16x16x32 f16 MFMA (the tile16 repack puts them there), turns nibbles /
-// bytes into packed f16 values with one mask per pair (the integer q is read as
-// an f16 subnormal q * 2^-24, exact), and multiplies against the activation.
+// into 256-element units (unit u goes to wave u % WAVES) and issue the loads of
+// all their units up front, so a whole K chunk of the tile is in flight at once.
+// Per unit a wave's coalesced 16-byte loads are, lane by lane, the B operand of a
+// 16x16x32 f16 MFMA (the tile16 repack puts them there); nibbles / bytes become
+// packed f16 values with one mask per pair (the integer q is read as an f16
+// subnormal q * 2^-24, exact) and are multiplied against the activation.
 // The activation is staged once per workgroup in LDS as f16 hi + lo parts of
-// x * 2^s (s per token, chosen so max|x| lands in [2^14, 2^15)), so the f16 MFMA
-// sees x to ~22 significant bits and every product is exact in the f32
-// accumulator.  Per-sub-block scales and mins are applied to the MFMA results
-// in f32; waves are combined through LDS at the end.
+// x * 2^s (s per token and 256-element unit, chosen so the unit's max|x| lands in
+// [2^14, 2^15)), so the f16 MFMA sees x to ~22 significant bits and every product
+// is exact in the f32 accumulator.  Per-sub-block scales and mins are applied to
+// the MFMA results in f32; waves are combined through LDS at the end.
 //
 // A-operand rows: Q4_K / Q8_0 use rows (2t, 2t+1) = (hi, lo) of token t (8 tokens);
 // Q6_K uses rows 4t..4t+3 = (hi, lo) x (first / second 16-value sub-block).
@@ -36,10 +37,8 @@ struct Fmt<FQ6K> {
     static constexpr int kMaxTok = 4, kSumGran = 16;
 };
 
-struct LdsPlan {
-    int kc;          // staged K per chunk
-    size_t bytes;
-};
+// Largest number of 8-element activation groups one thread stages per chunk.
+constexpr int kXGroups = 3;
 
 static inline size_t lds_bytes_for(int mt, int kc, int gran, int waves) {
     size_t stage = (size_t)mt * kc * 4 + (size_t)mt * (kc / gran) * 4;
@@ -48,96 +47,104 @@ static inline size_t lds_bytes_for(int mt, int kc, int gran, int waves) {
 }
 
 // ---------------------------------------------------------------------------------
-// Activation staging: x[t][k0 .. k0+kc) -> LDS hi/lo f16 planes + sub-block sums.
+// Activation staging: x[t][k0 .. k0+kc) -> LDS hi/lo f16 planes of x * 2^s(t,b),
+// sums of the unscaled x over GRAN consecutive k, and the factor 2^-s(t,b) of every
+// 32-element block b (four consecutive lanes hold one block of one token, so its
+// max is two DPP steps away and no whole-row pass over x is needed).  Staging is
+// split in two: the raw loads (issued before the weight loads of the chunk, so that
+// waiting for them does not wait for the weights) and the conversion.
 // ---------------------------------------------------------------------------------
-// `kcur` elements are staged (k >= a.k reads as zero: Q8_0 pads to 256), `kc` is the
-// plane stride.
-template <int GRAN>
-__device__ __forceinline__ void stage_x(const GemvArgs &a, int mt, int64_t k0, int kcur, int kc, const float *scl,
-                                        uint16_t *xs, float *xsum) {
+struct XRaw {
+    u32x4 r[kXGroups][2];
+    int t[kXGroups], g8[kXGroups];
+    bool valid[kXGroups];  // the group exists in this chunk
+    bool in[kXGroups];     // ... and lies inside x (Q8_0 pads K to whole 256-element units)
+};
+
+// Every thread issues the same two 16-byte loads per group whatever the group's
+// validity (out-of-range groups read x[0]; bf16 reads its one vector twice), so the
+// load sequence is branch-free and the wait for these loads does not extend to the
+// weight loads issued after them.
+__device__ __forceinline__ void stage_x_load(const GemvArgs &a, int mt, int64_t k0, int kcur, float inv_per_tok,
+                                             XRaw &raw) {
     const int tid = threadIdx.x, nth = blockDim.x;
     const int per_tok = kcur / 8;
-    for (int idx = tid; idx < mt * per_tok; idx += nth) {
-        int t = idx / per_tok, g8 = idx - t * per_tok;
-        int64_t kk = k0 + 8 * g8;
-        float v[8];
-        if (kk >= a.k) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = 0.0f;
-        } else if (a.x_bf16) {
-            const uint16_t *xp = (const uint16_t *)a.x + (int64_t)t * a.k + kk;
-            u32x4 w = *reinterpret_cast<const u32x4 *>(xp);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[2 * i] = bf16_to_f32(w[i] & 0xFFFFu);
-                v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
-            }
-        } else {
-            const float *xp = (const float *)a.x + (int64_t)t * a.k + kk;
-            floatx4 w0 = *reinterpret_cast<const floatx4 *>(xp);
-            floatx4 w1 = *reinterpret_cast<const floatx4 *>(xp + 4);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[i] = w0[i];
-                v[4 + i] = w1[i];
-            }
-        }
-        float s = scl[t];
-        uint32_t hi[8], lo[8];
-        float sum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            split_f16(v[i] * s, hi[i], lo[i]);
-            sum += v[i];
-        }
-        u32x4 H = {hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
-        u32x4 L = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
-        *reinterpret_cast<u32x4 *>(xs + ((size_t)t * 2 + 0) * kc + 8 * g8) = H;
-        *reinterpret_cast<u32x4 *>(xs + ((size_t)t * 2 + 1) * kc + 8 * g8) = L;
-        // sums over GRAN consecutive k: combine GRAN/8 neighbouring lanes
-        float tot = sum;
-#pragma unroll
-        for (int o = 1; o < GRAN / 8; o <<= 1) tot += __shfl_xor(tot, o, 64);
-        if ((g8 & (GRAN / 8 - 1)) == 0) xsum[(size_t)t * (kc / GRAN) + g8 / (GRAN / 8)] = tot;
+    for (int j = 0; j < kXGroups; j++) {
+        const int idx = tid + j * nth;
+        const bool valid = idx < mt * per_tok;
+        // idx / per_tok without an integer division (exact: idx < 2^15, per_tok >= 32)
+        const int t = valid ? (int)(((float)idx + 0.5f) * inv_per_tok) : 0;
+        const int g8 = valid ? idx - t * per_tok : 0;
+        const int64_t kk = k0 + 8 * g8;
+        raw.valid[j] = valid;
+        raw.t[j] = t;
+        raw.g8[j] = g8;
+        raw.in[j] = valid && kk < a.k;
+        const int64_t off = raw.in[j] ? (int64_t)t * a.k + kk : 0;
+        const uint8_t *p0 = reinterpret_cast<const uint8_t *>(a.x) + off * (a.x_bf16 ? 2 : 4);
+        const uint8_t *p1 = a.x_bf16 ? p0 : p0 + 16;
+        raw.r[j][0] = *reinterpret_cast<const u32x4 *>(p0);
+        raw.r[j][1] = *reinterpret_cast<const u32x4 *>(p1);
     }
 }
 
-// per-token prescale factors 2^s (max over the whole row of x)
-__device__ __forceinline__ void token_scales(const GemvArgs &a, int mt, float *scl, float *wred) {
-    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6, nw = nth >> 6;
-    for (int t = 0; t < mt; t++) {
-        float m = 0.0f;
+template <int GRAN, bool PADDED>
+__device__ __forceinline__ void stage_x_store(const GemvArgs &a, int kc, const XRaw &raw, uint16_t *xs, float *xsum,
+                                              float *backs) {
+#pragma unroll
+    for (int j = 0; j < kXGroups; j++) {
+        // the four lanes of one 32-element block are all valid or all invalid (mt * per_tok
+        // is a multiple of 32 groups and nth a multiple of 64), so the DPP steps below only
+        // read active lanes; waves without a valid group skip the conversion
+        if (!raw.valid[j]) continue;
+        float v[8];
         if (a.x_bf16) {
-            const uint16_t *xp = (const uint16_t *)a.x + (int64_t)t * a.k;
-            for (int64_t i = (int64_t)tid * 8; i < a.k; i += (int64_t)nth * 8) {
-                u32x4 w = *reinterpret_cast<const u32x4 *>(xp + i);
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    m = fmaxf(m, fabsf(bf16_to_f32(w[j] & 0xFFFFu)));
-                    m = fmaxf(m, fabsf(bf16_to_f32(w[j] >> 16)));
-                }
-                // NaN propagation: fmaxf drops NaN, so test explicitly
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (((w[j] & 0x7FFFu) > 0x7F80u) || (((w[j] >> 16) & 0x7FFFu) > 0x7F80u)) m = INFINITY;
+            for (int i = 0; i < 4; i++) {
+                v[2 * i] = bf16_to_f32(raw.r[j][0][i] & 0xFFFFu);
+                v[2 * i + 1] = bf16_to_f32(raw.r[j][0][i] >> 16);
             }
         } else {
-            const float *xp = (const float *)a.x + (int64_t)t * a.k;
-            for (int64_t i = (int64_t)tid * 4; i < a.k; i += (int64_t)nth * 4) {
-                floatx4 w = *reinterpret_cast<const floatx4 *>(xp + i);
 #pragma unroll
-                for (int j = 0; j < 4; j++) m = (fabsf(w[j]) <= m) ? m : (fabsf(w[j]) > m ? fabsf(w[j]) : INFINITY);
+            for (int i = 0; i < 4; i++) {
+                v[i] = __uint_as_float(raw.r[j][0][i]);
+                v[4 + i] = __uint_as_float(raw.r[j][1][i]);
             }
         }
-        m = wave_max(m);
-        if (lane == 0) wred[wv] = m;
-        __syncthreads();
-        if (tid == 0) {
-            float mm = 0.0f;
-            for (int i = 0; i < nw; i++) mm = fmaxf(mm, wred[i]);
-            scl[t] = f16_prescale(mm);
+        if (PADDED) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = raw.in[j] ? v[i] : 0.0f;
         }
-        __syncthreads();
+        float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            amax = fmaxf(amax, fabsf(v[i]));
+            sum += v[i];
+        }
+        if (!(fabsf(sum) <= 3.0e38f)) amax = INFINITY;  // NaN / inf in this group
+        amax = fmaxf(amax, dpp_xor1(amax));
+        amax = fmaxf(amax, dpp_xor2(amax));
+        float s, back;
+        f16_prescale(amax, s, back);
+        u32x4 H, L;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t h0, l0, h1, l1;
+            split_f16(v[2 * i] * s, h0, l0);
+            split_f16(v[2 * i + 1] * s, h1, l1);
+            H[i] = h0 | (h1 << 16);
+            L[i] = l0 | (l1 << 16);
+        }
+        float tot = sum + dpp_xor1(sum);
+        if (GRAN == 32) tot += dpp_xor2(tot);
+        {
+            const int t = raw.t[j], g8 = raw.g8[j];
+            *reinterpret_cast<u32x4 *>(xs + ((size_t)t * 2 + 0) * kc + 8 * g8) = H;
+            *reinterpret_cast<u32x4 *>(xs + ((size_t)t * 2 + 1) * kc + 8 * g8) = L;
+            if ((g8 & (GRAN / 8 - 1)) == 0) xsum[(size_t)t * (kc / GRAN) + g8 / (GRAN / 8)] = tot;
+            if ((g8 & 3) == 0) backs[t * (kc / 32) + g8 / 4] = back;
+        }
     }
 }
 
@@ -196,58 +203,81 @@ __device__ __forceinline__ u32x4 a_operand4(const uint16_t *xs, int kc, int mt, 
     return u32x4{0u, 0u, 0u, 0u};
 }
 
-__device__ __forceinline__ void compute_unit(const UnitQ4K &u, const uint16_t *xs, const float *xsum, int kc, int mt,
-                                             int kk, float acc1[2], float acc2[2]) {
-    const int g = (threadIdx.x & 63) >> 4;
-    // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K packing)
+// Q4_K, sub-block-per-lane-group form.  Lane 16G + n holds row n's 32 bytes of
+// group G, i.e. sub-blocks 2G (low nibbles) and 2G + 1 (high nibbles).  MFMA r of
+// a set consumes bytes 8r .. 8r + 7, so every lane group contributes 8 k of ITS
+// sub-block; the A operand of row 4G + i is non-zero only in k-group G (lanes with
+// l / 16 == (l % 16) / 4 read the activation, the others read zeros), so output
+// rows 4G .. 4G + 3 of lane group G are partial dots over sub-block 2G (+1) alone,
+// for (token 2tp, hi), (2tp, lo), (2tp + 1, hi), (2tp + 1, lo).  Four chained MFMAs
+// finish a sub-block, and its 6-bit scale is applied once per lane.
+template <int NTP>
+__device__ __forceinline__ void compute_q4k(const UnitQ4K &u, const uint16_t *xs, const float *xsum,
+                                            const uint16_t *zero_lds, int kc, int mt, int ul, const float *backs,
+                                            float acc1[4][2], float acc2[4][2]) {
+    const int lane = threadIdx.x & 63, G = lane >> 4, m = lane & 15, i = m & 3;
+    const bool own = G == (m >> 2);
+    // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K packing,
+    // get_scale_min_k4, crates/nn-core/src/layers/quantized/linear.rs:166-176)
     const float d = f16_to_f32(u.h[0] & 0xFFFFu), dmin = f16_to_f32(u.h[0] >> 16);
     const uint32_t S1 = u.h[1], S2 = u.h[2], S3 = u.h[3];
     const uint32_t sc03 = S1 & 0x3F3F3F3Fu, mn03 = S2 & 0x3F3F3F3Fu;
     const uint32_t sc47 = (S3 & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
     const uint32_t mn47 = ((S3 >> 4) & 0x0F0F0F0Fu) | ((S2 >> 2) & 0x30303030u);
-    float t1e[2] = {0.f, 0.f}, t1o[2] = {0.f, 0.f}, t2[2] = {0.f, 0.f};
-    const float *xs0 = xsum + (size_t)(2 * g) * (kc / 32) + kk / 32;
-    const float *xs1 = xsum + (size_t)(2 * g + 1) * (kc / 32) + kk / 32;
-    const bool tok0 = 2 * g < mt, tok1 = 2 * g + 1 < mt;
+    const uint32_t hsel = 0u - (uint32_t)(G >> 1);  // all ones for sub-blocks 4..7
+    const uint32_t scw = (sc03 & ~hsel) | (sc47 & hsel), mnw = (mn03 & ~hsel) | (mn47 & hsel);
+    const uint32_t scp = scw >> (16 * (G & 1)), mnp = mnw >> (16 * (G & 1));
+    const float sc_lo = (float)(scp & 0xFFu), sc_hi = 0.0625f * (float)((scp >> 8) & 0xFFu);
+    const float mn_lo = (float)(mnp & 0xFFu), mn_hi = (float)((mnp >> 8) & 0xFFu);
+
+    floatx4 clo[NTP], chi[NTP];
+    const uint16_t *ap[NTP];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const u32x4 q = h ? u.q1 : u.q0;
-        const uint32_t scb = h ? sc47 : sc03, mnb = h ? mn47 : mn03;
+    for (int tp = 0; tp < NTP; tp++) {
+        clo[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
+        chi[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const int t = 2 * tp + (i >> 1);
+        ap[tp] = (own && t < mt) ? xs + (size_t)(t * 2 + (i & 1)) * kc + ul * 256 + 64 * G : zero_lds;
+    }
 #pragma unroll
-        for (int gg = 0; gg < 2; gg++) {
-            const uint32_t w0 = q[2 * gg], w1 = q[2 * gg + 1];
-            const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
-            const u32x4 blo = {w0 & 0x000F000Fu, w0s & 0x000F000Fu, w1 & 0x000F000Fu, w1s & 0x000F000Fu};
-            const u32x4 bhi = {w0 & 0x00F000F0u, w0s & 0x00F000F0u, w1 & 0x00F000F0u, w1s & 0x00F000F0u};
-            const int jl = 4 * h + 2 * gg, jh = jl + 1;  // sub-block indices (low / high nibbles)
-            const int klo = kk + 64 * (2 * h + gg), khi = klo + 32;
-            floatx4 cl = mfma16x16x32_f16(a_operand2(xs, kc, mt, klo), blo, floatx4{0.f, 0.f, 0.f, 0.f});
-            floatx4 ch = mfma16x16x32_f16(a_operand2(xs, kc, mt, khi), bhi, floatx4{0.f, 0.f, 0.f, 0.f});
-            const float scl = (float)((scb >> (16 * gg)) & 0xFFu), sch = (float)((scb >> (16 * gg + 8)) & 0xFFu);
-            const float mnl = (float)((mnb >> (16 * gg)) & 0xFFu), mnh = (float)((mnb >> (16 * gg + 8)) & 0xFFu);
-            t1e[0] += scl * (cl[0] + cl[1]);
-            t1e[1] += scl * (cl[2] + cl[3]);
-            t1o[0] += sch * (ch[0] + ch[1]);
-            t1o[1] += sch * (ch[2] + ch[3]);
-            const float x0l = tok0 ? xs0[jl] : 0.f, x0h = tok0 ? xs0[jh] : 0.f;
-            const float x1l = tok1 ? xs1[jl] : 0.f, x1h = tok1 ? xs1[jh] : 0.f;
-            t2[0] += mnl * x0l + mnh * x0h;
-            t2[1] += mnl * x1l + mnh * x1h;
+    for (int r = 0; r < 4; r++) {
+        const u32x4 q = r < 2 ? u.q0 : u.q1;
+        const uint32_t w0 = q[2 * (r & 1)], w1 = q[2 * (r & 1) + 1];
+        const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
+        const u32x4 blo = {w0 & 0x000F000Fu, w0s & 0x000F000Fu, w1 & 0x000F000Fu, w1s & 0x000F000Fu};
+        const u32x4 bhi = {w0 & 0x00F000F0u, w0s & 0x00F000F0u, w1 & 0x00F000F0u, w1s & 0x00F000F0u};
+#pragma unroll
+        for (int tp = 0; tp < NTP; tp++) {
+            clo[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 8 * r), blo, clo[tp]);
+            chi[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 32 + 8 * r), bhi, chi[tp]);
         }
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        acc1[i] += d * (t1e[i] + 0.0625f * t1o[i]);
-        acc2[i] += dmin * t2[i];
+    for (int tp = 0; tp < NTP; tp++) {
+        {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int t = 2 * tp + h;
+                if (t < mt) {
+                    const float *bk = backs + t * (kc / 32) + ul * 8 + 2 * G;
+                    const float T = (sc_lo * bk[0]) * (clo[tp][2 * h] + clo[tp][2 * h + 1]) +
+                                    (sc_hi * bk[1]) * (chi[tp][2 * h] + chi[tp][2 * h + 1]);
+                    acc1[tp][h] += d * T;
+                    const float *xsp = xsum + (size_t)t * (kc / 32) + ul * 8 + 2 * G;
+                    acc2[tp][h] += dmin * (mn_lo * xsp[0] + mn_hi * xsp[1]);
+                }
+            }
+        }
     }
 }
 
 __device__ __forceinline__ void compute_unit(const UnitQ80 &u, const uint16_t *xs, const float *xsum, int kc, int mt,
-                                             int kk, float acc1[2], float acc2[2]) {
+                                             int kk, const float *bku, float acc1[2], float acc2[2]) {
     const int g = (threadIdx.x & 63) >> 4;
     const float *xs0 = xsum + (size_t)(2 * g) * (kc / 32) + kk / 32;
     const float *xs1 = xsum + (size_t)(2 * g + 1) * (kc / 32) + kk / 32;
     const bool tok0 = 2 * g < mt, tok1 = 2 * g + 1 < mt;
+    float t1[2] = {0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
 #pragma unroll
@@ -257,16 +287,20 @@ __device__ __forceinline__ void compute_unit(const UnitQ80 &u, const uint16_t *x
             const u32x4 b = {w0 & 0x00FF00FFu, (w0 >> 8) & 0x00FF00FFu, w1 & 0x00FF00FFu, (w1 >> 8) & 0x00FF00FFu};
             floatx4 c = mfma16x16x32_f16(a_operand2(xs, kc, mt, kk + 32 * j), b, floatx4{0.f, 0.f, 0.f, 0.f});
             const float dj = f16_to_f32((u.h[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-            acc1[0] += dj * (c[0] + c[1]);
-            acc1[1] += dj * (c[2] + c[3]);
+            const float b0 = tok0 ? bku[(2 * g) * (kc / 32) + j] : 0.f;
+            const float b1 = tok1 ? bku[(2 * g + 1) * (kc / 32) + j] : 0.f;
+            t1[0] += (dj * b0) * (c[0] + c[1]);
+            t1[1] += (dj * b1) * (c[2] + c[3]);
             acc2[0] += dj * (tok0 ? xs0[j] : 0.f);
             acc2[1] += dj * (tok1 ? xs1[j] : 0.f);
         }
     }
+    acc1[0] += t1[0];
+    acc1[1] += t1[1];
 }
 
 __device__ __forceinline__ void compute_unit(const UnitQ6K &u, const uint16_t *xs, const float *xsum, int kc, int mt,
-                                             int kk, float acc1[2], float acc2[2]) {
+                                             int kk, const float *bku, float acc1[2], float acc2[2]) {
     const int g = (threadIdx.x & 63) >> 4;  // token of this lane group
     const bool tok = g < mt;
     const float *xsg = xsum + (size_t)g * (kc / 16) + kk / 16;
@@ -289,7 +323,8 @@ __device__ __forceinline__ void compute_unit(const UnitQ6K &u, const uint16_t *x
         const uint32_t sw = u.s[c];
         const float s0 = (float)(int8_t)(sw & 0xFF), s1 = (float)(int8_t)((sw >> 8) & 0xFF);
         const float s2 = (float)(int8_t)((sw >> 16) & 0xFF), s3 = (float)(int8_t)(sw >> 24);
-        t1 += s0 * (ca[0] + ca[1]) + s1 * (ca[2] + ca[3]) + s2 * (cb[0] + cb[1]) + s3 * (cb[2] + cb[3]);
+        const float xba = tok ? bku[g * (kc / 32) + 2 * c] : 0.f, xbb = tok ? bku[g * (kc / 32) + 2 * c + 1] : 0.f;
+        t1 += xba * (s0 * (ca[0] + ca[1]) + s1 * (ca[2] + ca[3])) + xbb * (s2 * (cb[0] + cb[1]) + s3 * (cb[2] + cb[3]));
         if (tok) t2 += s0 * xsg[4 * c] + s1 * xsg[4 * c + 1] + s2 * xsg[4 * c + 2] + s3 * xsg[4 * c + 3];
     }
     acc1[0] += d * t1;
@@ -317,7 +352,11 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
     return ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - idx);
 }
 
-template <int FMT, int WAVES>
+// One workgroup per 16-row tile.  Per K chunk: the raw activation loads are issued
+// first, then every wave issues the weight loads of all its units of the chunk
+// (unit u goes to wave u % WAVES), then the activation is converted into LDS while
+// the weight loads are in flight, and finally each wave runs its units on the MFMA.
+template <int FMT, int WAVES, int NTP, int UPW>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     using Unit = typename UnitOf<FMT>::T;
@@ -328,33 +367,41 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     const int kc = a.kc;
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
     float *xsum = reinterpret_cast<float *>(smem + (size_t)mt * kc * 4);
-    __shared__ float scl[8];
-    __shared__ float wred[WAVES];
+    __shared__ float backs[kXGroups * WAVES * 64 * 8 / 32];  // one per staged 32-element block
 
     const int64_t kpad = a.nblk * (FMT == FQ80 ? 32 : 256);  // K rounded up to whole 256-element units
 
-    // issue the first unit's weight loads before touching x
-    Unit cur;
-    int kcur0 = (int)(kpad < kc ? kpad : kc);
-    if (wv < kcur0 / 256) load_unit(a, tile, wv, cur);
+    __shared__ u32x4 zero_lds[8];  // A operand of lanes that carry no activation (Q4_K)
+    if (tid < 8) zero_lds[tid] = u32x4{0u, 0u, 0u, 0u};
 
-    token_scales(a, mt, scl, wred);
-
-    float acc1[2] = {0.f, 0.f}, acc2[2] = {0.f, 0.f};
+    // Q4_K: acc[tp][h] = token 2tp + h (partial over this lane group's sub-blocks);
+    // Q8_0 / Q6_K: acc[0][*] as in the per-token-row form
+    float acc1[4][2] = {}, acc2[4][2] = {};
     for (int64_t k0 = 0; k0 < kpad; k0 += kc) {
         const int kcur = (int)((kpad - k0) < kc ? (kpad - k0) : kc);
         const int64_t u0 = k0 / 256;
         const int ucnt = kcur / 256;
-        if (k0 > 0 && wv < ucnt) load_unit(a, tile, u0 + wv, cur);
+        XRaw raw;
+        stage_x_load(a, mt, k0, kcur, 1.0f / (float)(kcur / 8), raw);
+        Unit buf[UPW];
+#pragma unroll
+        for (int i = 0; i < UPW; i++) {
+            const int ul = wv + i * WAVES;
+            load_unit(a, tile, u0 + (ul < ucnt ? ul : ucnt - 1), buf[i]);  // unconditional: see stage_x_load
+        }
+        if (k0 > 0) __syncthreads();  // the previous chunk's units have finished reading LDS
+        stage_x_store<GRAN, FMT == FQ80>(a, kc, raw, xs, xsum, backs);
         __syncthreads();
-        stage_x<GRAN>(a, mt, k0, kcur, kc, scl, xs, xsum);
-        __syncthreads();
-        for (int ul = wv; ul < ucnt; ul += WAVES) {
-            Unit nxt;
-            const bool has = ul + WAVES < ucnt;
-            if (has) load_unit(a, tile, u0 + ul + WAVES, nxt);
-            compute_unit(cur, xs, xsum, kc, mt, ul * 256, acc1, acc2);
-            if (has) cur = nxt;
+#pragma unroll
+        for (int i = 0; i < UPW; i++) {
+            const int ul = wv + i * WAVES;
+            if (ul < ucnt) {
+                if constexpr (FMT == FQ4K)
+                    compute_q4k<NTP>(buf[i], xs, xsum, reinterpret_cast<const uint16_t *>(zero_lds), kc, mt, ul, backs,
+                                acc1, acc2);
+                else
+                    compute_unit(buf[i], xs, xsum, kc, mt, ul * 256, backs + ul * 8, acc1[0], acc2[0]);
+            }
         }
     }
     __syncthreads();
@@ -363,14 +410,30 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     float *red1 = reinterpret_cast<float *>(smem);
     float *red2 = red1 + WAVES * 8 * 16;
     const int g = lane >> 4, n = lane & 15;
-    if (FMT == FQ6K) {
-        red1[(wv * 8 + g) * 16 + n] = acc1[0];
-        red2[(wv * 8 + g) * 16 + n] = acc2[0];
+    if constexpr (FMT == FQ4K) {
+        // sum the four lane groups (sub-block partials), lane group 0 stores
+#pragma unroll
+        for (int tp = 0; tp < NTP; tp++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float v1 = acc1[tp][h], v2 = acc2[tp][h];
+                v1 += __shfl_xor(v1, 16, 64);
+                v2 += __shfl_xor(v2, 16, 64);
+                v1 += __shfl_xor(v1, 32, 64);
+                v2 += __shfl_xor(v2, 32, 64);
+                if (g == 0) {
+                    red1[(wv * 8 + 2 * tp + h) * 16 + n] = v1;
+                    red2[(wv * 8 + 2 * tp + h) * 16 + n] = v2;
+                }
+            }
+    } else if constexpr (FMT == FQ6K) {
+        red1[(wv * 8 + g) * 16 + n] = acc1[0][0];
+        red2[(wv * 8 + g) * 16 + n] = acc2[0][0];
     } else {
-        red1[(wv * 8 + 2 * g) * 16 + n] = acc1[0];
-        red1[(wv * 8 + 2 * g + 1) * 16 + n] = acc1[1];
-        red2[(wv * 8 + 2 * g) * 16 + n] = acc2[0];
-        red2[(wv * 8 + 2 * g + 1) * 16 + n] = acc2[1];
+        red1[(wv * 8 + 2 * g) * 16 + n] = acc1[0][0];
+        red1[(wv * 8 + 2 * g + 1) * 16 + n] = acc1[0][1];
+        red2[(wv * 8 + 2 * g) * 16 + n] = acc2[0][0];
+        red2[(wv * 8 + 2 * g + 1) * 16 + n] = acc2[0][1];
     }
     __syncthreads();
     if (tid < mt * 16) {
@@ -380,9 +443,189 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             s1 += red1[(w * 8 + t) * 16 + nn];
             s2 += red2[(w * 8 + t) * 16 + nn];
         }
-        const float back = 16777216.0f / scl[t];  // 2^(24 - s)
+        // s1 carries the f16-subnormal factor 2^-24 of the integer weight codes
         const float bias_k = FMT == FQ4K ? 1.0f : (FMT == FQ80 ? 128.0f : 32.0f);
-        float y = s1 * back - bias_k * s2;
+        float y = s1 * 16777216.0f - bias_k * s2;
+        const int64_t row = tile * 16 + nn;
+        if (row < a.n) {
+            if (a.bias) y += a.bias[row];
+            if (a.y_bf16)
+                reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+            else
+                reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+        }
+        if (a.argmax_partial && t == 0) {
+            // first-index argmax of this tile's 16 logits (row-major order), NaN -> max key
+            uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
+            for (int o = 8; o > 0; o >>= 1) {
+                uint64_t other = __shfl_xor(key, o, 16);
+                key = other > key ? other : key;
+            }
+            if (nn == 0) a.argmax_partial[tile] = key;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Decode kernel (m <= 2 tokens): every wave works on its own units from start to
+// end.  It issues the activation slices and the (non-temporal) weight loads of all
+// its units first, then per unit converts its activation slice into a wave-private
+// LDS buffer and runs the MFMAs on it, so units are consumed in arrival order and
+// there is no workgroup barrier before the final cross-wave reduction.
+// ---------------------------------------------------------------------------------
+constexpr int kUnitBufHalfs = 2 * 2 * 256;  // [token][hi/lo][256] f16
+struct UnitBuf {
+    uint16_t xs[kUnitBufHalfs];
+    float xsum[2 * 16];  // [token][256 / GRAN]
+    float backs[2 * 8];  // [token][8 blocks of 32]
+};
+
+// Lane l holds elements 4l .. 4l + 3 of the unit for one token.
+template <int GRAN, bool PADDED>
+__device__ __forceinline__ void stage_unit(const u32x4 &raw, bool x_bf16, bool in, int t, UnitBuf &ub) {
+    const int lane = threadIdx.x & 63;
+    float v[4];
+    if (x_bf16) {
+        v[0] = bf16_to_f32(raw[0] & 0xFFFFu);
+        v[1] = bf16_to_f32(raw[0] >> 16);
+        v[2] = bf16_to_f32(raw[1] & 0xFFFFu);
+        v[3] = bf16_to_f32(raw[1] >> 16);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = __uint_as_float(raw[i]);
+    }
+    if (PADDED) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = in ? v[i] : 0.0f;
+    }
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const float sum = (v[0] + v[1]) + (v[2] + v[3]);
+    if (!(fabsf(sum) <= 3.0e38f)) amax = INFINITY;  // NaN / inf in this lane's values
+    // max over the 8 lanes of each 32-element block
+    amax = fmaxf(amax, dpp_xor1(amax));
+    amax = fmaxf(amax, dpp_xor2(amax));
+    amax = fmaxf(amax, dpp_half_mirror(amax));
+    float s, back;
+    f16_prescale(amax, s, back);
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) split_f16(v[i] * s, h[i], l[i]);
+    *reinterpret_cast<u32x2 *>(ub.xs + (t * 2 + 0) * 256 + 4 * lane) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    *reinterpret_cast<u32x2 *>(ub.xs + (t * 2 + 1) * 256 + 4 * lane) = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+    float tot = sum + dpp_xor1(sum);
+    tot += dpp_xor2(tot);
+    if (GRAN == 32) tot += dpp_half_mirror(tot);
+    if ((lane & (GRAN / 4 - 1)) == 0) ub.xsum[t * (256 / GRAN) + lane / (GRAN / 4)] = tot;
+    if ((lane & 7) == 0) ub.backs[t * 8 + lane / 8] = back;
+}
+
+template <int FMT, int WAVES, int UPW>
+__global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
+    using Unit = typename UnitOf<FMT>::T;
+    constexpr int GRAN = Fmt<FMT>::kSumGran;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t tile = blockIdx.x;
+    const int mt = (int)a.m;  // 1 or 2
+    __shared__ __attribute__((aligned(16))) UnitBuf ubuf[WAVES][2];
+    __shared__ u32x4 zero_lds[8];
+    __shared__ float red[WAVES][2][2][16];  // [wave][acc1/acc2][token][row]
+    if (tid < 8) zero_lds[tid] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+
+    const int64_t units = FMT == FQ80 ? a.nblk / 8 : a.nblk;
+    const size_t xe = a.x_bf16 ? 2 : 4;
+    float acc1[4][2] = {}, acc2[4][2] = {};
+    for (int64_t ub0 = 0; ub0 < units; ub0 += WAVES * UPW) {
+        // activation slices first (their wait then does not cover the weight loads)
+        u32x4 xr[UPW][2];
+        bool xin[UPW];
+        int64_t uu[UPW];
+#pragma unroll
+        for (int i = 0; i < UPW; i++) {
+            const int64_t u = ub0 + wv + i * WAVES;
+            uu[i] = u < units ? u : units - 1;
+            const int64_t kk = uu[i] * 256 + 4 * lane;
+            xin[i] = kk < a.k;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int64_t off = xin[i] ? (int64_t)(t < mt ? t : 0) * a.k + kk : 0;
+                const uint8_t *p = reinterpret_cast<const uint8_t *>(a.x) + off * xe;
+                if (a.x_bf16) {
+                    const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+                    xr[i][t] = u32x4{w2[0], w2[1], 0u, 0u};
+                } else {
+                    xr[i][t] = *reinterpret_cast<const u32x4 *>(p);
+                }
+            }
+        }
+        Unit w[UPW];
+#pragma unroll
+        for (int i = 0; i < UPW; i++) load_unit(a, tile, uu[i], w[i]);
+#pragma unroll
+        for (int i = 0; i < UPW; i++) {
+            if (ub0 + wv + i * WAVES >= units) break;  // wave-uniform
+            UnitBuf &b = ubuf[wv][i & 1];
+            stage_unit<GRAN, FMT == FQ80>(xr[i][0], a.x_bf16, xin[i], 0, b);
+            if (mt > 1) stage_unit<GRAN, FMT == FQ80>(xr[i][1], a.x_bf16, xin[i], 1, b);
+            // the wave's own LDS writes are read back by other lanes of the same wave
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if constexpr (FMT == FQ4K)
+                compute_q4k<1>(w[i], b.xs, b.xsum, reinterpret_cast<const uint16_t *>(zero_lds), 256, mt, 0, b.backs,
+                               acc1, acc2);
+            else
+                compute_unit(w[i], b.xs, b.xsum, 256, mt, 0, b.backs, acc1[0], acc2[0]);
+        }
+    }
+
+    // combine the waves (and, for Q4_K, the four lane groups)
+    const int g = lane >> 4, n = lane & 15;
+    float r1[2], r2[2];
+    if constexpr (FMT == FQ4K) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float v1 = acc1[0][h], v2 = acc2[0][h];
+            v1 += __shfl_xor(v1, 16, 64);
+            v2 += __shfl_xor(v2, 16, 64);
+            v1 += __shfl_xor(v1, 32, 64);
+            v2 += __shfl_xor(v2, 32, 64);
+            r1[h] = v1;
+            r2[h] = v2;
+        }
+        if (g == 0) {
+            red[wv][0][0][n] = r1[0];
+            red[wv][0][1][n] = r1[1];
+            red[wv][1][0][n] = r2[0];
+            red[wv][1][1][n] = r2[1];
+        }
+    } else if constexpr (FMT == FQ6K) {
+        // lane group g holds token g
+        if (g < 2) {
+            red[wv][0][g][n] = acc1[0][0];
+            red[wv][1][g][n] = acc2[0][0];
+        }
+    } else {
+        // lane group 0 holds tokens 0 and 1
+        if (g == 0) {
+            red[wv][0][0][n] = acc1[0][0];
+            red[wv][0][1][n] = acc1[0][1];
+            red[wv][1][0][n] = acc2[0][0];
+            red[wv][1][1][n] = acc2[0][1];
+        }
+    }
+    __syncthreads();
+    if (tid < mt * 16) {
+        const int t = tid >> 4, nn = tid & 15;
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; w2++) {
+            s1 += red[w2][0][t][nn];
+            s2 += red[w2][1][t][nn];
+        }
+        // s1 carries the f16-subnormal factor 2^-24 of the integer weight codes
+        const float bias_k = FMT == FQ4K ? 1.0f : (FMT == FQ80 ? 128.0f : 32.0f);
+        float y = s1 * 16777216.0f - bias_k * s2;
         const int64_t row = tile * 16 + nn;
         if (row < a.n) {
             if (a.bias) y += a.bias[row];
@@ -413,47 +656,43 @@ __global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t *qs, con
     const int64_t job = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (job >= ntile * nblk) return;
     const int64_t tile = job / nblk, b = job % nblk;
-    const int r = lane & 15, p = lane >> 4;
+    const int r = lane & 15, p = lane >> 4;  // row r of the tile, byte group p (sub-blocks 2p, 2p + 1)
     const int64_t row = tile * 16 + r;
     const uint8_t *qb = qs + job * 2048 + 16 * lane;
     const u32x4 h = ldg128(hdr + job * 256 + 16 * r);
     if (row >= n) return;
     const float d = f16_to_f32(h[0] & 0xFFFFu), dmin = f16_to_f32(h[0] >> 16);
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(&h) + 4;
-    float *o = out + row * k + b * 256;
+    // get_scale_min_k4 (crates/nn-core/src/layers/quantized/linear.rs:166-176)
+    auto gsm = [&](int j, uint32_t &sc, uint32_t &mn) {
+        if (j < 4) {
+            sc = sb[j] & 63;
+            mn = sb[j + 4] & 63;
+        } else {
+            sc = (sb[j + 4] & 0xF) | ((sb[j - 4] >> 6) << 4);
+            mn = (sb[j + 4] >> 4) | ((sb[j] >> 6) << 4);
+        }
+    };
+    uint32_t scl, mnl, sch, mnh;
+    gsm(2 * p, scl, mnl);
+    gsm(2 * p + 1, sch, mnh);
+    // BlockQ4K::dequantize (linear.rs:73-89): d1 = d * sc, m1 = dmin * m, v = d1 * q - m1
+    const float d1 = d * (float)scl, m1 = dmin * (float)mnl;
+    const float d2 = d * (float)sch, m2 = dmin * (float)mnh;
+    float *o = out + row * k + b * 256 + 64 * p;
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
         const u32x4 q = ldg128(qb + 1024 * hh);
 #pragma unroll
-        for (int gg = 0; gg < 2; gg++) {
-            const int gidx = 2 * hh + gg;
-            int jl = 2 * gidx, jh = jl + 1;
-            uint32_t scl, ml, sch, mh;
-            // get_scale_min_k4 (crates/nn-core/src/layers/quantized/linear.rs:166-176)
-            auto gsm = [&](int j, uint32_t &s, uint32_t &m) {
-                if (j < 4) {
-                    s = sb[j] & 63;
-                    m = sb[j + 4] & 63;
-                } else {
-                    s = (sb[j + 4] & 0xF) | ((sb[j - 4] >> 6) << 4);
-                    m = (sb[j + 4] >> 4) | ((sb[j] >> 6) << 4);
-                }
-            };
-            gsm(jl, scl, ml);
-            gsm(jh, sch, mh);
-            const float d1 = d * (float)scl, m1 = dmin * (float)ml;
-            const float d2 = d * (float)sch, m2 = dmin * (float)mh;
+        for (int w = 0; w < 4; w++) {
+            const uint32_t word = q[w];
+            // stored byte order (e0, e2, e1, e3) of bytes i0 .. i0 + 3
+            const uint32_t e[4] = {word & 0xFF, (word >> 16) & 0xFF, (word >> 8) & 0xFF, word >> 24};
+            const int i0 = 16 * hh + 4 * w;
 #pragma unroll
-            for (int w = 0; w < 2; w++) {
-                const uint32_t word = q[2 * gg + w];
-                // stored byte order (e0, e2, e1, e3) of elements i0..i0+3
-                const uint32_t e[4] = {word & 0xFF, (word >> 16) & 0xFF, (word >> 8) & 0xFF, word >> 24};
-                const int i0 = 8 * p + 4 * w;
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    o[64 * gidx + i0 + c] = d1 * (float)(e[c] & 0xF) - m1;
-                    o[64 * gidx + 32 + i0 + c] = d2 * (float)(e[c] >> 4) - m2;
-                }
+            for (int c = 0; c < 4; c++) {
+                o[i0 + c] = d1 * (float)(e[c] & 0xF) - m1;
+                o[32 + i0 + c] = d2 * (float)(e[c] >> 4) - m2;
             }
         }
     }
@@ -564,38 +803,96 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int
 // ---------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------
-template <int FMT, int WAVES>
+template <int FMT, int WAVES, int NTP, int UPW>
 static int launch_gemv_t(const GemvArgs &a0, void *stream) {
     GemvArgs a = a0;
     const int mt = (int)a.m;
-    // largest K chunk (multiple of 256) whose staging fits in 64 KB
+    constexpr int gran = Fmt<FMT>::kSumGran;
     const int64_t kpad = a.nblk * (FMT == FQ80 ? 32 : 256);
-    int kc = (int)((65536 / ((size_t)mt * (4 + 4 * 1.0 / Fmt<FMT>::kSumGran))) / 256 * 256);
+    // K chunk: bounded by LDS (60 KB of staging), by the activation groups the
+    // threads stage in registers, and by the units the waves hold in registers
+    int64_t kc = (int64_t)(61440.0 / (mt * (4.0 + 4.0 / gran)));
+    const int64_t kc_x = (int64_t)kXGroups * WAVES * 64 * 8 / mt;
+    const int64_t kc_u = (int64_t)WAVES * UPW * 256;
+    if (kc > kc_x) kc = kc_x;
+    if (kc > kc_u) kc = kc_u;
+    kc = kc / 256 * 256;
     if (kc < 256) kc = 256;
-    if (kc > kpad) kc = (int)kpad;
-    a.kc = kc;
-    size_t lds = lds_bytes_for(mt, kc, Fmt<FMT>::kSumGran, WAVES);
-    hipLaunchKernelGGL((gemv_kernel<FMT, WAVES>), dim3((unsigned)a.ntile), dim3(WAVES * 64), lds,
+    if (kc > kpad) kc = kpad;
+    a.kc = (int)kc;
+    const size_t lds = lds_bytes_for(mt, a.kc, gran, WAVES);
+    hipLaunchKernelGGL((gemv_kernel<FMT, WAVES, NTP, UPW>), dim3((unsigned)a.ntile), dim3(WAVES * 64), lds,
                        (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
+// units per wave: just enough for one chunk to cover K (capped by registers)
+template <int FMT, int WAVES, int NTP>
+static int launch_gemv_u(const GemvArgs &a, int64_t units, void *stream) {
+    constexpr int umax = (FMT == FQ4K && NTP == 1) ? 6 : 3;
+    const int64_t need = (units + WAVES - 1) / WAVES;
+    if (need <= 1) return launch_gemv_t<FMT, WAVES, NTP, 1>(a, stream);
+    if (need <= 2) return launch_gemv_t<FMT, WAVES, NTP, 2>(a, stream);
+    if (need <= 3 || umax == 3) return launch_gemv_t<FMT, WAVES, NTP, 3>(a, stream);
+    if constexpr (umax > 3) {
+        if (need <= 4) return launch_gemv_t<FMT, WAVES, NTP, 4>(a, stream);
+        if (need <= 5) return launch_gemv_t<FMT, WAVES, NTP, 5>(a, stream);
+        return launch_gemv_t<FMT, WAVES, NTP, 6>(a, stream);
+    }
+    return (int)hipErrorInvalidValue;
+}
+
+template <int FMT, int NTP>
+static int launch_gemv_w(const GemvArgs &a, int64_t units, void *stream) {
+    // 8 waves (two per SIMD) unless K is too short to give each of them a unit
+    if (units >= 8) return launch_gemv_u<FMT, 8, NTP>(a, units, stream);
+    return launch_gemv_u<FMT, 4, NTP>(a, units, stream);
+}
+
+template <int FMT, int WAVES, int UPW>
+static int launch_wave_t(const GemvArgs &a, void *stream) {
+    hipLaunchKernelGGL((gemv_wave_kernel<FMT, WAVES, UPW>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                       (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+
+// decode (m <= 2): 8 waves with just enough units each to cover K in one pass
+// (longer K loops over passes)
+template <int FMT>
+static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
+    constexpr int umax = FMT == FQ4K ? 6 : 4;
+    if (units < 8) return launch_wave_t<FMT, 4, 2>(a, stream);
+    const int64_t need = (units + 7) / 8;
+    if (need <= 1) return launch_wave_t<FMT, 8, 1>(a, stream);
+    if (need <= 2) return launch_wave_t<FMT, 8, 2>(a, stream);
+    if (need <= 3) return launch_wave_t<FMT, 8, 3>(a, stream);
+    if (need <= 4 || umax == 4) return launch_wave_t<FMT, 8, 4>(a, stream);
+    if constexpr (umax > 4) {
+        if (need <= 5) return launch_wave_t<FMT, 8, 5>(a, stream);
+        return launch_wave_t<FMT, 8, 6>(a, stream);
+    }
+    return (int)hipErrorInvalidValue;
+}
+
 int launch_gemv(int fmt, const GemvArgs &a, void *stream) {
-    // fewer waves when K is short so that every wave owns at least one unit
-    const int64_t units = (a.k + 255) / 256;
+    if (a.m < 1 || a.m > 8 || (fmt == FQ6K && a.m > 4)) return (int)hipErrorInvalidValue;
+    const int64_t units = fmt == FQ80 ? a.nblk / 8 : a.nblk;
+    if (a.m <= 2) {
+        switch (fmt) {
+        case FQ4K: return launch_wave<FQ4K>(a, units, stream);
+        case FQ80: return launch_wave<FQ80>(a, units, stream);
+        case FQ6K: return launch_wave<FQ6K>(a, units, stream);
+        }
+        return (int)hipErrorInvalidValue;
+    }
     switch (fmt) {
     case FQ4K:
-        if (units >= 16) return launch_gemv_t<FQ4K, 16>(a, stream);
-        if (units >= 8) return launch_gemv_t<FQ4K, 8>(a, stream);
-        return launch_gemv_t<FQ4K, 4>(a, stream);
+        if (a.m <= 4) return launch_gemv_w<FQ4K, 2>(a, units, stream);
+        return launch_gemv_w<FQ4K, 4>(a, units, stream);
     case FQ80:
-        if (units >= 16) return launch_gemv_t<FQ80, 16>(a, stream);
-        if (units >= 8) return launch_gemv_t<FQ80, 8>(a, stream);
-        return launch_gemv_t<FQ80, 4>(a, stream);
+        return launch_gemv_w<FQ80, 1>(a, units, stream);
     case FQ6K:
-        if (units >= 16) return launch_gemv_t<FQ6K, 16>(a, stream);
-        if (units >= 8) return launch_gemv_t<FQ6K, 8>(a, stream);
-        return launch_gemv_t<FQ6K, 4>(a, stream);
+        return launch_gemv_w<FQ6K, 1>(a, units, stream);
     }
     return (int)hipErrorInvalidValue;
 }

@@ -32,8 +32,10 @@ struct Layout {
     size_t total() const { return qs_bytes + hdr_bytes; }
 };
 
-// Q4_K: per (tile, block of 256): qs 2048 B (two 1 KB halves: groups {0,1}, {2,3}),
-//       header 16 rows x 16 B (d, dmin, scales[12] in GGUF-spec packing).
+// Q4_K: per (tile, block of 256): qs 2048 B (two 1 KB planes; lane 16p + r of plane h
+//       holds bytes [16h, 16h + 16) of row r's 32-byte group p, i.e. the nibbles of
+//       sub-blocks 2p (low) and 2p + 1 (high)), header 16 rows x 16 B (d, dmin,
+//       scales[12] in GGUF-spec packing).
 // Q8_0: per (tile, block pair): qs 1024 B; per (tile, 8 blocks): 16 rows x 8 f16 scales.
 // Q6_K: per (tile, block of 256): qs 3072 B (four 64-k chunks x 64 lanes x 12 B),
 //       header 16 rows x 16 int8 scales + 16 rows x f16 d (288 B).

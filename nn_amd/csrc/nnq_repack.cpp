@@ -128,14 +128,14 @@ void repack_q4k(const uint8_t *src, int legacy, const Layout &L, uint8_t *dst) {
                     blk = tmp;
                 }
                 std::memcpy(hdr + (t * L.nblk + b) * 256 + 16 * r, blk, 16);
+                // lane l = 16p + r of plane h holds bytes [16h, 16h + 16) of group p (the 32
+                // bytes whose low / high nibbles are sub-blocks 2p / 2p + 1) of row r
                 uint8_t *qb = qs + (t * L.nblk + b) * 2048;
                 for (int h = 0; h < 2; h++)
                     for (int p = 0; p < 4; p++) {
                         uint8_t *d = qb + 1024 * h + 16 * (16 * p + r);
-                        for (int gg = 0; gg < 2; gg++) {
-                            int g = 2 * h + gg;
-                            put_perm8(d + 8 * gg, blk + 16 + 32 * g + 8 * p);
-                        }
+                        put_perm8(d, blk + 16 + 32 * p + 16 * h);
+                        put_perm8(d + 8, blk + 16 + 32 * p + 16 * h + 8);
                     }
             }
 }

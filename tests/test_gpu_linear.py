@@ -122,7 +122,7 @@ def test_dequant_q4k_reference_known_block(O):
 
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q4_k_legacy", "q6_k"])
 @pytest.mark.parametrize("n,k", [(48, 256), (37, 1024), (300, 4096)])
-@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 8])
 def test_linear_small(O, dev, fmt, n, k, m):
     import nn_amd
     b = quantized_weight_bytes(fmt, n, k, seed=1000 + n + k, O=O)
