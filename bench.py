@@ -105,6 +105,36 @@ def bench_q4k_gemv(steps, warmup):
                 n=n, k=k)
 
 
+def bench_q4k_gemm(m, n, k, steps, warmup, min_bytes=256 << 20):
+    """Prefill GEMM: X [m, k] bf16 (N(0,1)) x Q4_K W [n, k]^T -> Y [m, n] bf16, f32 accumulate.
+    A call is the activation staging kernel plus the GEMM kernel."""
+    import torch
+
+    import nn_amd
+    w = nn_amd.synth_normal(4, k, (n, k), 0.02)
+    wb = nn_amd.quantize_q4_k(w)
+    copies = make_copies(wb, nn_amd.QuantType.Q4_K, n, k, min_bytes)
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(nn_amd.synth_normal(4, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    ys = [torch.empty((m, n), device=dev, dtype=torch.bfloat16) for _ in copies]
+    from nn_amd import _lib
+    import ctypes
+    L = _lib.load()
+
+    def launcher(wi, yi):
+        def f():
+            st = torch.cuda.current_stream().cuda_stream
+            rc = L.nnq_linear(wi.handle, ctypes.c_void_p(x.data_ptr()), 2, m, k, None, 0,
+                              ctypes.c_void_p(yi.data_ptr()), 2, ctypes.c_void_p(st))
+            assert rc == 0, _lib.last_error()
+        return f
+
+    fns = [launcher(c, y) for c, y in zip(copies, ys)]
+    sec, nsteps = time_graph(fns, steps, warmup)
+    flops = 2.0 * m * n * k
+    return dict(sec=sec, steps=nsteps, tflops=flops / sec / 1e12, m=m, n=n, k=k, copies=len(copies))
+
+
 def cpu_baseline_q4k(wb, xnp, n, k, budget_s=10.0):
     from oracle import oracle as O
     t0 = time.perf_counter()
@@ -125,6 +155,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the quantized-linear kernels run on one device's share "
@@ -139,6 +170,17 @@ def main():
     gbs = r["algo_bytes"] / r["sec"] / 1e9
     gbs1 = r["algo_bytes"] / r["sec_single"] / 1e9
     log(f"  {r['sec'] * 1e6:.2f} us/step  {gbs:.1f} GB/s  (cache-resident single copy: {gbs1:.1f} GB/s)")
+
+    prefill = {}
+    if not args.no_prefill:
+        for (m, n, k) in [(512, 12288, 4096), (512, 4096, 12288)]:
+            log(f"bench: Q4_K prefill GEMM M={m} N={n} K={k} (bf16 in/out)")
+            g = bench_q4k_gemm(m, n, k, max(50, args.steps // 10), 20)
+            log(f"  {g['sec'] * 1e6:.2f} us/call  {g['tflops']:.1f} TFLOP/s "
+                f"({100 * g['tflops'] / FP16_PEAK_TFLOPS:.1f}% of fp16 dense peak)")
+            prefill[f"{m}x{n}x{k}"] = {"us_per_call": round(g["sec"] * 1e6, 3), "tflops": round(g["tflops"], 2),
+                                       "frac_fp16_peak": round(g["tflops"] / FP16_PEAK_TFLOPS, 4),
+                                       "tokens_per_s": round(m / g["sec"], 1)}
 
     cpu = None
     if not args.no_cpu:
@@ -170,6 +212,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
+        "prefill_q4k_gemm": prefill or None,
     }
     print(json.dumps(line), flush=True)
 

@@ -250,11 +250,8 @@ int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m,
         g.ntile = L.ntile;
         g.nblk = L.nblk;
         Scratch s;
-        HIP_TRY(s.alloc(gemm_scratch_bytes(m, L.k), (hipStream_t)stream), "scratch alloc");
-        uint8_t *base = (uint8_t *)s.p;
-        g.xs = (uint16_t *)base;
-        g.rowscale = (float *)(base + (size_t)m * L.k * 2);
-        g.xsum = (float *)(base + (size_t)m * L.k * 2 + (size_t)m * 4 + 256 - ((size_t)m * 4) % 256);
+        HIP_TRY(s.alloc(gemm_scratch_bytes(m, L.k, g.x_bf16), (hipStream_t)stream), "scratch alloc");
+        g.scratch = s.p;
         int e = launch_gemm_q4k(g, stream);
         if (e) return hip_fail((hipError_t)e, "gemm launch");
         return NNQ_OK;
@@ -329,41 +326,34 @@ int nnq_moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, co
     if (E <= 0 || H <= 0 || I <= 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "bad MoE shape");
     if (!gu_packed || !gu_scales || !gu_bias || !dn_packed || !dn_scales || !dn_bias)
         return fail(NNQ_ERR_INVALID_ARGUMENT, "null weight pointer");
-    if ((2 * I) % 32 || H % 32 || H % 16 || I % 16)
-        return fail(NNQ_ERR_INVALID_SHAPE, "MoE dims must be multiples of 32 along the output dimension");
+    if (H % 32 || I % 32)
+        return fail(NNQ_ERR_INVALID_SHAPE, "MoE hidden (%lld) and intermediate (%lld) sizes must be multiples of 32",
+                    (long long)H, (long long)I);
+    if (E > 256) return fail(NNQ_ERR_UNSUPPORTED, "at most 256 experts");
     const size_t gu_el = (size_t)E * H * 2 * I, dn_el = (size_t)E * I * H;
     nnq_moe *m = new nnq_moe;
     hipGetDevice(&m->device);
-    auto dalloc = [&](size_t bytes, void **p) -> hipError_t {
+    auto upload = [&](const void *src, size_t bytes, void **p) -> hipError_t {
         hipError_t e = hipMalloc(p, bytes);
-        if (e == hipSuccess) m->allocs.push_back(*p);
-        return e;
+        if (e != hipSuccess) return e;
+        m->allocs.push_back(*p);
+        return hipMemcpy(*p, src, bytes, hipMemcpyHostToDevice);
     };
-    std::vector<uint8_t> rq;
-    void *p[8] = {};
+    void *p[6] = {};
+    std::vector<uint8_t> rq, rs;
     hipError_t e = hipSuccess;
-    // repacked codes for the grouped GEMMs
     rq.resize(gu_el / 2);
-    moe_repack(gu_packed, E, H, 2 * I, rq.data());
-    if ((e = dalloc(gu_el / 2, &p[0])) == hipSuccess) e = hipMemcpy(p[0], rq.data(), gu_el / 2, hipMemcpyHostToDevice);
+    rs.resize(gu_el / 32);
+    moe_repack(gu_packed, gu_scales, E, H, 2 * I, rq.data(), rs.data());
+    if ((e = upload(rq.data(), rq.size(), &p[0])) == hipSuccess) e = upload(rs.data(), rs.size(), &p[1]);
     if (e == hipSuccess) {
         rq.resize(dn_el / 2);
-        moe_repack(dn_packed, E, I, H, rq.data());
-        if ((e = dalloc(dn_el / 2, &p[1])) == hipSuccess)
-            e = hipMemcpy(p[1], rq.data(), dn_el / 2, hipMemcpyHostToDevice);
+        rs.resize(dn_el / 32);
+        moe_repack(dn_packed, dn_scales, E, I, H, rq.data(), rs.data());
+        if ((e = upload(rq.data(), rq.size(), &p[2])) == hipSuccess) e = upload(rs.data(), rs.size(), &p[3]);
     }
-    if (e == hipSuccess && (e = dalloc(gu_el / 32, &p[2])) == hipSuccess)
-        e = hipMemcpy(p[2], gu_scales, gu_el / 32, hipMemcpyHostToDevice);
-    if (e == hipSuccess && (e = dalloc(dn_el / 32, &p[3])) == hipSuccess)
-        e = hipMemcpy(p[3], dn_scales, dn_el / 32, hipMemcpyHostToDevice);
-    if (e == hipSuccess && (e = dalloc((size_t)E * 2 * I * 4, &p[4])) == hipSuccess)
-        e = hipMemcpy(p[4], gu_bias, (size_t)E * 2 * I * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess && (e = dalloc((size_t)E * H * 4, &p[5])) == hipSuccess)
-        e = hipMemcpy(p[5], dn_bias, (size_t)E * H * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess && (e = dalloc(gu_el / 2, &p[6])) == hipSuccess)
-        e = hipMemcpy(p[6], gu_packed, gu_el / 2, hipMemcpyHostToDevice);
-    if (e == hipSuccess && (e = dalloc(dn_el / 2, &p[7])) == hipSuccess)
-        e = hipMemcpy(p[7], dn_packed, dn_el / 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = upload(gu_bias, (size_t)E * 2 * I * 4, &p[4]);
+    if (e == hipSuccess) e = upload(dn_bias, (size_t)E * H * 4, &p[5]);
     if (e != hipSuccess) {
         for (void *q : m->allocs) hipFree(q);
         delete m;
@@ -373,13 +363,11 @@ int nnq_moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, co
     m->d.H = H;
     m->d.I = I;
     m->d.gu_q = (const uint8_t *)p[0];
-    m->d.dn_q = (const uint8_t *)p[1];
-    m->d.gu_s = (const uint8_t *)p[2];
+    m->d.gu_s = (const uint8_t *)p[1];
+    m->d.dn_q = (const uint8_t *)p[2];
     m->d.dn_s = (const uint8_t *)p[3];
     m->d.gu_b = (const float *)p[4];
     m->d.dn_b = (const float *)p[5];
-    m->d.gu_raw_q = (const uint8_t *)p[6];
-    m->d.dn_raw_q = (const uint8_t *)p[7];
     *out = m;
     return NNQ_OK;
 }
@@ -400,9 +388,14 @@ int nnq_moe_forward(const nnq_moe *m, const void *x, nnq_dtype x_dtype, int64_t 
     if (x_dtype != NNQ_F32 && x_dtype != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d", (int)x_dtype);
     if (tokens == 0) return NNQ_OK;
     if (!x || !router_logits || !y) return fail(NNQ_ERR_INVALID_ARGUMENT, "null pointer");
-    if (m->d.E > 256) return fail(NNQ_ERR_UNSUPPORTED, "at most 256 experts");
+    if ((uintptr_t)x & 15) return fail(NNQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if (tokens * top_k > 16384)
+        return fail(NNQ_ERR_UNSUPPORTED, "at most 16384 token-expert assignments per call (%lld)",
+                    (long long)(tokens * top_k));
     Scratch s;
-    HIP_TRY(s.alloc(moe_scratch_bytes(tokens, m->d.E, m->d.H, m->d.I, top_k), (hipStream_t)stream), "scratch alloc");
+    HIP_TRY(s.alloc(moe_scratch_bytes(tokens, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16),
+                    (hipStream_t)stream),
+            "scratch alloc");
     int e = launch_moe(m->d, x, x_dtype == NNQ_BF16, tokens, router_logits, top_k, swiglu_limit, y, topk_idx, topk_w,
                        s.p, stream);
     if (e) return hip_fail((hipError_t)e, "moe launch");

@@ -73,7 +73,8 @@ int launch_argmax_reduce(const float *v, int64_t n, uint32_t *idx, int32_t *stat
 int launch_argmax_final(const unsigned long long *partial, int64_t count, uint32_t *idx, int32_t *status,
                         void *stream);
 
-// GEMM (prefill) for Q4_K: x bf16/f32 [m, k] -> y [m, n]
+// GEMM (prefill) for Q4_K: x bf16/f32 [m, k] -> y [m, n].  `scratch` holds the
+// staged activation (gemm_scratch_bytes(m, k, x_bf16) bytes, 256-byte aligned).
 struct GemmArgs {
     const uint8_t *qs;
     const uint8_t *hdr;
@@ -84,29 +85,32 @@ struct GemmArgs {
     int y_bf16;
     int64_t n, k, m;
     int64_t ntile, nblk;
-    uint16_t *xs;      // scratch: x converted to f16 * 2^s_row [m, k]
-    float *rowscale;   // scratch: per-row 2^-s factors [m]
-    float *xsum;       // scratch: per-row sums over 32-element sub-blocks [m, k/32]
+    void *scratch;
 };
 int launch_gemm_q4k(const GemmArgs &a, void *stream);
-size_t gemm_scratch_bytes(int64_t m, int64_t k);
+size_t gemm_scratch_bytes(int64_t m, int64_t k, int x_bf16);
 
-// MoE (GPT-OSS MXFP4)
+// MoE (GPT-OSS MXFP4).  Expert weights [E][K][N] with 32-element blocks along N
+// (Mxfp4Tensor of the flat tensor) are repacked per (expert, 32-column block nb,
+// 32-row block kb): codes [E][N/32][K/32][512] (lane l = 16p + c holds the 8 bytes
+// of rows 32kb + 8p .. 8p + 7 at byte column c, i.e. columns 2c (high nibble) and
+// 2c + 1 (low nibble)) and scales [E][N/32][K/32][32] (rows 32kb .. 32kb + 31).  A
+// bijection on the bytes.
 struct MoeDev {
     int64_t E, H, I;
-    const uint8_t *gu_q;    // repacked gate_up codes
+    const uint8_t *gu_q;    // gate_up codes, K = H, N = 2I
     const uint8_t *gu_s;    // gate_up scales
     const float *gu_b;      // [E, 2I]
-    const uint8_t *dn_q;
+    const uint8_t *dn_q;    // down codes, K = I, N = H
     const uint8_t *dn_s;
     const float *dn_b;      // [E, H]
-    const uint8_t *gu_raw_q;  // original packed bytes (for bit-exact dequant)
-    const uint8_t *dn_raw_q;
 };
-size_t moe_scratch_bytes(int64_t T, int64_t E, int64_t H, int64_t I, int top_k);
+size_t moe_scratch_bytes(int64_t T, int64_t E, int64_t H, int64_t I, int top_k, int x_bf16);
 int launch_moe(const MoeDev &m, const void *x, int x_bf16, int64_t T, const float *logits, int top_k, float limit,
                float *y, uint32_t *topk_idx, float *topk_w, void *scratch, void *stream);
 int launch_moe_dequant(const MoeDev &m, int64_t e, float *gate_up, float *down, void *stream);
-void moe_repack(const uint8_t *packed, int64_t E, int64_t K, int64_t N, uint8_t *dst);
+// host repack of one weight (codes and scales of E experts, K rows, N columns)
+void moe_repack(const uint8_t *packed, const uint8_t *scales, int64_t E, int64_t K, int64_t N, uint8_t *dst_codes,
+                uint8_t *dst_scales);
 
 }  // namespace nnq

@@ -220,3 +220,31 @@ void repack_q6k(const uint8_t *src, const Layout &L, uint8_t *dst) {
 }
 
 }  // namespace nnq
+
+namespace nnq {
+
+// GPT-OSS MXFP4 expert weights (Mxfp4Tensor of the flat [E][K][N] tensor,
+// crates/nn-gptoss/src/quantize.rs:122-163: byte p of a 32-element block holds
+// element 2p in the high nibble and 2p + 1 in the low nibble, one E8M0 scale per
+// block) -> per (expert, 32-column block, 32-row block) fragments whose bytes each
+// lane of a 16x16x32 MFMA wave needs; see MoeDev.
+void moe_repack(const uint8_t *packed, const uint8_t *scales, int64_t E, int64_t K, int64_t N, uint8_t *dc,
+                uint8_t *ds) {
+    const int64_t NB = N / 32, KB = K / 32;
+    for (int64_t e = 0; e < E; e++)
+        for (int64_t nb = 0; nb < NB; nb++)
+            for (int64_t kb = 0; kb < KB; kb++) {
+                const int64_t frag = (e * NB + nb) * KB + kb;
+                uint8_t *c = dc + frag * 512;
+                for (int p = 0; p < 4; p++)
+                    for (int col = 0; col < 16; col++)
+                        for (int i = 0; i < 8; i++) {
+                            const int64_t row = kb * 32 + 8 * p + i;
+                            c[(16 * p + col) * 8 + i] = packed[(e * K + row) * (N / 2) + nb * 16 + col];
+                        }
+                uint8_t *s = ds + frag * 32;
+                for (int r = 0; r < 32; r++) s[r] = scales[(e * K + kb * 32 + r) * NB + nb];
+            }
+}
+
+}  // namespace nnq

@@ -1,0 +1,109 @@
+"""GPU parity for the Q4_K prefill GEMM (m > 8 tokens).
+
+The HIP GEMM runs through the C ABI (nn_amd -> libnnq.so) and is compared with the
+CPU oracle on the same bytes and activations (tolerances as in test_gpu_linear):
+normwise and elementwise max relative error <= 1e-3 (near-zero skip at 1% of the
+peak), per-row cosine >= 0.99999.  Small shapes use the oracle's own f32 path
+(QLinear::forward restated: full dequant + x @ W^T); the BASELINE shapes use the
+oracle's bit-exact dequant followed by an f64 matmul (numpy), which is the exact
+product the f32 reference approximates.
+"""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_linear import check_close, make_weight, rand_bytes
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def dev():
+    import nn_amd
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    nn_amd.init(0)
+    return torch.device("cuda:0")
+
+
+def q4k_bytes(n, k, seed):
+    import nn_amd
+    return nn_amd.quantize_q4_k(nn_amd.synth_normal(seed, 1, (n, k), 0.02))
+
+
+def ref_f64(O, wb, n, k, x, legacy=False):
+    w = (O.dequant_q4_k_legacy if legacy else O.dequant_q4_k)(wb, n * k).reshape(n, k)
+    return (np.asarray(x, np.float64) @ w.astype(np.float64).T).astype(np.float32)
+
+
+@pytest.mark.parametrize("m", [9, 33, 100])
+@pytest.mark.parametrize("n,k", [(48, 256), (200, 1024), (64, 2048)])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_gemm_small_vs_oracle(O, dev, m, n, k, xdt):
+    import nn_amd
+    wb = q4k_bytes(n, k, seed=31 + n + k)
+    w = make_weight("q4_k", wb, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(5 + m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    y = nn_amd.quantized_linear(x, w).cpu().numpy()
+    ref = O.q4k_linear(x.float().cpu().numpy(), wb, n)
+    check_close(ref, y, f"gemm m={m} n={n} k={k} x={xdt}")
+
+
+def test_gemm_legacy_random_blocks(O, dev):
+    """nn-gguf layout with random block bytes (arbitrary finite d / dmin / scales)."""
+    import nn_amd
+    m, n, k = 40, 96, 1024
+    b = rand_bytes("q4_k", n, k, seed=77)
+    w = make_weight("q4_k_legacy", b, n, k)
+    x = nn_amd.synth_normal(77, 2, (m, k), 1.0)
+    y = nn_amd.quantized_linear(torch.from_numpy(x).to(dev), w).cpu().numpy()
+    check_close(ref_f64(O, b, n, k, x, legacy=True), y, "gemm legacy random")
+
+
+def test_gemm_zero_d_blocks(O, dev):
+    """Super-blocks with d = 0 (only the min term survives) inside a row."""
+    import nn_amd
+    m, n, k = 24, 32, 1024
+    b = q4k_bytes(n, k, seed=3).reshape(-1, 144).copy()
+    b[::3, 0:2] = 0  # d = +0.0 for every third super-block
+    b = b.ravel()
+    w = make_weight("q4_k", b, n, k)
+    x = nn_amd.synth_normal(3, 2, (m, k), 1.0)
+    y = nn_amd.quantized_linear(torch.from_numpy(x).to(dev), w).cpu().numpy()
+    check_close(ref_f64(O, b, n, k, x), y, "gemm zero-d blocks")
+
+
+def test_gemm_bias_bf16_out_and_nan_row(O, dev):
+    import nn_amd
+    m, n, k = 64, 160, 2048
+    wb = q4k_bytes(n, k, seed=11)
+    w = make_weight("q4_k", wb, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(11, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    bias = torch.from_numpy(nn_amd.synth_normal(11, 3, (n,), 0.5)).to(dev)
+    y32 = nn_amd.quantized_linear(x, w, bias)
+    yb = nn_amd.quantized_linear(x, w, bias, out_dtype=torch.bfloat16)
+    ref = ref_f64(O, wb, n, k, x.float().cpu().numpy()) + bias.cpu().numpy()
+    check_close(ref, y32.cpu().numpy(), "gemm bias")
+    ref_b = torch.from_numpy(ref).to(torch.bfloat16).float().numpy()
+    got_b = yb.float().cpu().numpy()
+    assert np.all(np.abs(got_b - ref_b) <= np.abs(ref_b) * 2.0 ** -7 + 1e-30)
+    x[5, 100] = float("nan")
+    yn = nn_amd.quantized_linear(x, w).cpu().numpy()
+    assert np.isnan(yn[5]).all() and np.isfinite(np.delete(yn, 5, axis=0)).all()
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 4096, 4096), (512, 12288, 4096), (512, 4096, 12288), (16, 4096, 12288),
+                                   (64, 12288, 4096)])
+def test_gemm_baseline_shapes(O, dev, m, n, k):
+    """Config 4: Qwen3-8B MLP prefill shapes, bf16 activations, bf16 and f32 outputs."""
+    import nn_amd
+    wb = q4k_bytes(n, k, seed=4000 + k)
+    w = make_weight("q4_k", wb, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(4000 + m, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    y = nn_amd.quantized_linear(x, w).cpu().numpy()
+    ref = ref_f64(O, wb, n, k, x.float().cpu().numpy())
+    check_close(ref, y, f"gemm {m}x{n}x{k}")
+    yb = nn_amd.quantized_linear(x, w, out_dtype=torch.bfloat16).float().cpu().numpy()
+    ref_b = torch.from_numpy(y).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(yb, ref_b), "bf16 output must be the f32 result rounded once"

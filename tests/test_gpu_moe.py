@@ -1,0 +1,139 @@
+"""GPU parity for the GPT-OSS MXFP4 mixture-of-experts layer.
+
+The device pipeline (route -> permute -> gate_up + SwiGLU -> down -> combine) runs
+through the C ABI and is compared with the CPU oracle's restatement of
+QuantizedDecoderLayer::moe_forward (crates/nn-gptoss/src/quantized_model.rs:99-194):
+  * routing: the top-k expert sets equal per token, weights within 1e-6;
+  * expert decode: bit-exact with Mxfp4Tensor::dequantize;
+  * outputs: normwise and elementwise max relative error <= 1e-3 (near-zero skip at
+    1% of the peak) and per-row cosine >= 0.99999.
+Small layers use the oracle's own f32 forward; the BASELINE layer (config 5) uses
+the oracle's routing and bit-exact decode with the expert math in f64.
+"""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_linear import check_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def dev():
+    import nn_amd
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    nn_amd.init(0)
+    return torch.device("cuda:0")
+
+
+def make_layer(E, H, I, seed):
+    import nn_amd
+    wgu = nn_amd.synth_normal(seed, 1, (E, H, 2 * I), 0.02)
+    wdn = nn_amd.synth_normal(seed, 2, (E, I, H), 0.02)
+    gp, gs = nn_amd.quantize_mxfp4(wgu)
+    dp, ds = nn_amd.quantize_mxfp4(wdn)
+    gb = nn_amd.synth_normal(seed, 3, (E, 2 * I), 0.02)
+    db = nn_amd.synth_normal(seed, 4, (E, H), 0.02)
+    return dict(gp=gp, gs=gs, gb=gb, dp=dp, ds=ds, db=db)
+
+
+def upload(L, E, H, I):
+    import nn_amd
+    return nn_amd.QuantizedMoE(E, H, I, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"])
+
+
+def ref_f64(O, x, logits, k, L, E, H, I, limit=7.0):
+    """moe_forward with the oracle's routing and decode, expert math in f64."""
+    probs = O.softmax_rows(logits)
+    tw, ti = O.topk_rows(probs, k)
+    tw = (tw / tw.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    out = np.zeros((x.shape[0], H), np.float64)
+    gper, dper = H * 2 * I, I * H
+    for e in range(E):
+        rows = [(t, s) for t in range(x.shape[0]) for s in range(k) if ti[t, s] == e]
+        if not rows:
+            continue
+        toks = np.array([t for t, _ in rows])
+        w = np.array([tw[t, s] for t, s in rows], np.float64)
+        Wg = O.mxfp4_dequantize(L["gp"][e * gper // 2:(e + 1) * gper // 2], L["gs"][e * gper // 32:(e + 1) * gper // 32],
+                                gper).reshape(H, 2 * I).astype(np.float64)
+        Wd = O.mxfp4_dequantize(L["dp"][e * dper // 2:(e + 1) * dper // 2], L["ds"][e * dper // 32:(e + 1) * dper // 32],
+                                dper).reshape(I, H).astype(np.float64)
+        gu = x[toks].astype(np.float64) @ Wg + L["gb"][e].astype(np.float64)
+        g, u = gu[:, :I], gu[:, I:]
+        h = np.clip(g / (1.0 + np.exp(-g)), -limit, limit) * u
+        y = h @ Wd + L["db"][e].astype(np.float64)
+        out[toks] += w[:, None] * y
+    return out.astype(np.float32), ti, tw
+
+
+@pytest.mark.parametrize("E,H,I,T,k,xdt", [(4, 64, 64, 24, 2, "f32"), (8, 256, 320, 64, 4, "bf16"),
+                                          (8, 256, 320, 64, 4, "f32"), (6, 128, 96, 40, 3, "bf16"),
+                                          (16, 96, 64, 150, 4, "bf16")])
+def test_moe_small_vs_oracle(O, dev, E, H, I, T, k, xdt):
+    import nn_amd
+    L = make_layer(E, H, I, seed=E * 7 + H)
+    moe = upload(L, E, H, I)
+    x = torch.from_numpy(nn_amd.synth_normal(9, 5, (T, H), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    logits = torch.from_numpy(nn_amd.synth_normal(9, 6, (T, E), 1.0)).to(dev)
+    y, ti, tw = moe.forward(x, logits, top_k=k, return_routing=True)
+    xf = x.float().cpu().numpy()
+    ref, rti, rtw = O.moe_forward(xf, logits.cpu().numpy(), k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    gti = ti.cpu().numpy().astype(np.uint32)
+    assert np.array_equal(np.sort(gti, axis=1), np.sort(rti, axis=1)), "routing expert sets differ"
+    assert np.array_equal(gti, rti), "routing order differs"
+    assert np.allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    check_close(ref, y.cpu().numpy(), f"moe E={E} H={H} I={I} T={T} k={k} x={xdt}")
+
+
+def test_moe_expert_dequant_bit_exact(O, dev):
+    E, H, I = 3, 96, 64
+    L = make_layer(E, H, I, seed=5)
+    moe = upload(L, E, H, I)
+    gper, dper = H * 2 * I, I * H
+    for e in range(E):
+        gu, dn = moe.dequant_expert(e)
+        rg = O.mxfp4_dequantize(L["gp"][e * gper // 2:(e + 1) * gper // 2], L["gs"][e * gper // 32:(e + 1) * gper // 32],
+                                gper).reshape(H, 2 * I)
+        rd = O.mxfp4_dequantize(L["dp"][e * dper // 2:(e + 1) * dper // 2], L["ds"][e * dper // 32:(e + 1) * dper // 32],
+                                dper).reshape(I, H)
+        assert np.array_equal(gu.cpu().numpy().view(np.uint32), rg.view(np.uint32))
+        assert np.array_equal(dn.cpu().numpy().view(np.uint32), rd.view(np.uint32))
+
+
+def test_moe_dequant_extreme_scales(O, dev):
+    """E8M0 bytes 0, 1, 127, 200 and every fp4 code decode exactly (byte 0 -> 2^-126)."""
+    import nn_amd
+    E, H, I = 1, 32, 32
+    gp = np.arange(H * 2 * I // 2, dtype=np.uint32).astype(np.uint8)
+    gs = np.array([0, 1, 127, 200] * (H * 2 * I // 32 // 4), np.uint8)
+    dp = (np.arange(I * H // 2, dtype=np.uint32) * 7).astype(np.uint8)
+    ds = np.array([126, 0, 128, 1] * (I * H // 32 // 4), np.uint8)
+    moe = nn_amd.QuantizedMoE(E, H, I, gp, gs, np.zeros((E, 2 * I), np.float32), dp, ds,
+                              np.zeros((E, H), np.float32))
+    gu, dn = moe.dequant_expert(0)
+    rg = O.mxfp4_dequantize(gp, gs, H * 2 * I).reshape(H, 2 * I)
+    rd = O.mxfp4_dequantize(dp, ds, I * H).reshape(I, H)
+    assert np.array_equal(gu.cpu().numpy().view(np.uint32), rg.view(np.uint32))
+    assert np.array_equal(dn.cpu().numpy().view(np.uint32), rd.view(np.uint32))
+    assert (rg != 0).any() and (np.abs(rg[rg != 0]) < 1e-37).any(), "the case covers subnormal decodes"
+
+
+def test_moe_baseline_config(O, dev):
+    """Config 5: 32 experts, hidden = intermediate = 2880, top-4, 256 bf16 tokens."""
+    import nn_amd
+    E, H, I, T, k = 32, 2880, 2880, 256, 4
+    L = make_layer(E, H, I, seed=20)
+    moe = upload(L, E, H, I)
+    x = torch.from_numpy(nn_amd.synth_normal(20, 5, (T, H), 1.0)).to(dev).to(torch.bfloat16)
+    logits = torch.from_numpy(nn_amd.synth_normal(20, 6, (T, E), 1.0)).to(dev)
+    y, ti, tw = moe.forward(x, logits, top_k=k, return_routing=True)
+    ref, rti, rtw = ref_f64(O, x.float().cpu().numpy(), logits.cpu().numpy(), k, L, E, H, I)
+    assert np.array_equal(ti.cpu().numpy().astype(np.uint32), rti)
+    assert np.allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    counts = np.bincount(rti.ravel(), minlength=E)
+    print(f"expert loads min {counts.min()} max {counts.max()}")
+    check_close(ref, y.cpu().numpy(), "moe config 5")
