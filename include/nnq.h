@@ -154,6 +154,9 @@ int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const floa
  *           (packed bytes E*hidden*2*inter/2, scales E*hidden*2*inter/32),
  *  down:    Mxfp4Tensor of the flat [E, inter, hidden] tensor,
  *  biases:  f32 [E, 2*inter] and [E, hidden] (host).
+ * hidden and inter must be multiples of 32 (NNQ_ERR_INVALID_SHAPE), at most 256
+ * experts.  The codes are repacked on upload into per-(expert, 32-column block,
+ * 32-row block) fragments in MFMA lane order (a permutation of the bytes).
  * Replaces QuantizedDecoderLayer::load's expert tensors
  * (crates/nn-gptoss/src/quantized_model.rs:70-78). */
 int nnq_moe_create(int64_t num_experts, int64_t hidden, int64_t inter, const uint8_t *gu_packed,
@@ -164,8 +167,10 @@ int nnq_moe_destroy(nnq_moe *moe);
 
 /* y[t, hidden] (f32) = MoE(x[t, hidden]) with router logits [t, E] (f32):
  * softmax -> top_k -> renormalise -> per expert clamp(silu(x@Wg+bg), -limit, limit)
- * * (x@Wu+bu) -> @Wd + bd -> weighted sum.  x: NNQ_F32 or NNQ_BF16.  Routing,
- * permutation and combine run on the device (no host synchronisation).
+ * * (x@Wu+bu) -> @Wd + bd -> weighted sum.  x: NNQ_F32 or NNQ_BF16, 16-byte aligned;
+ * tokens * top_k <= 16384, top_k <= 8.  Routing, permutation and combine run on the
+ * device (no host synchronisation); the expert outputs are summed per token in
+ * ascending expert order, as moe_forward's index_add does.
  * Optional outputs topk_idx [t, top_k] u32 and topk_w [t, top_k] f32 (device).
  * Replaces QuantizedDecoderLayer::moe_forward / expert_forward
  * (crates/nn-gptoss/src/quantized_model.rs:99-194). */

@@ -480,3 +480,34 @@ def test_moe_matches_f64_bruteforce(O):
                   db.reshape(E, H), I, 7.0)
     assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
     assert np.allclose(tw.sum(1), 1.0, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------------
+# build-defined input generators (no reference encoder exists): round-trip bounds
+# ---------------------------------------------------------------------------------
+
+def test_q8_0_encoder_round_trip_bound(O):
+    """d = f16(amax / 127), q = round(v / d): every decoded value within d / 2 (+ the f16
+    rounding of d) of the input, and the block maximum maps to |q| = 127."""
+    rng = np.random.default_rng(11)
+    v = (rng.standard_normal(32 * 64) * 0.02).astype(np.float32)
+    b = O.quantize_q8_0(v)
+    dec = O.dequant_q8_0(b, v.size)
+    d = O.f16_bits_to_f32(b.reshape(-1, 34)[:, 0:2].copy().view(np.uint16).ravel())
+    err = np.abs(dec - v).reshape(-1, 32)
+    assert np.all(err <= d[:, None] * 0.5 + np.abs(v).reshape(-1, 32) * 2.0 ** -10 + 1e-12)
+    q = b.reshape(-1, 34)[:, 2:].view(np.int8)
+    assert np.all(np.abs(q).max(axis=1) >= 126)
+
+
+def test_q6_k_encoder_round_trip_bound(O):
+    """Decoded values within half a quantisation step (d * |sc|) of the input plus the
+    rounding of the f16 / int8 scales (a few percent of the block range)."""
+    rng = np.random.default_rng(12)
+    v = (rng.standard_normal(256 * 16) * 0.02).astype(np.float32)
+    b = O.quantize_q6_k(v)
+    dec = O.dequant_q6_k(b, v.size)
+    rng_blk = np.abs(v).reshape(-1, 256).max(axis=1)
+    err = np.abs(dec - v).reshape(-1, 256).max(axis=1)
+    assert np.all(err <= rng_blk * 0.05)
+    assert np.corrcoef(dec, v)[0, 1] > 0.999
