@@ -70,23 +70,28 @@ def make_copies(fmt_bytes, qt, n, k, min_bytes, layout=0):
     return [nn_amd.QuantizedWeight.from_quantized(fmt_bytes, qt, (n, k), layout=layout) for _ in range(copies)]
 
 
-def time_graph(fn_list, steps, warmup):
-    """Capture fn_list (one call each) into a HIP graph, replay it until `steps` calls
-    ran, and return seconds per call from events on the replay stream."""
+def time_graph(fn_list, steps, warmup, min_graph_calls=200):
+    """Capture rounds of fn_list (one call each per round, at least `min_graph_calls`
+    calls) into one HIP graph, replay it until about `steps` calls ran, and return
+    seconds per call from events on the replay stream.  Long graphs keep the
+    per-replay launch cost out of the per-call figure, as in a decode loop."""
     import torch
     for i in range(warmup):
         fn_list[i % len(fn_list)]()
     torch.cuda.synchronize()
+    rounds = max(1, -(-min_graph_calls // len(fn_list)))
+    per_graph = rounds * len(fn_list)
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
-            for fn in fn_list:
-                fn()
+            for _ in range(rounds):
+                for fn in fn_list:
+                    fn()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    reps = max(1, steps // len(fn_list))
+    reps = max(1, steps // per_graph)
     g.replay()
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -95,7 +100,7 @@ def time_graph(fn_list, steps, warmup):
         g.replay()
     en.record()
     torch.cuda.synchronize()
-    return st.elapsed_time(en) / 1e3 / (reps * len(fn_list)), reps * len(fn_list)
+    return st.elapsed_time(en) / 1e3 / (reps * per_graph), reps * per_graph
 
 
 # ---------------------------------------------------------------------------------
@@ -177,7 +182,7 @@ def bench_gemm(m, n, k, steps, warmup, min_bytes=256 << 20):
             check(L.nnq_linear(wi.handle, vp(x), 2, m, k, None, 0, vp(yi), 2, cur_stream()))
         return f
 
-    sec, nsteps = time_graph([launcher(c, y) for c, y in zip(copies, ys)], steps, warmup)
+    sec, nsteps = time_graph([launcher(c, y) for c, y in zip(copies, ys)], steps, warmup, min_graph_calls=20)
     flops = 2.0 * m * n * k
     return dict(sec=sec, steps=nsteps, tflops=flops / sec / 1e12, copies=len(copies))
 
@@ -205,7 +210,7 @@ def bench_moe(steps, warmup, seed=20):
         check(L.nnq_moe_forward(moe._h, vp(x), 2, T, vp(logits), K, ctypes.c_float(7.0), vp(y), None, None,
                                 cur_stream()))
 
-    sec, nsteps = time_graph([f], steps, warmup)
+    sec, nsteps = time_graph([f], steps, warmup, min_graph_calls=20)
     _, ti, _ = moe.forward(x, logits, top_k=K, return_routing=True)
     used = len(np.unique(ti.cpu().numpy()))
     per_expert = (H * 2 * I + I * H) * 17 // 32 + (2 * I + H) * 4  # MXFP4 codes + scales + biases

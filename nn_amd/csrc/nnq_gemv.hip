@@ -647,6 +647,265 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
+// Q4_K decode kernel (m <= 2).  Same division of work as gemv_wave_kernel (one
+// workgroup per 16-row tile, unit u of K to wave u % WAVES, all loads of a pass
+// issued up front), arranged so that almost nothing but the MFMA inputs goes
+// through LDS:
+//  * staging lane 16G + j holds elements 64G + 4j .. 64G + 4j + 3 of the unit, so
+//    sub-blocks 2G and 2G + 1 live in the same 16-lane row that consumes them in
+//    the MFMA epilogue (compute lane 16G + n, row n of the tile).  The per
+//    sub-block power-of-two scale and sum of x are reduced over each half-row with
+//    DPP and swapped between the two half-rows with one rotation; they stay in
+//    registers;
+//  * x * s is split into f16 hi + lo pairs by mixed-precision FMAs that write both
+//    halves of a register, so a pair costs two instructions;
+//  * the wave index is made scalar, so unit indices and base addresses are scalar;
+//  * the four lane groups are summed with the permlane swaps, and each lane folds
+//    its two accumulators (codes * 2^-24 sums, min terms) into one value first.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t mix_hi2(float a, float b, float s) {
+    uint32_t r;  // f16(a * s) | f16(b * s) << 16
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0\n\tv_fma_mixhi_f16 %0, %3, %2, 0" : "=&v"(r) : "v"(a), "v"(s), "v"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t mix_lo2(float a, float b, float s, uint32_t hi) {
+    uint32_t r;  // f16(a * s - hi.x) | f16(b * s - hi.y) << 16, each residual formed exactly by the FMA
+    asm("v_fma_mixlo_f16 %0, %1, %2, -%4 op_sel_hi:[0,0,1]\n\t"
+        "v_fma_mixhi_f16 %0, %3, %2, -%4 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+        : "=&v"(r)
+        : "v"(a), "v"(s), "v"(b), "v"(hi));
+    return r;
+}
+__device__ __forceinline__ float absmax4(float a, float b, float c, float d) {
+    float r;
+    asm("v_max3_f32 %0, |%1|, |%2|, |%3|\n\tv_max3_f32 %0, %0, |%4|, |%4|" : "=&v"(r) : "v"(a), "v"(b), "v"(c), "v"(d));
+    return r;
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t umax_dpp(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+    return v > o ? v : o;
+}
+template <int CTRL>
+__device__ __forceinline__ float add_dpp(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ float mov_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// sum over the four 16-lane rows (every lane receives the total of its column)
+__device__ __forceinline__ float sum_rows(float v) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+// Per-lane activation statistics of one token: 1/scale and sum of x for sub-blocks
+// 2G (lo) and 2G + 1 (hi) of the lane's row.
+struct XStat {
+    float b_lo, b_hi, xs_lo, xs_hi;
+};
+
+// Stage this lane's 4 activations (f32, or bf16 in raw[0..1]) of one token into
+// the hi / lo f16 planes of the wave's unit buffer.
+template <bool XB>
+__device__ __forceinline__ void stage_q4k(const u32x4 &raw, uint16_t *hi_plane, uint16_t *lo_plane, XStat &st) {
+    const int lane = threadIdx.x & 63;
+    float v0, v1, v2, v3;
+    if (XB) {
+        v0 = __uint_as_float(raw[0] << 16);
+        v1 = __uint_as_float(raw[0] & 0xFFFF0000u);
+        v2 = __uint_as_float(raw[1] << 16);
+        v3 = __uint_as_float(raw[1] & 0xFFFF0000u);
+    } else {
+        v0 = __uint_as_float(raw[0]);
+        v1 = __uint_as_float(raw[1]);
+        v2 = __uint_as_float(raw[2]);
+        v3 = __uint_as_float(raw[3]);
+    }
+    // max |x| of the lane's 32-element sub-block (8 lanes), compared as bit patterns
+    uint32_t m = __float_as_uint(absmax4(v0, v1, v2, v3));
+    m = umax_dpp<0xB1>(m);   // lane ^ 1
+    m = umax_dpp<0x4E>(m);   // lane ^ 2
+    m = umax_dpp<0x141>(m);  // row_half_mirror: the other quad of the 8
+    // s = 2^(14 - e) (e = unbiased exponent of the max) capped at 2^126, so max * s
+    // lies in [2^14, 2^15); back = 1/s, a normal f32 for every input.  A NaN or inf
+    // max gives a finite s and the non-finite value propagates through the products.
+    const uint32_t sb = min(0x86000000u - (m & 0x7F800000u), 0x7E800000u);
+    const float s = __uint_as_float(sb);
+    const uint32_t h01 = mix_hi2(v0, v1, s), h23 = mix_hi2(v2, v3, s);
+    const uint32_t l01 = mix_lo2(v0, v1, s, h01), l23 = mix_lo2(v2, v3, s, h23);
+    *reinterpret_cast<u32x2 *>(hi_plane + 4 * lane) = u32x2{h01, h23};
+    *reinterpret_cast<u32x2 *>(lo_plane + 4 * lane) = u32x2{l01, l23};
+    float sum = (v0 + v1) + (v2 + v3);
+    sum = add_dpp<0xB1>(sum);
+    sum = add_dpp<0x4E>(sum);
+    sum = add_dpp<0x141>(sum);
+    const float back = __uint_as_float(0x7F000000u - sb);
+    const float back_o = mov_dpp<0x128>(back), sum_o = mov_dpp<0x128>(sum);  // row_ror:8, the other half-row
+    const bool first = (lane & 8) == 0;
+    st.b_lo = first ? back : back_o;
+    st.b_hi = first ? back_o : back;
+    st.xs_lo = first ? sum : sum_o;
+    st.xs_hi = first ? sum_o : sum;
+}
+
+template <int WAVES, int UPW, int R, bool XB, int MT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile0 = (int)blockIdx.x * R;  // this workgroup's tiles: tile0 .. tile0 + R - 1
+    // per wave: two unit buffers [token, hi/lo][256] f16, each followed by 64 zero
+    // halves that the A operand of the rows without data reads
+    constexpr int kBuf = MT * 512 + 64;
+    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][2][kBuf];
+    __shared__ float red[WAVES][R * MT][16];
+    if (lane < 16)  // the wave's own pads, read later only by lanes of this wave
+        *reinterpret_cast<u32x4 *>(&xbuf[wv][lane >> 3][MT * 512 + 8 * (lane & 7)]) = u32x4{0u, 0u, 0u, 0u};
+
+    // A-operand rows of lane group G: 4G + 2t + part (token t, hi / lo part) over the
+    // k-group of sub-block 2G (low nibbles) or 2G + 1 (high nibbles); other rows zero.
+    const int G = lane >> 4, n = lane & 15, i = n & 3;
+    const bool own = G == (n >> 2) && (i >> 1) < MT;
+    const int aoff = own ? ((i >> 1) * 2 + (i & 1)) * 256 + 64 * G : MT * 512;
+
+    const int units = (int)a.nblk, k = (int)a.k, ntile = (int)a.ntile;
+    const uint8_t *qbase[R], *hbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int tile = min(tile0 + r, ntile - 1);  // a tail tile re-reads the last one
+        qbase[r] = a.qs + (size_t)tile * units * 2048 + 16 * lane;
+        hbase[r] = a.hdr + (size_t)tile * units * 256 + 16 * n;
+    }
+    constexpr int xe = XB ? 2 : 4;
+    const uint8_t *xbase = reinterpret_cast<const uint8_t *>(a.x) + 4 * lane * xe;
+    float acc1[R][MT], acc2[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) acc1[r][t] = acc2[r][t] = 0.f;
+    int ub0 = 0;
+    do {  // passes over K (units >= 1: the host checks k >= 256)
+        // activation slices first (L2 hits), then the weights of every unit of the pass
+        u32x4 xr[UPW][MT];
+        UnitQ4K w[UPW][R];
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            const uint32_t u = (uint32_t)min(ub0 + wv + j * WAVES, units - 1);
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const uint8_t *p = xbase + (uint32_t)(t * k + (int)u * 256) * (uint32_t)xe;
+                if (XB) {
+                    const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+                    xr[j][t] = u32x4{w2[0], w2[1], 0u, 0u};
+                } else {
+                    xr[j][t] = *reinterpret_cast<const u32x4 *>(p);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep this issue order
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            const uint32_t u = (uint32_t)min(ub0 + wv + j * WAVES, units - 1);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                w[j][r].q0 = ldg128(qbase[r] + u * 2048u);
+                w[j][r].q1 = ldg128(qbase[r] + u * 2048u + 1024u);
+                w[j][r].h = ldg128(hbase[r] + u * 256u);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
+            uint16_t *buf = xbuf[wv][j & 1];
+            XStat st[MT];
+#pragma unroll
+            for (int t = 0; t < MT; t++) stage_q4k<XB>(xr[j][t], buf + 512 * t, buf + 512 * t + 256, st[t]);
+            // the wave's own LDS writes are read back by other lanes of the same wave
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const uint16_t *ap = buf + aoff;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K
+                // packing, get_scale_min_k4, crates/nn-core/src/layers/quantized/linear.rs:166-176)
+                const u32x4 &h = w[j][r].h;
+                const float d = f16_to_f32(h[0] & 0xFFFFu), dmin = f16_to_f32(h[0] >> 16);
+                const uint32_t S1 = h[1], S2 = h[2], S3 = h[3];
+                const uint32_t hsel = 0u - (uint32_t)(G >> 1);  // all ones for sub-blocks 4..7
+                const uint32_t scw =
+                    ((S1 & 0x3F3F3F3Fu) & ~hsel) | (((S3 & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) & hsel);
+                const uint32_t mnw =
+                    ((S2 & 0x3F3F3F3Fu) & ~hsel) | ((((S3 >> 4) & 0x0F0F0F0Fu) | ((S2 >> 2) & 0x30303030u)) & hsel);
+                const uint32_t scp = scw >> (16 * (G & 1)), mnp = mnw >> (16 * (G & 1));
+                const float sc_lo = (float)(scp & 0xFFu), sc_hi = 0.0625f * (float)((scp >> 8) & 0xFFu);
+                const float mn_lo = (float)(mnp & 0xFFu), mn_hi = (float)((mnp >> 8) & 0xFFu);
+
+                floatx4 clo = {0.f, 0.f, 0.f, 0.f}, chi = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {
+                    const u32x4 q = q4 < 2 ? w[j][r].q0 : w[j][r].q1;
+                    const uint32_t w0 = q[2 * (q4 & 1)], w1 = q[2 * (q4 & 1) + 1];
+                    const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
+                    const u32x4 blo = {w0 & 0x000F000Fu, w0s & 0x000F000Fu, w1 & 0x000F000Fu, w1s & 0x000F000Fu};
+                    const u32x4 bhi = {w0 & 0x00F000F0u, w0s & 0x00F000F0u, w1 & 0x00F000F0u, w1s & 0x00F000F0u};
+                    clo = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap + 8 * q4), blo, clo);
+                    chi = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap + 32 + 8 * q4), bhi, chi);
+                }
+                // lane 16G + n now holds, for row n and sub-blocks 2G / 2G + 1, the
+                // (hi, lo) partial dot products of token 0 (entries 0, 1) and token 1 (2, 3)
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const float T = (sc_lo * st[t].b_lo) * (clo[2 * t] + clo[2 * t + 1]) +
+                                    (sc_hi * st[t].b_hi) * (chi[2 * t] + chi[2 * t + 1]);
+                    acc1[r][t] += d * T;
+                    acc2[r][t] += dmin * (mn_lo * st[t].xs_lo + mn_hi * st[t].xs_hi);
+                }
+            }
+        }
+        ub0 += WAVES * UPW;
+    } while (ub0 < units);
+
+    // y = 2^24 * (code sums) - (min terms), summed over the lane groups, then the waves
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const float v = sum_rows(acc1[r][t] * 16777216.0f - acc2[r][t]);
+            if (lane < 16) red[wv][r * MT + t][lane] = v;
+        }
+    __syncthreads();
+    if (tid < R * MT * 16) {
+        const int rt = tid >> 4, nn = tid & 15, t = rt % MT;
+        const int64_t tile = tile0 + rt / MT;  // rows of a tail tile fail row < n
+        float y = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; w2++) y += red[w2][rt][nn];
+        const int64_t row = tile * 16 + nn;
+        if (row < a.n) {
+            if (a.bias) y += a.bias[row];
+            if (a.y_bf16)
+                reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+            else
+                reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+        }
+        if (a.argmax_partial && t == 0) {
+            // first-index argmax of this tile's 16 logits (the 16 lanes hold one tile)
+            uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
+            for (int o = 8; o > 0; o >>= 1) {
+                uint64_t other = __shfl_xor(key, o, 16);
+                key = other > key ? other : key;
+            }
+            if (nn == 0 && tile < a.ntile) a.argmax_partial[tile] = key;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Bit-exact dequantization from the device layout (the parity gate for decode).
 // One wave per (tile, unit); lane l = 16p + n decodes its bytes for row n.
 // ---------------------------------------------------------------------------------
@@ -874,12 +1133,43 @@ static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
     return (int)hipErrorInvalidValue;
 }
 
+template <int WAVES, int UPW, int R, bool XB>
+static int launch_q4k_decode_x(const GemvArgs &a, void *stream) {
+    const dim3 grid((unsigned)((a.ntile + R - 1) / R));
+    if (a.m == 1)
+        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, R, XB, 1>), grid, dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, R, XB, 2>), grid, dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+template <int WAVES, int UPW, int R>
+static int launch_q4k_decode_t(const GemvArgs &a, void *stream) {
+    return a.x_bf16 ? launch_q4k_decode_x<WAVES, UPW, R, true>(a, stream)
+                    : launch_q4k_decode_x<WAVES, UPW, R, false>(a, stream);
+}
+
+// Q4_K decode shapes, from sweeps on MI355X: K of up to 16 units takes 8 waves of
+// up to 2 units, longer K 16 waves of up to 4 units (then passes); one tile per
+// workgroup (two tiles per workgroup, sharing the staged activation, measured slower).
+static int launch_q4k_decode(const GemvArgs &a, void *stream) {
+    const int64_t units = a.nblk;
+    if (units <= 4) return launch_q4k_decode_t<4, 1, 1>(a, stream);
+    if (units <= 8) return launch_q4k_decode_t<8, 1, 1>(a, stream);
+    if (units <= 16) return launch_q4k_decode_t<8, 2, 1>(a, stream);
+    const int64_t need = (units + 15) / 16;
+    if (need <= 2) return launch_q4k_decode_t<16, 2, 1>(a, stream);
+    if (need <= 3) return launch_q4k_decode_t<16, 3, 1>(a, stream);
+    return launch_q4k_decode_t<16, 4, 1>(a, stream);
+}
+
 int launch_gemv(int fmt, const GemvArgs &a, void *stream) {
     if (a.m < 1 || a.m > 8 || (fmt == FQ6K && a.m > 4)) return (int)hipErrorInvalidValue;
     const int64_t units = fmt == FQ80 ? a.nblk / 8 : a.nblk;
     if (a.m <= 2) {
         switch (fmt) {
-        case FQ4K: return launch_wave<FQ4K>(a, units, stream);
+        case FQ4K: return launch_q4k_decode(a, stream);
         case FQ80: return launch_wave<FQ80>(a, units, stream);
         case FQ6K: return launch_wave<FQ6K>(a, units, stream);
         }

@@ -135,6 +135,23 @@ def test_linear_small(O, dev, fmt, n, k, m):
     check_close(ref, y, f"{fmt} n={n} k={k} m={m}")
 
 
+@pytest.mark.parametrize("k", [1536, 2560, 6144, 16384, 20480])
+@pytest.mark.parametrize("m,xdt", [(1, "f32"), (2, "f32"), (1, "bf16"), (2, "bf16")])
+def test_q4k_decode_launch_shapes(O, dev, k, m, xdt):
+    """Every decode launch shape: K of 6, 10, 24, 64 and 80 units (one wave with a
+    partial second unit, one and two passes), a 37-row tail tile, f32 and bf16 x."""
+    import nn_amd
+    n = 37
+    b = quantized_weight_bytes("q4_k", n, k, seed=77 + k, O=O)
+    w = make_weight("q4_k", b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(11 + m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    y = nn_amd.quantized_linear(x, w).cpu().numpy()
+    ref = oracle_linear(O, "q4_k", b, n, k, x.float().cpu().numpy())
+    check_close(ref, y, f"q4_k decode n={n} k={k} m={m} x={xdt}")
+
+
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k"])
 def test_linear_bf16_in_out_bias(O, dev, fmt):
     import nn_amd
