@@ -23,7 +23,10 @@ ARCH = "gfx950"
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 
-HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_moe.hip"]
+HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_moe.hip"]
+# per-file device flags: the ring GEMM keeps its MFMA accumulators in VGPRs, where the
+# per-super-block rescale is one multiply per element
+EXTRA_FLAGS = {"nnq_gemm_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HOST_SOURCES = ["nnq_abi.cpp", "nnq_repack.cpp", "nnq_host.cpp"]
 
 
@@ -38,7 +41,8 @@ def _compile(src: str) -> str:
     path = os.path.join(CSRC, src)
     obj = os.path.join(BUILD, src + ".o")
     if src.endswith(".hip"):
-        cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, *DEVICE_FLAGS, "-c", path, "-o", obj]
+        cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, *DEVICE_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", path, "-o",
+               obj]
     else:
         # host-only C++ (HIP runtime API): no FMA contraction in the encoders
         cmd = [HIPCC, "-x", "c++", *COMMON, "-ffp-contract=off", f"-I{ROCM}/include", "-D__HIP_PLATFORM_AMD__",

@@ -150,6 +150,7 @@ int nnq_weight_create(nnq_format fmt, nnq_layout layout, const uint8_t *bytes, s
             size_t per_q = L.qs_bytes / L.ntile, per_h = L.hdr_bytes / L.ntile;
             S.qs_bytes = per_q * S.ntile;
             S.hdr_bytes = per_h * S.ntile;
+            S.aux_bytes = 0;
             std::vector<uint8_t> tmp(S.total());
             const uint8_t *src = bytes + (size_t)lo * kTile * (k / 256) * block_bytes(fmt);
             if (fmt == NNQ_FMT_Q4_K)
@@ -159,6 +160,10 @@ int nnq_weight_create(nnq_format fmt, nnq_layout layout, const uint8_t *bytes, s
             std::memcpy(host.data() + per_q * lo, tmp.data(), S.qs_bytes);
             std::memcpy(host.data() + L.qs_bytes + per_h * lo, tmp.data() + S.qs_bytes, S.hdr_bytes);
         });
+        if (fmt == NNQ_FMT_Q4_K)
+            parallel_for(L.ntile, [&](int64_t lo, int64_t hi) {
+                q4k_aux_plane(host.data() + L.qs_bytes, L, host.data() + L.qs_bytes + L.hdr_bytes, lo, hi);
+            });
         break;
     }
     case NNQ_FMT_Q8_0:
@@ -239,6 +244,7 @@ int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m,
         GemmArgs g{};
         g.qs = w->dev;
         g.hdr = w->dev + L.qs_bytes;
+        g.aux = w->dev + L.qs_bytes + L.hdr_bytes;
         g.x = x;
         g.x_bf16 = x_dtype == NNQ_BF16;
         g.bias = bias;

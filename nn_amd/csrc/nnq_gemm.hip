@@ -25,6 +25,8 @@
 // wave dequantizes its own B fragments from the raw nibbles (mask into f16-subnormal
 // pairs, one packed f16 multiply by the sub-block scale) and reuses each across its
 // WM / 16 A rows.
+#include <cstdlib>
+
 #include "nnq_device.h"
 #include "nnq_internal.h"
 
@@ -33,12 +35,6 @@ namespace nnq {
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 namespace {
-
-struct GemmScratch {
-    uint16_t *xh;      // [P][m][k] f16 of x * 2^s_row
-    uint16_t *xs;      // [2][m][k / 32] f16 hi / lo of 2^-8 * sum(x * 2^s_row) per 32
-    float *rowback;    // [m] 2^-s_row
-};
 
 inline size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -81,7 +77,9 @@ __device__ __forceinline__ uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
 // ---------------------------------------------------------------------------------
 // Activation staging: one workgroup per row.
 // ---------------------------------------------------------------------------------
-template <int P>
+// HI16: the f16 planes of the odd sub-blocks (k % 64 >= 32) carry an extra 2^-4 (the
+// ring kernel reads their high nibbles as 16 q); the sums stay unscaled.
+template <int P, bool HI16>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf16, int64_t m, int64_t k,
                                                         GemmScratch sc) {
     const int64_t row = blockIdx.x;
@@ -124,12 +122,13 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf1
         load8(x, x_bf16, xoff + 8 * g, v);
         u32x4 H, L;
         float sum = 0.0f;
+        const float sx = HI16 && ((g >> 2) & 1) ? 0.0625f : 1.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float a0 = v[2 * i] * s, a1 = v[2 * i + 1] * s;
             uint32_t h0, l0, h1, l1;
-            split_f16(a0, h0, l0);
-            split_f16(a1, h1, l1);
+            split_f16(a0 * sx, h0, l0);
+            split_f16(a1 * sx, h1, l1);
             H[i] = h0 | (h1 << 16);
             L[i] = l0 | (l1 << 16);
             sum += a0 + a1;
@@ -423,11 +422,16 @@ static int launch_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) 
     return (int)hipGetLastError();
 }
 
+static bool use_ring(const GemmArgs &a) {
+    static const int ring = getenv("NNQ_GEMM_OLD") ? 0 : 1;
+    return ring && gemm_ring_fits(a);
+}
+
 template <int P>
 static int launch_p(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    // Largest output tile that still gives every CU a workgroup (256 CUs).
     const int64_t ncols = a.ntile * 16;
     auto wgs = [&](int64_t bm, int64_t bn) { return ((a.m + bm - 1) / bm) * ((ncols + bn - 1) / bn); };
+    if (use_ring(a)) return launch_gemm_ring(a, sc, st);
     if constexpr (P == 1) {  // the f32 (hi + lo) staging doubles the activation LDS
         if (a.m >= 128 && ncols % 192 == 0 && wgs(128, 192) >= 256) return launch_cfg<128, 192, 2, 2, P>(a, sc, st);
         if (a.m >= 128 && wgs(128, 128) >= 256) return launch_cfg<128, 128, 2, 2, P>(a, sc, st);
@@ -437,15 +441,21 @@ static int launch_p(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
     return launch_cfg<32, 64, 2, 2, P>(a, sc, st);
 }
 
+template <int P, bool HI16>
+static void launch_prep(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_prep_kernel<P, HI16>), dim3((unsigned)a.m), dim3(256), 0, st, a.x, a.x_bf16, a.m, a.k, sc);
+}
+
 int launch_gemm_q4k(const GemmArgs &a, void *stream) {
     if (a.m <= 0) return 0;
     const int P = a.x_bf16 ? 1 : 2;
     const GemmScratch sc = carve(a.scratch, a.m, a.k, P);
     hipStream_t st = (hipStream_t)stream;
+    const bool ring = use_ring(a);
     if (P == 1)
-        hipLaunchKernelGGL((gemm_prep_kernel<1>), dim3((unsigned)a.m), dim3(256), 0, st, a.x, a.x_bf16, a.m, a.k, sc);
+        ring ? launch_prep<1, true>(a, sc, st) : launch_prep<1, false>(a, sc, st);
     else
-        hipLaunchKernelGGL((gemm_prep_kernel<2>), dim3((unsigned)a.m), dim3(256), 0, st, a.x, a.x_bf16, a.m, a.k, sc);
+        ring ? launch_prep<2, true>(a, sc, st) : launch_prep<2, false>(a, sc, st);
     int e = (int)hipGetLastError();
     if (e) return e;
     return P == 1 ? launch_p<1>(a, sc, st) : launch_p<2>(a, sc, st);

@@ -29,13 +29,18 @@ struct Layout {
     int64_t nblk = 0;   // format blocks per row after padding (Q8_0: padded to a multiple of 8)
     size_t qs_bytes = 0;   // bytes of the quant plane
     size_t hdr_bytes = 0;  // bytes of the scale/header plane
-    size_t total() const { return qs_bytes + hdr_bytes; }
+    size_t aux_bytes = 0;  // bytes of the derived plane (Q4_K: min-term operands of the GEMM)
+    size_t total() const { return qs_bytes + hdr_bytes + aux_bytes; }
 };
 
 // Q4_K: per (tile, block of 256): qs 2048 B (two 1 KB planes; lane 16p + r of plane h
 //       holds bytes [16h, 16h + 16) of row r's 32-byte group p, i.e. the nibbles of
 //       sub-blocks 2p (low) and 2p + 1 (high)), header 16 rows x 16 B (d, dmin,
 //       scales[12] in GGUF-spec packing).
+//       aux (derived from the headers for the prefill GEMM): per (tile, block) 512 B =
+//       16 rows x 8 f16 hi parts, then 16 x 8 lo parts, of dmin * m_j * s_row (exact as
+//       hi + lo: 17 significant bits); then per row one f32 s_row, the power of two that
+//       puts max_b |dmin_b| * 63 in [2^14, 2^15).
 // Q8_0: per (tile, block pair): qs 1024 B; per (tile, 8 blocks): 16 rows x 8 f16 scales.
 // Q6_K: per (tile, block of 256): qs 3072 B (four 64-k chunks x 64 lanes x 12 B),
 //       header 16 rows x 16 int8 scales + 16 rows x f16 d (288 B).
@@ -48,6 +53,8 @@ void repack_q6k(const uint8_t *src, const Layout &L, uint8_t *dst);
 
 // nn-gguf legacy Q4_K block -> GGUF-spec (BlockQ4K) block with identical decoded values.
 void q4k_legacy_to_gguf(const uint8_t *legacy, uint8_t *gguf);
+// Q4_K aux plane of tiles [t0, t1) from the device header plane (GGUF-spec headers).
+void q4k_aux_plane(const uint8_t *hdr, const Layout &L, uint8_t *aux, int64_t t0, int64_t t1);
 
 // ---- kernel launch parameters ------------------------------------------------------
 struct GemvArgs {
@@ -78,6 +85,7 @@ int launch_argmax_final(const unsigned long long *partial, int64_t count, uint32
 struct GemmArgs {
     const uint8_t *qs;
     const uint8_t *hdr;
+    const uint8_t *aux;
     const void *x;
     int x_bf16;
     const float *bias;
@@ -89,6 +97,15 @@ struct GemmArgs {
 };
 int launch_gemm_q4k(const GemmArgs &a, void *stream);
 size_t gemm_scratch_bytes(int64_t m, int64_t k, int x_bf16);
+// staged activation (gemm_prep_kernel): P = 1 (bf16 x) or 2 (f32 x, hi + lo planes)
+struct GemmScratch {
+    uint16_t *xh;      // [P][m][k] f16 of x * 2^s_row (odd sub-blocks * 2^-4 for the ring kernel)
+    uint16_t *xs;      // [2][m][k / 32] f16 hi / lo of 2^-8 * sum(x * 2^s_row) per 32
+    float *rowback;    // [m] 2^-s_row
+};
+// ring kernel (nnq_gemm_ring.hip): shapes it takes, and its launch
+bool gemm_ring_fits(const GemmArgs &a);
+int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream);
 
 // MoE (GPT-OSS MXFP4).  Expert weights [E][K][N] with 32-element blocks along N
 // (Mxfp4Tensor of the flat tensor) are repacked per (expert, 32-column block nb,

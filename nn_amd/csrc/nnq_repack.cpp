@@ -3,6 +3,7 @@
 // Every transform here is a bijection on the block bytes (plus zero padding of
 // the last row tile and, for Q8_0, of the last group of 8 blocks), so the
 // algorithmic bytes a kernel streams equal the bytes of the source blocks.
+#include <cmath>
 #include <cstring>
 #include <vector>
 
@@ -30,6 +31,7 @@ bool make_layout(int fmt, int layout, int64_t n, int64_t k, Layout *L, const cha
         L->nblk = k / 256;
         L->qs_bytes = (size_t)L->ntile * L->nblk * 2048;
         L->hdr_bytes = (size_t)L->ntile * L->nblk * 256;
+        L->aux_bytes = (size_t)L->ntile * L->nblk * 512 + (size_t)L->ntile * kTile * 4;
         return true;
     case NNQ_FMT_Q8_0:
         if (layout != NNQ_LAYOUT_GGUF && layout != NNQ_LAYOUT_NN_GGUF) {
@@ -245,6 +247,54 @@ void moe_repack(const uint8_t *packed, const uint8_t *scales, int64_t E, int64_t
                 uint8_t *s = ds + frag * 32;
                 for (int r = 0; r < 32; r++) s[r] = scales[(e * K + kb * 32 + r) * NB + nb];
             }
+}
+
+}  // namespace nnq
+
+namespace nnq {
+
+// Power of two s with amax * s in [2^14, 2^15) (1 for amax = 0, NaN for a non-finite
+// amax), exponent clamped to +-126: the device f16_prescale.
+static float prescale_pow2(float amax) {
+    if (!(amax <= 3.0e38f)) return std::nanf("");
+    if (amax == 0.0f) return 1.0f;
+    uint32_t u;
+    std::memcpy(&u, &amax, 4);
+    int eb = (int)((u >> 23) & 0xFF);
+    int se = 141 - (eb > 1 ? eb : 1);
+    se = se > 126 ? 126 : (se < -126 ? -126 : se);
+    return std::ldexp(1.0f, se);
+}
+
+void q4k_aux_plane(const uint8_t *hdr, const Layout &L, uint8_t *aux, int64_t t0, int64_t t1) {
+    float *srow = reinterpret_cast<float *>(aux + (size_t)L.ntile * L.nblk * 512);
+    for (int64_t t = t0; t < t1; t++)
+        for (int r = 0; r < kTile; r++) {
+            auto dmin_of = [&](int64_t b) {
+                uint16_t h;
+                std::memcpy(&h, hdr + (t * L.nblk + b) * 256 + 16 * r + 2, 2);
+                _Float16 f;
+                std::memcpy(&f, &h, 2);
+                return (float)f;
+            };
+            float dmax = 0.0f;
+            for (int64_t b = 0; b < L.nblk; b++) dmax = std::fmax(dmax, std::fabs(dmin_of(b)));
+            const float s = prescale_pow2(dmax * 63.0f);
+            srow[t * kTile + r] = s;
+            for (int64_t b = 0; b < L.nblk; b++) {
+                const uint8_t *q = hdr + (t * L.nblk + b) * 256 + 16 * r + 4;  // scales[12]
+                const float dm = dmin_of(b) * s;
+                uint8_t *hi = aux + (t * L.nblk + b) * 512 + 16 * r, *lo = hi + 256;
+                for (int j = 0; j < 8; j++) {
+                    // get_scale_min_k4 (crates/nn-core/src/layers/quantized/linear.rs:166-176): the min
+                    const uint8_t m = j < 4 ? (q[j + 4] & 63) : (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+                    const float v = dm * (float)m;  // exact: 11 + 6 significant bits
+                    const _Float16 h = (_Float16)v, l = (_Float16)(v - (float)h);
+                    std::memcpy(hi + 2 * j, &h, 2);
+                    std::memcpy(lo + 2 * j, &l, 2);
+                }
+            }
+        }
 }
 
 }  // namespace nnq
