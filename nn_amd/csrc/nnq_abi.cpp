@@ -256,7 +256,7 @@ int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m,
         g.ntile = L.ntile;
         g.nblk = L.nblk;
         Scratch s;
-        HIP_TRY(s.alloc(gemm_scratch_bytes(m, L.k, g.x_bf16), (hipStream_t)stream), "scratch alloc");
+        HIP_TRY(s.alloc(gemm_scratch_bytes(g), (hipStream_t)stream), "scratch alloc");
         g.scratch = s.p;
         int e = launch_gemm_q4k(g, stream);
         if (e) return hip_fail((hipError_t)e, "gemm launch");

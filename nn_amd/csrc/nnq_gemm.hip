@@ -38,14 +38,30 @@ namespace {
 
 inline size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
-GemmScratch carve(void *base, int64_t m, int64_t k, int P) {
+bool use_ring(const GemmArgs &a) {
+    static const int ring = getenv("NNQ_GEMM_OLD") ? 0 : 1;
+    return ring && gemm_ring_plan(a, nullptr) > 0;
+}
+
+// scratch layout: xh | xs | rowback | ysplit; base null: offsets from 0 (sizing)
+GemmScratch carve(void *base, const GemmArgs &a, size_t *bytes) {
+    const int P = a.x_bf16 ? 1 : 2;
     uint8_t *b = reinterpret_cast<uint8_t *>(base);
+    size_t off = 0;
     GemmScratch s;
-    s.xh = reinterpret_cast<uint16_t *>(b);
-    b += al256((size_t)P * m * k * 2);
-    s.xs = reinterpret_cast<uint16_t *>(b);
-    b += al256((size_t)2 * m * (k / 32) * 2);
-    s.rowback = reinterpret_cast<float *>(b);
+    s.xh = reinterpret_cast<uint16_t *>(b + off);
+    off += al256((size_t)P * a.m * a.k * 2);
+    s.xs = reinterpret_cast<uint16_t *>(b + off);
+    off += al256((size_t)2 * a.m * (a.k / 32) * 2);
+    s.rowback = reinterpret_cast<float *>(b + off);
+    off += al256((size_t)a.m * 4);
+    s.ksplit = use_ring(a) ? gemm_ring_plan(a, nullptr) : 1;
+    s.ysplit = nullptr;
+    if (s.ksplit > 1) {
+        s.ysplit = reinterpret_cast<float *>(b + off);
+        off += al256((size_t)s.ksplit * a.m * a.n * 4);
+    }
+    if (bytes) *bytes = off;
     return s;
 }
 
@@ -402,9 +418,10 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_q4k_kernel(GemmArgs a, Gem
 // ---------------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------------
-size_t gemm_scratch_bytes(int64_t m, int64_t k, int x_bf16) {
-    const int P = x_bf16 ? 1 : 2;
-    return al256((size_t)P * m * k * 2) + al256((size_t)2 * m * (k / 32) * 2) + al256((size_t)m * 4);
+size_t gemm_scratch_bytes(const GemmArgs &a) {
+    size_t bytes = 0;
+    carve(nullptr, a, &bytes);
+    return bytes;
 }
 
 template <int BM, int BN, int WGM, int WGN, int P>
@@ -420,11 +437,6 @@ static int launch_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) 
     const dim3 grid((unsigned)((a.ntile * 16 + BN - 1) / BN), (unsigned)((a.m + BM - 1) / BM));
     hipLaunchKernelGGL((gemm_q4k_kernel<BM, BN, WGM, WGN, P>), grid, dim3(C::NTH), C::LDS, st, a, sc);
     return (int)hipGetLastError();
-}
-
-static bool use_ring(const GemmArgs &a) {
-    static const int ring = getenv("NNQ_GEMM_OLD") ? 0 : 1;
-    return ring && gemm_ring_fits(a);
 }
 
 template <int P>
@@ -449,7 +461,7 @@ static void launch_prep(const GemmArgs &a, const GemmScratch &sc, hipStream_t st
 int launch_gemm_q4k(const GemmArgs &a, void *stream) {
     if (a.m <= 0) return 0;
     const int P = a.x_bf16 ? 1 : 2;
-    const GemmScratch sc = carve(a.scratch, a.m, a.k, P);
+    const GemmScratch sc = carve(a.scratch, a, nullptr);
     hipStream_t st = (hipStream_t)stream;
     const bool ring = use_ring(a);
     if (P == 1)

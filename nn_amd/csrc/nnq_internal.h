@@ -81,7 +81,8 @@ int launch_argmax_final(const unsigned long long *partial, int64_t count, uint32
                         void *stream);
 
 // GEMM (prefill) for Q4_K: x bf16/f32 [m, k] -> y [m, n].  `scratch` holds the
-// staged activation (gemm_scratch_bytes(m, k, x_bf16) bytes, 256-byte aligned).
+// staged activation and split-K partials (gemm_scratch_bytes(args) bytes, 256-byte
+// aligned; every field but scratch set).
 struct GemmArgs {
     const uint8_t *qs;
     const uint8_t *hdr;
@@ -96,15 +97,18 @@ struct GemmArgs {
     void *scratch;
 };
 int launch_gemm_q4k(const GemmArgs &a, void *stream);
-size_t gemm_scratch_bytes(int64_t m, int64_t k, int x_bf16);
+size_t gemm_scratch_bytes(const GemmArgs &a);
 // staged activation (gemm_prep_kernel): P = 1 (bf16 x) or 2 (f32 x, hi + lo planes)
 struct GemmScratch {
     uint16_t *xh;      // [P][m][k] f16 of x * 2^s_row (odd sub-blocks * 2^-4 for the ring kernel)
     uint16_t *xs;      // [2][m][k / 32] f16 hi / lo of 2^-8 * sum(x * 2^s_row) per 32
     float *rowback;    // [m] 2^-s_row
+    int ksplit;        // K split of the ring kernel (1: none)
+    float *ysplit;     // [ksplit][m][n] f32 partial results when ksplit > 1
 };
-// ring kernel (nnq_gemm_ring.hip): shapes it takes, and its launch
-bool gemm_ring_fits(const GemmArgs &a);
+// ring kernel (nnq_gemm_ring.hip): its K split for a shape (0: the shape does not fit
+// the kernel; bn, when given, receives the tile width), and its launch
+int gemm_ring_plan(const GemmArgs &a, int *bn);
 int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream);
 
 // MoE (GPT-OSS MXFP4).  Expert weights [E][K][N] with 32-element blocks along N

@@ -107,3 +107,26 @@ def test_gemm_baseline_shapes(O, dev, m, n, k):
     yb = nn_amd.quantized_linear(x, w, out_dtype=torch.bfloat16).float().cpu().numpy()
     ref_b = torch.from_numpy(y).to(torch.bfloat16).float().numpy()
     assert np.array_equal(yb, ref_b), "bf16 output must be the f32 result rounded once"
+
+
+@pytest.mark.parametrize("m,n,k", [(130, 256, 4096), (256, 384, 2048), (128, 192, 256), (300, 640, 1280),
+                                   (384, 1024, 4096)])
+def test_gemm_ring_edges(O, dev, m, n, k):
+    """The LDS-ring kernel's edges (bf16 activations, m >= 128): ragged last row tile,
+    128- and 192-wide column tiles, a single super-block, K split 1, 2 and 4 ways, with
+    random block bytes (arbitrary finite d / dmin / scales), d = 0 super-blocks, bias,
+    f32 and bf16 outputs; the split-K sum is deterministic (two calls agree bit for bit)."""
+    import nn_amd
+    b = rand_bytes("q4_k", n, k, seed=m + n + k).reshape(-1, 144).copy()
+    b[::5, 0:2] = 0  # d = +0.0 for every fifth super-block
+    b = b.ravel()
+    w = make_weight("q4_k_legacy", b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(m, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    bias = torch.from_numpy(nn_amd.synth_normal(m, 3, (n,), 0.5)).to(dev)
+    y = nn_amd.quantized_linear(x, w, bias)
+    y2 = nn_amd.quantized_linear(x, w, bias)
+    assert torch.equal(y, y2), "repeated calls must agree bit for bit"
+    ref = ref_f64(O, b, n, k, x.float().cpu().numpy(), legacy=True) + bias.cpu().numpy()
+    check_close(ref, y.cpu().numpy(), f"gemm ring {m}x{n}x{k}")
+    yb = nn_amd.quantized_linear(x, w, bias, out_dtype=torch.bfloat16).float().cpu().numpy()
+    assert np.array_equal(yb, y.to(torch.bfloat16).float().cpu().numpy()), "bf16 output: the f32 result rounded once"
