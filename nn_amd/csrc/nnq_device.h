@@ -31,11 +31,11 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
-// round-to-nearest-even f32 -> bf16 bits (NaN kept quiet)
+// round-to-nearest-even f32 -> bf16 bits (NaN kept quiet); a select, not a branch
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    uint32_t x = __float_as_uint(f);
-    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (x >> 16) | 0x40u;
-    return (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t r = (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
+    return (x & 0x7FFFFFFFu) > 0x7F800000u ? ((x >> 16) | 0x40u) : r;
 }
 
 // Split x (already scaled into f16 range) into hi + lo f16 parts: x ~= hi + lo with

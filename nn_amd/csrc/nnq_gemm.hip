@@ -93,9 +93,7 @@ __device__ __forceinline__ uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
 // ---------------------------------------------------------------------------------
 // Activation staging: one workgroup per row.
 // ---------------------------------------------------------------------------------
-// HI16: the f16 planes of the odd sub-blocks (k % 64 >= 32) carry an extra 2^-4 (the
-// ring kernel reads their high nibbles as 16 q); the sums stay unscaled.
-template <int P, bool HI16>
+template <int P>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf16, int64_t m, int64_t k,
                                                         GemmScratch sc) {
     const int64_t row = blockIdx.x;
@@ -138,13 +136,12 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf1
         load8(x, x_bf16, xoff + 8 * g, v);
         u32x4 H, L;
         float sum = 0.0f;
-        const float sx = HI16 && ((g >> 2) & 1) ? 0.0625f : 1.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float a0 = v[2 * i] * s, a1 = v[2 * i + 1] * s;
             uint32_t h0, l0, h1, l1;
-            split_f16(a0 * sx, h0, l0);
-            split_f16(a1 * sx, h1, l1);
+            split_f16(a0, h0, l0);
+            split_f16(a1, h1, l1);
             H[i] = h0 | (h1 << 16);
             L[i] = l0 | (l1 << 16);
             sum += a0 + a1;
@@ -453,9 +450,9 @@ static int launch_p(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
     return launch_cfg<32, 64, 2, 2, P>(a, sc, st);
 }
 
-template <int P, bool HI16>
+template <int P>
 static void launch_prep(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_prep_kernel<P, HI16>), dim3((unsigned)a.m), dim3(256), 0, st, a.x, a.x_bf16, a.m, a.k, sc);
+    hipLaunchKernelGGL((gemm_prep_kernel<P>), dim3((unsigned)a.m), dim3(256), 0, st, a.x, a.x_bf16, a.m, a.k, sc);
 }
 
 int launch_gemm_q4k(const GemmArgs &a, void *stream) {
@@ -463,11 +460,10 @@ int launch_gemm_q4k(const GemmArgs &a, void *stream) {
     const int P = a.x_bf16 ? 1 : 2;
     const GemmScratch sc = carve(a.scratch, a, nullptr);
     hipStream_t st = (hipStream_t)stream;
-    const bool ring = use_ring(a);
     if (P == 1)
-        ring ? launch_prep<1, true>(a, sc, st) : launch_prep<1, false>(a, sc, st);
+        launch_prep<1>(a, sc, st);
     else
-        ring ? launch_prep<2, true>(a, sc, st) : launch_prep<2, false>(a, sc, st);
+        launch_prep<2>(a, sc, st);
     int e = (int)hipGetLastError();
     if (e) return e;
     return P == 1 ? launch_p<1>(a, sc, st) : launch_p<2>(a, sc, st);

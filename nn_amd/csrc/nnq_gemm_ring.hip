@@ -1,37 +1,36 @@
-// Prefill GEMM for Q4_K weights on gfx950, warp-specialized ring kernel (bf16
-// activations, M >= 128): Y[m, n] = X[m, k] . W[n, k]^T (+ bias), the same arithmetic
-// as gemm_q4k_kernel (QLinear::forward with a batch of tokens,
-// crates/nn-core/src/layers/quantized/linear.rs:366-400).
+// Prefill GEMM for Q4_K weights on gfx950, LDS-ring kernel (bf16 activations, M >= 128):
+// Y[m, n] = X[m, k] . W[n, k]^T (+ bias), the arithmetic of QLinear::forward with a batch
+// of tokens (crates/nn-core/src/layers/quantized/linear.rs:366-400).
 //
-// Stage s = 64 k = byte group p = s % 4 of super-block sb = s / 4, i.e. sub-blocks 2p
-// (low nibbles: k 0..31 of the stage) and 2p + 1 (high nibbles: k 32..63).  A ring of
-// NBUF LDS buffers holds consecutive stages:
-//   A: BM rows x 8 chunks of 8 f16; chunk c of row r sits at slot c ^ ((r >> 1) & 7),
-//      so the 16-byte fragment reads of 16 consecutive rows fall in distinct banks;
-//   B: NTILE tiles x 2 planes x 16 rows x 16 bytes (the tile16 bytes of group p).
-// Stages are copied NBUF - 1 ahead with global_load_lds (16 bytes per lane, no
-// register round trip); the super-block headers are copied the same way, one
-// super-block ahead, into two LDS areas by super-block parity.
+// Stage s = 64 k = byte group p = s % 4 of super-block sb = s / 4: sub-blocks 2p (the low
+// nibbles of the group's 32 bytes per row) and 2p + 1 (the high nibbles).  A ring of NBUF
+// LDS buffers holds consecutive stages, copied NBUF - 1 stages ahead by every thread with
+// global_load_lds (16 bytes per lane, no register round trip):
+//   A: 128 rows x 8 chunks of 8 f16; chunk c of row r sits at slot c ^ ((r >> 1) & 7), so
+//      the 16-byte fragment reads of 16 consecutive rows fall in distinct banks;
+//   B: the raw tile16 bytes of group p: tile x plane x 16 rows x 16 bytes;
+// and the super-block headers ride along with the first stage of each super-block.
 //
-// Eight waves: 0..3 consume (MFMA only, wave tile BM x BN / 4), 4..7 produce, one of
-// each per SIMD, so the producers' dequantization VALU runs beside the consumers'
-// MFMAs.  Per iteration s, after one barrier:
-//   producers: copy stage s + NBUF - 1, wait for their own copies of stage s + 1, and
-//     dequantize the raw B bytes they copied themselves into the f16 buffer (s + 1) & 1
-//     ([tile][hf][lane] x 16 bytes: the consumers' B fragments), sc folded in;
-//   consumers: the MFMAs of stage s (A from the ring, B from f16 buffer s & 1).
-// B is sc * q as an exact f16: the masked low nibbles q * 2^-24 (subnormals) times sc,
-// and the masked high nibbles (16 q) * 2^-24 times sc, with the staged activation of
-// the odd sub-blocks pre-scaled by 2^-4 to match (gemm_prep_kernel<P, true>).  The
-// accumulator of column n is kept in units of u_n, the latest non-zero d of the
-// column, and rescaled by u_prev / u_next when a super-block starts.  The min term runs
-// after the main loop from the weight's aux plane (dmin * m_j * s_n precomputed at
-// upload as exact f16 hi + lo).
+// Four waves in a 2 x 2 arrangement, each a 64 x BN/2 wave tile; every wave dequantizes
+// the raw bytes of its own columns in registers (no dequantized copy through LDS):
+// consumer lane 16G + r takes bytes 8G .. 8G + 7 of row r's group (plane G >> 1), whose
+// low nibbles are k = 64p + 8G + i of sub-block 2p and high nibbles k = 64p + 32 + 8G + i
+// of sub-block 2p + 1, so each stage is two MFMA steps of 32 k, one sub-block each, and
+// the A fragment of lane group G is chunk G (step 0) or 4 + G (step 1) of the row.
+// B = sc * q is an exact f16: the masked nibble pairs are f16 subnormals q * 2^-24 (low
+// nibbles) or 16 q * 2^-24 (high nibbles), times sc or sc / 16 (exact f16 products).
 //
-// Split-K (KS > 1, when the output tiles alone would leave CUs idle): workgroup
-// (tile, ks) covers super-blocks [ks * nblk / KS, (ks + 1) * nblk / KS) and stores its
-// partial result in f32 slab ks of the scratch; a finalize kernel sums the slabs in
-// order (deterministic), adds the bias and converts.
+// The per-super-block factor d: the MFMAs of a super-block accumulate from zero into
+// AGPR partial sums (so the dequantization VALU work issues beside the MFMAs), and at the
+// super-block's end every lane adds d_n * partial into its f32 totals.  The min term
+// dmin * m_j * sum(x over the sub-block) runs after the main loop on the MFMA from the
+// weight's aux plane (dmin * m_j * s_n precomputed at upload as exact f16 hi + lo) and
+// the staged sub-block sums of x (hi + lo).
+//
+// Split-K (KS > 1, when the output tiles alone would leave CUs idle): workgroup (tile,
+// ks) covers super-blocks [ks * nblk / KS, (ks + 1) * nblk / KS) and stores its partial
+// result in f32 slab ks of the scratch; a finalize kernel sums the slabs in order
+// (deterministic), adds the bias and converts.
 #include <cstdlib>
 
 #include "nnq_device.h"
@@ -43,14 +42,12 @@ namespace {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) * __builtin_bit_cast(half2v, b));
-}
-
-// f16 pair (v, v) of a small non-negative integer v (exact)
-__device__ __forceinline__ uint32_t f16_pair_int(uint32_t v) {
-    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)(float)v);
-    return h | (h << 16);
+// f16 pair product a * (s.lo, s.lo) (HI = 0) or a * (s.hi, s.hi) (HI = 1)
+template <int HI>
+__device__ __forceinline__ uint32_t pk_mul_bcast(uint32_t a, uint32_t s) {
+    const half2v sv = __builtin_bit_cast(half2v, s);
+    const half2v b = HI ? half2v{sv[1], sv[1]} : half2v{sv[0], sv[0]};
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) * b);
 }
 
 // s_waitcnt vmcnt(N) only (expcnt and lgkmcnt left at their maxima)
@@ -63,48 +60,60 @@ __device__ __forceinline__ void wait_vmcnt() {
 #define NNQ_GPTR(p) ((const __attribute__((address_space(1))) void *)(p))
 #define NNQ_LPTR(p) ((__attribute__((address_space(3))) void *)(p))
 
-
-// ---------------------------------------------------------------------------------
-template <int BN, int NBUF>
-struct WS {
-    static constexpr int BM = 128, NTILE = BN / 16, NC = 4, NP = 4;
-    static constexpr int NTH = (NC + NP) * 64, PTH = NP * 64;
-    static constexpr int MT = BM / 16, NT = NTILE / NC;
+template <int BN, int NBUF, int WGN>
+struct RK {
+    // WGN wave columns x (4 / WGN) wave rows, wave tile WM x (BN / WGN)
+    static constexpr int BM = 128, NTH = 256, NTILE = BN / 16, NT = NTILE / WGN, MT = 2 * WGN;
+    static constexpr int WM = BM * WGN / 4;
     static constexpr int A_CH = BM * 8, B_CH = NTILE * 32, CH = A_CH + B_CH;
-    static constexpr int LPT = (CH + PTH - 1) / PTH;
-    static constexpr int NO = (B_CH + PTH - 1) / PTH;  // raw B chunks dequantized per producer thread
-    static constexpr int BUF = LPT * PTH * 16;
-    static constexpr int F16B = NTILE * 2 * 64 * 16;
-    static constexpr int HDR = PTH * 16;
-    static constexpr size_t LDS = (size_t)NBUF * BUF + 2 * F16B + 2 * HDR;
-    static_assert(NTILE % NC == 0, "tiles split evenly over the consumers");
-    static_assert(A_CH % PTH == 0, "a copy instruction is all A or all B");
-    static_assert(NTILE * 16 <= PTH, "one header copy per producer thread");
+    static constexpr int LPT = (CH + NTH - 1) / NTH;  // copy instructions per thread and stage
+    static constexpr int BUF = LPT * NTH * 16;
+    // per super-block (two areas, by parity): headers (NTILE x 16 rows x 16 B), the
+    // staged sub-block sums of x (BM rows x hi / lo x 16 B), the weight's min-term
+    // operands (NTILE x hi / lo x 16 rows x 16 B)
+    static constexpr int AUX_CH = NTILE * 32, AUXI = (AUX_CH + NTH - 1) / NTH;
+    static constexpr int SB_EXTRA = 2 + AUXI;  // copy instructions per thread and super-block
+    static constexpr int HDR_OFF = 0, XS_OFF = NTH * 16, AUX_OFF = XS_OFF + BM * 2 * 16;
+    static constexpr int SBA = AUX_OFF + AUXI * NTH * 16;
+    // epilogue factors: 2^-s_row of the BM rows, s_n of the BN columns (f32)
+    static constexpr int EPI_CH = (BM + BN) / 4;
+    static constexpr size_t LDS = (size_t)NBUF * BUF + 2 * SBA + NTH * 16;
+    static_assert(EPI_CH <= NTH, "one epilogue-factor copy per thread");
+    static_assert((size_t)BM * (BN * 4 + 16) <= (size_t)NBUF * BUF + 2 * SBA, "the f32 output tile fits below the factors");
+    static_assert(NTILE % WGN == 0, "column tiles split evenly over the wave columns");
+    static_assert(MT * 16 == WM, "wave rows");
+    static_assert(A_CH % NTH == 0, "a copy instruction is all A or all B");
+    static_assert(NTILE * 16 <= NTH && BM * 2 == NTH, "one header and one sums copy per thread");
     static_assert(LDS <= 160 * 1024, "LDS budget of a gfx950 workgroup");
-    static_assert(NBUF >= 4 && (NBUF - 2) * LPT + 2 < 64, "vmcnt range");
+    static_assert((NBUF - 1) * (LPT + SB_EXTRA) < 64, "vmcnt range");
 };
 
-// header batches (at iterations t = 3 mod 4, before that iteration's copies) issued
-// after the copies of stage s + 1 and before the producers' wait in iteration s
-constexpr int ws_batches(int p, int nbuf) {
-    int n = 0;
-    for (int d = 3 - nbuf; d <= 0; d++)
-        if ((((p + d) % 4) + 4) % 4 == 3) n++;
+// VMEM instructions a thread issues after the batch of stage s and before the wait in
+// iteration s: the batches of stages s + 1 .. s + NBUF - 2, those that start a
+// super-block carrying SBX extra copies.  p = s % 4 fixes the count.
+template <int NBUF, int LPT, int SBX>
+constexpr int rk_wait(int p) {
+    int n = (NBUF - 2) * LPT;
+    for (int t = p + 1; t <= p + NBUF - 2; t++)
+        if (t % 4 == 0) n += SBX;
     return n;
 }
 
-template <int BN, int NBUF>
-__global__ __launch_bounds__(512) void gemm_q4k_ws_kernel(GemmArgs a, GemmScratch sc) {
-    using C = WS<BN, NBUF>;
-    constexpr int MT = C::MT, NT = C::NT, LPT = C::LPT, PTH = C::PTH, BM = C::BM, NO = C::NO;
+template <int BN, int NBUF, int WGN>
+__global__ __launch_bounds__(256) void gemm_q4k_rk_kernel(GemmArgs a, GemmScratch sc) {
+    using C = RK<BN, NBUF, WGN>;
+    constexpr int MT = C::MT, NT = C::NT, LPT = C::LPT, NTH = C::NTH, BM = C::BM;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     unsigned char *ring = smem;
-    unsigned char *f16b = smem + (size_t)NBUF * C::BUF;
-    unsigned char *hdr_lds = f16b + 2 * C::F16B;
+    unsigned char *sba = smem + (size_t)NBUF * C::BUF;  // the two per-super-block areas
+    float *epi = reinterpret_cast<float *>(sba + 2 * C::SBA);  // [BM] 2^-s_row, [BN] s_n
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wv / WGN, wn = wv % WGN;
+    const int G = lane >> 4, c16 = lane & 15;
     const int K = (int)a.k, M = (int)a.m, nblk_all = (int)a.nblk, ntile = (int)a.ntile;
     const int KS = sc.ksplit;
+    const int nsub = K / 32;
 
     // Tile order: workgroup ids go round-robin over the 8 XCDs, so when the count
     // allows, each XCD gets a contiguous run of tiles (same activation rows and K range,
@@ -117,280 +126,265 @@ __global__ __launch_bounds__(512) void gemm_q4k_ws_kernel(GemmArgs a, GemmScratc
     const int nblk = nblk_all / KS, sb0 = ks * nblk;  // this workgroup's super-blocks
     const int nstage = nblk * 4;
 
-    if (wv >= C::NC) {
-        // ================================ producers ================================
-        const int pw = wv - C::NC, pj = tid - C::NC * 64;
-        const uint8_t *src[LPT];
-#pragma unroll
-        for (int j = 0; j < LPT; j++) {
-            const int c = j * PTH + pj;
-            if (j * PTH < C::A_CH) {
-                const int r = c >> 3, kc = (c & 7) ^ ((r >> 1) & 7);
-                const int row = min(m0 + r, M - 1);
-                src[j] = reinterpret_cast<const uint8_t *>(sc.xh) + ((size_t)row * K + (size_t)sb0 * 256 + 8 * kc) * 2;
-            } else {
-                const int cb = min(c - C::A_CH, C::B_CH - 1);
-                const int tile = min(t0 + (cb >> 5), ntile - 1);
-                src[j] = a.qs + ((size_t)tile * nblk_all + sb0) * 2048 + ((cb >> 4) & 1) * 1024 + (cb & 15) * 16;
-            }
-        }
-        auto issue = [&](int s) {  // stages past the end re-copy the last one into a free buffer
-            const int sv = min(s, nstage - 1);
-            const uint32_t offa = (uint32_t)sv * 128u, offb = (uint32_t)sv * 256u + (uint32_t)(sv >> 2) * 1024u;
-            unsigned char *buf = ring + (size_t)(s % NBUF) * C::BUF;
-#pragma unroll
-            for (int j = 0; j < LPT; j++)
-                __builtin_amdgcn_global_load_lds(NNQ_GPTR(src[j] + (j * PTH < C::A_CH ? offa : offb)),
-                                                 NNQ_LPTR(buf + (size_t)(j * PTH + pw * 64) * 16), 16, 0, 0);
-        };
-        const uint8_t *hcsrc;
-        {
-            const int cc = min(pj, C::NTILE * 16 - 1);
-            hcsrc = a.hdr + ((size_t)min(t0 + cc / 16, ntile - 1) * nblk_all + sb0) * 256 + (cc % 16) * 16;
-        }
-        auto hload = [&](int sb) {
-            __builtin_amdgcn_global_load_lds(NNQ_GPTR(hcsrc + (size_t)min(sb, nblk - 1) * 256),
-                                             NNQ_LPTR(hdr_lds + (size_t)((sb & 1) * PTH + pw * 64) * 16), 16, 0, 0);
-        };
-        // dequantization ownership: raw B chunks cb = o * 256 + pj (when < B_CH): tile
-        // cb >> 5, plane (cb >> 4) & 1, row cb & 15; the column is tile * 16 + row
-        int cbo[NO];
-        bool own[NO];
-#pragma unroll
-        for (int o = 0; o < NO; o++) {
-            cbo[o] = min(o * PTH + pj, C::B_CH - 1);
-            own[o] = o * PTH + pj < C::B_CH;
-        }
-        uint32_t scw[NO][2];
-        auto decode = [&](int sb) {
-#pragma unroll
-            for (int o = 0; o < NO; o++) {
-                const int col = (cbo[o] >> 5) * 16 + (cbo[o] & 15);
-                const u32x4 h = *reinterpret_cast<const u32x4 *>(hdr_lds + (size_t)(sb & 1) * PTH * 16 + col * 16);
-                // BlockQ4K header (get_scale_min_k4, crates/nn-core/src/layers/quantized/linear.rs:166-176)
-                const uint32_t nzm = (h[0] & 0x7FFFu) != 0u ? 0xFFFFFFFFu : 0u;  // d != 0
-                scw[o][0] = h[1] & 0x3F3F3F3Fu & nzm;
-                scw[o][1] = ((h[3] & 0x0F0F0F0Fu) | ((h[1] >> 2) & 0x30303030u)) & nzm;
-            }
-        };
-        auto dequant = [&](int s) {  // stage s: raw bytes (ring) -> f16 fragments (buffer s & 1)
-            const int p = s & 3;
-            const unsigned char *raw = ring + (size_t)(s % NBUF) * C::BUF + C::A_CH * 16;
-            unsigned char *dst = f16b + (size_t)(s & 1) * C::F16B;
-#pragma unroll
-            for (int o = 0; o < NO; o++) {
-                if (!own[o]) continue;
-                const int cb = cbo[o], t = cb >> 5, h = (cb >> 4) & 1, r = cb & 15;
-                const u32x4 w = *reinterpret_cast<const u32x4 *>(raw + cb * 16);
-                const uint32_t sw = scw[o][p >> 1];
-                const uint32_t sl = f16_pair_int((sw >> (16 * (p & 1))) & 0xFFu);
-                const uint32_t sh = f16_pair_int((sw >> (16 * (p & 1) + 8)) & 0xFFu);
-#pragma unroll
-                for (int half = 0; half < 2; half++) {  // bytes 8 half .. + 7: consumer lane (2h + half) * 16 + r
-                    const uint32_t w0 = w[2 * half], w1 = w[2 * half + 1], w0s = w0 >> 8, w1s = w1 >> 8;
-                    const int L = (2 * h + half) * 16 + r;
-                    const u32x4 lo = {pk_mul_f16(w0 & 0x000F000Fu, sl), pk_mul_f16(w0s & 0x000F000Fu, sl),
-                                      pk_mul_f16(w1 & 0x000F000Fu, sl), pk_mul_f16(w1s & 0x000F000Fu, sl)};
-                    const u32x4 hi = {pk_mul_f16(w0 & 0x00F000F0u, sh), pk_mul_f16(w0s & 0x00F000F0u, sh),
-                                      pk_mul_f16(w1 & 0x00F000F0u, sh), pk_mul_f16(w1s & 0x00F000F0u, sh)};
-                    *reinterpret_cast<u32x4 *>(dst + ((t * 2 + 0) * 64 + L) * 16) = lo;
-                    *reinterpret_cast<u32x4 *>(dst + ((t * 2 + 1) * 64 + L) * 16) = hi;
-                }
-            }
-        };
-
-        hload(0);
-#pragma unroll
-        for (int t = -(NBUF - 1); t <= -1; t++) {
-            if (t == -1) hload(1);
-            issue(t + NBUF - 1);
-        }
-        wait_vmcnt<(NBUF - 2) * LPT + 1>();  // header 0 and stage 0 (own copies)
-        __builtin_amdgcn_s_barrier();        // every producer's header copy is visible
-        decode(0);
-        dequant(0);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the f16 fragments are written
-        for (int sb = 0; sb < nblk; sb++) {
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                const int s = 4 * sb + p;
-                __builtin_amdgcn_s_barrier();
-                if (p == 3) hload(sb + 2);  // into the area of super-block sb: decoded already
-                issue(s + NBUF - 1);
-                if (ws_batches(p, NBUF) == 1)  // p is a constant once the loop is unrolled
-                    wait_vmcnt<(NBUF - 2) * LPT + 1>();
-                else
-                    wait_vmcnt<(NBUF - 2) * LPT>();
-                if (p == 3) decode(sb + 1);  // visible since the barrier of iteration s - 1
-                dequant(s + 1);
-                __builtin_amdgcn_s_waitcnt(0xC07F);
-            }
-        }
-        wait_vmcnt<0>();
-        return;
+    // epilogue factors, copied to LDS now (read back after the main loop): 2^-s_row of
+    // the tile's rows, s_n (the power of two of the min-term operands) of its columns.
+    // A ragged last row tile clamps to the granule holding row M - 1; the scratch that
+    // holds 2^-s_row is padded to 256 bytes, so that granule is inside it.
+    {
+        const float *s_rows = reinterpret_cast<const float *>(a.aux + (size_t)ntile * nblk_all * 512);
+        const int g = min(tid, C::EPI_CH - 1);
+        const float *esrc = g < BM / 4 ? sc.rowback + 4 * min(m0 / 4 + g, (M - 1) / 4)
+                                       : s_rows + (size_t)t0 * 16 + 4 * (g - BM / 4);
+        __builtin_amdgcn_global_load_lds(NNQ_GPTR(esrc), NNQ_LPTR(reinterpret_cast<unsigned char *>(epi) + wv * 64 * 16),
+                                         16, 0, 0);
     }
 
-    // ================================== consumers ==================================
-    const int wn = wv;
-    const int q = lane >> 4, c16 = lane & 15;
-    float ucur[NT], ratio[NT];
+    // ---- copy sources (every thread copies LPT granules per stage) ----
+    const uint8_t *src[LPT];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) ucur[nt] = 1.0f;
-    auto decode_d = [&](int sb) {
+    for (int j = 0; j < LPT; j++) {
+        const int c = j * NTH + tid;
+        if (j * NTH < C::A_CH) {
+            const int r = c >> 3, kc = (c & 7) ^ ((r >> 1) & 7);
+            const int row = min(m0 + r, M - 1);
+            src[j] = reinterpret_cast<const uint8_t *>(sc.xh) + ((size_t)row * K + (size_t)sb0 * 256 + 8 * kc) * 2;
+        } else {
+            // granules past B_CH re-copy the last one into slots nobody reads
+            const int cb = min(c - C::A_CH, C::B_CH - 1);
+            const int tile = min(t0 + (cb >> 5), ntile - 1);
+            src[j] = a.qs + ((size_t)tile * nblk_all + sb0) * 2048 + ((cb >> 4) & 1) * 1024 + (cb & 15) * 16;
+        }
+    }
+    // per super-block: header granule (tile, row), sums granule (row, hi / lo), min-term
+    // operand granules (tile, hi / lo, row); all advance by one super-block at a time
+    const uint8_t *hsrc, *xsrc, *asrc[C::AUXI];
+    {
+        const int cc = min(tid, C::NTILE * 16 - 1);
+        hsrc = a.hdr + ((size_t)min(t0 + cc / 16, ntile - 1) * nblk_all + sb0) * 256 + (cc % 16) * 16;
+        const int row = min(m0 + (tid >> 1), M - 1);
+        xsrc = reinterpret_cast<const uint8_t *>(sc.xs) +
+               ((size_t)(tid & 1) * M * nsub + (size_t)row * nsub + (size_t)sb0 * 8) * 2;
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int col = (wn * NT + nt) * 16 + c16;
-            const uint32_t h0 = *reinterpret_cast<const uint32_t *>(hdr_lds + (size_t)(sb & 1) * PTH * 16 + col * 16);
-            const float d = f16_to_f32(h0 & 0xFFFFu);
-            const float un = d != 0.0f ? d : ucur[nt];
-            ratio[nt] = ucur[nt] * __builtin_amdgcn_rcpf(un);
-            ucur[nt] = un;
+        for (int i = 0; i < C::AUXI; i++) {
+            const int c = min(i * NTH + tid, C::AUX_CH - 1);
+            asrc[i] = a.aux + ((size_t)min(t0 + (c >> 5), ntile - 1) * nblk_all + sb0) * 512 + ((c >> 4) & 1) * 256 +
+                      (c & 15) * 16;
+        }
+    }
+    // stage s: its A and B granules, plus (first stage of a super-block) the super-block's
+    // header, sums and min-term operands; stages past the end re-copy the last one into a
+    // buffer nobody reads any more
+    auto issue = [&](int s) {
+        const int sv = min(s, nstage - 1);
+        const uint32_t offa = (uint32_t)sv * 128u, offb = (uint32_t)sv * 256u + (uint32_t)(sv >> 2) * 1024u;
+        unsigned char *buf = ring + (size_t)(s % NBUF) * C::BUF;
+#pragma unroll
+        for (int j = 0; j < LPT; j++)
+            __builtin_amdgcn_global_load_lds(NNQ_GPTR(src[j] + (j * NTH < C::A_CH ? offa : offb)),
+                                             NNQ_LPTR(buf + (size_t)(j * NTH + wv * 64) * 16), 16, 0, 0);
+        if ((s & 3) == 0) {
+            const int sb = s >> 2, sbc = min(sb, nblk - 1);
+            unsigned char *area = sba + (size_t)(sb & 1) * C::SBA;
+            __builtin_amdgcn_global_load_lds(NNQ_GPTR(hsrc + (size_t)sbc * 256),
+                                             NNQ_LPTR(area + C::HDR_OFF + (size_t)(wv * 64) * 16), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(NNQ_GPTR(xsrc + (size_t)sbc * 16),
+                                             NNQ_LPTR(area + C::XS_OFF + (size_t)(wv * 64) * 16), 16, 0, 0);
+#pragma unroll
+            for (int i = 0; i < C::AUXI; i++)
+                __builtin_amdgcn_global_load_lds(NNQ_GPTR(asrc[i] + (size_t)sbc * 512),
+                                                 NNQ_LPTR(area + C::AUX_OFF + (size_t)(i * NTH + wv * 64) * 16), 16, 0,
+                                                 0);
         }
     };
-    floatx4 acc[MT][NT];
+
+    // ---- per-lane state ----
+    floatx4 part[MT][NT];  // this super-block's sums of x * sc * q (MFMA accumulators)
+    floatx4 mins[MT][NT];  // min term, all super-blocks (MFMA accumulators)
+    float tot[MT][NT][4];  // sum over super-blocks of d_n * part
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < NT; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    int abase[2];
+        for (int j = 0; j < NT; j++) {
+            part[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            mins[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int hf = 0; hf < 2; hf++) abase[hf] = (c16 * 8 + ((4 * hf + q) ^ ((c16 >> 1) & 7))) * 16;
-    // A fragments of a stage in consumption order f = hf * MT + mt, read D ahead
-    constexpr int F = 2 * MT, D = 4;
-    auto read_frag = [&](const unsigned char *buf, int f) -> u32x4 {
-        return *reinterpret_cast<const u32x4 *>(buf + (f % MT) * 2048 + abase[f / MT]);
-    };
+            for (int e = 0; e < 4; e++) tot[i][j][e] = 0.f;
+        }
+    float dcol[NT];
+    uint32_t scw[NT][4];  // per byte group p: f16 (sc_2p, sc_2p+1 / 16)
+    int arow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) arow[mt] = wm * C::WM + mt * 16 + c16;
 
-    __builtin_amdgcn_s_barrier();  // the producers' prologue barrier
+#pragma unroll
+    for (int t = 0; t < NBUF - 1; t++) issue(t);
+
     for (int sb = 0; sb < nblk; sb++) {
+        const unsigned char *area = sba + (size_t)(sb & 1) * C::SBA;
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int s = 4 * sb + p;
-            __builtin_amdgcn_s_barrier();  // stage s: copied, dequantized
+            // this thread's copies of stage s (p is a constant once the loop is unrolled)
+            if (p == 0)
+                wait_vmcnt<rk_wait<NBUF, LPT, C::SB_EXTRA>(0)>();
+            else if (p == 1)
+                wait_vmcnt<rk_wait<NBUF, LPT, C::SB_EXTRA>(1)>();
+            else if (p == 2)
+                wait_vmcnt<rk_wait<NBUF, LPT, C::SB_EXTRA>(2)>();
+            else
+                wait_vmcnt<rk_wait<NBUF, LPT, C::SB_EXTRA>(3)>();
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage s - 1
+            __builtin_amdgcn_s_barrier();        // everyone's copies of stage s have landed
+            __builtin_amdgcn_sched_barrier(0);
+            issue(s + NBUF - 1);                 // into the buffer of stage s - 1
             const unsigned char *buf = ring + (size_t)(s % NBUF) * C::BUF;
-            const unsigned char *fb = f16b + (size_t)(s & 1) * C::F16B;
-            u32x4 bfr[2][NT], af[F];
+            u32x2 braw[NT];
 #pragma unroll
             for (int nt = 0; nt < NT; nt++)
+                braw[nt] = *reinterpret_cast<const u32x2 *>(
+                    buf + C::A_CH * 16 + ((((wn * NT + nt) * 2 + (G >> 1)) * 16 + c16) * 16) + 8 * (G & 1));
+            u32x4 af[2][MT];
 #pragma unroll
-                for (int hf = 0; hf < 2; hf++)
-                    bfr[hf][nt] = *reinterpret_cast<const u32x4 *>(fb + (((wn * NT + nt) * 2 + hf) * 64 + lane) * 16);
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int f = 0; f < D; f++) af[f] = read_frag(buf, f);
-            if (p == 0) decode_d(sb);
-            __builtin_amdgcn_sched_barrier(0);
+                for (int mt = 0; mt < MT; mt++) {
+                    const int r = arow[mt], kc = 4 * j + G;
+                    af[j][mt] = *reinterpret_cast<const u32x4 *>(buf + (size_t)(r * 8 + (kc ^ ((r >> 1) & 7))) * 16);
+                }
+            if (p == 0) {
+                // BlockQ4K header: d | dmin, scales[12] (get_scale_min_k4,
+                // crates/nn-core/src/layers/quantized/linear.rs:166-176)
 #pragma unroll
-            for (int f = 0; f < F; f++) {
-                if (f + D < F) af[f + D] = read_frag(buf, f + D);
-                const int hf = f / MT, mt = f % MT;
-                if (p == 0 && hf == 0) {  // a new super-block: rescale to its unit first
+                for (int nt = 0; nt < NT; nt++) {
+                    const u32x4 h = *reinterpret_cast<const u32x4 *>(area + C::HDR_OFF +
+                                                                     (size_t)((wn * NT + nt) * 16 + c16) * 16);
+                    dcol[nt] = f16_to_f32(h[0] & 0xFFFFu);
+                    const uint32_t sc03 = h[1] & 0x3F3F3F3Fu;
+                    const uint32_t sc47 = (h[3] & 0x0F0F0F0Fu) | ((h[1] >> 2) & 0x30303030u);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const uint32_t w = q < 2 ? sc03 : sc47;
+                        const uint32_t lo = (w >> (16 * (q & 1))) & 0xFFu, hi = (w >> (16 * (q & 1) + 8)) & 0xFFu;
+                        scw[nt][q] = f32_to_f16_bits((float)lo) | (f32_to_f16_bits(0.0625f * (float)hi) << 16);
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const uint32_t w0 = braw[nt][0], w1 = braw[nt][1];
+                    const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
+                    u32x4 b;
+                    if (j == 0)
+                        b = u32x4{pk_mul_bcast<0>(w0 & 0x000F000Fu, scw[nt][p]),
+                                  pk_mul_bcast<0>(w0s & 0x000F000Fu, scw[nt][p]),
+                                  pk_mul_bcast<0>(w1 & 0x000F000Fu, scw[nt][p]),
+                                  pk_mul_bcast<0>(w1s & 0x000F000Fu, scw[nt][p])};
+                    else
+                        b = u32x4{pk_mul_bcast<1>(w0 & 0x00F000F0u, scw[nt][p]),
+                                  pk_mul_bcast<1>(w0s & 0x00F000F0u, scw[nt][p]),
+                                  pk_mul_bcast<1>(w1 & 0x00F000F0u, scw[nt][p]),
+                                  pk_mul_bcast<1>(w1s & 0x00F000F0u, scw[nt][p])};
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+                        part[mt][nt] = mfma16x16x32_f16(af[j][mt], b,
+                                                        (p == 0 && j == 0) ? floatx4{0.f, 0.f, 0.f, 0.f} : part[mt][nt]);
+                }
+            }
+            if (p == 2) {
+                // min term of the super-block: one MFMA per tile whose 32 k are the four
+                // (x hi / lo) x (w hi / lo) cross products of its 8 sub-blocks: lane group G
+                // takes x part G & 1 (negated: the min term is subtracted) and w part G >> 1
+                u32x4 xa[MT], wb[NT];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    xa[mt] = *reinterpret_cast<const u32x4 *>(area + C::XS_OFF + (size_t)(arow[mt] * 2 + (G & 1)) * 16) ^
+                             0x80008000u;
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    wb[nt] = *reinterpret_cast<const u32x4 *>(
+                        area + C::AUX_OFF + (size_t)(((wn * NT + nt) * 2 + (G >> 1)) * 16 + c16) * 16);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) mins[mt][nt] = mfma16x16x32_f16(xa[mt], wb[nt], mins[mt][nt]);
+            }
+            if (p == 3) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                     for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-                        for (int e = 0; e < 4; e++) acc[mt][nt][e] *= ratio[nt];
-                }
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) acc[mt][nt] = mfma16x16x32_f16(af[f], bfr[hf][nt], acc[mt][nt]);
-                __builtin_amdgcn_sched_barrier(0);
+                        for (int e = 0; e < 4; e++) tot[mt][nt][e] += dcol[nt] * part[mt][nt][e];
             }
         }
     }
+    wait_vmcnt<0>();  // the trailing (unused) copies
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // every wave is done with the ring: it becomes the output tile
 
-    // Back to true scale (times 2^-8 * s_n, s_n the column's power of two for the min
-    // term, stored in the aux plane), then subtract the min term on the MFMA: A = the
-    // staged sub-block sums (hi, lo), B = dmin * m_j * s_n (hi, lo) from the aux plane.
-    const float *s_rows = reinterpret_cast<const float *>(a.aux + (size_t)ntile * nblk_all * 512);
-    float colf[NT];
-    const uint8_t *msrc[NT];
+    // y = (tot * 2^24 (the f16-subnormal codes) * 2^-8 * s_n + mins) * (2^8 / s_n) * 2^-s_row:
+    // the staged sums carry 2^-8 and the min-term operands s_n.  The tile is assembled in
+    // LDS (rows padded by 16 bytes, so the four row groups of a store land in distinct
+    // banks) and written out as 16-byte row chunks.
+    const bool f32out = KS > 1 || !a.y_bf16;
+    const int es = f32out ? 4 : 2, rs = BN * es + 16;
+    unsigned char *stg = smem;
+    // every factor is read before the first tile write (the compiler cannot tell the
+    // two LDS regions apart, so a read after a write would wait for it)
+    float rb[MT][4], f1[NT], f2[NT], bc[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) rb[mt][e] = epi[wm * C::WM + mt * 16 + 4 * G + e];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        const int tile = min(t0 + wn * NT + nt, ntile - 1);
-        const float s_n = s_rows[tile * 16 + c16];
-        const float f = ucur[nt] * 16777216.0f * 0.00390625f * s_n;
+        const int cl = (wn * NT + nt) * 16 + c16;
+        // s_n = 2^e is a normal power of two: 2^16 * s_n and 2^8 / s_n are exact
+        const uint32_t eb = __float_as_uint(epi[BM + cl]) >> 23;
+        f1[nt] = __uint_as_float((eb + 16u) << 23);
+        f2[nt] = __uint_as_float((262u - eb) << 23);
+        bc[nt] = (a.bias && KS == 1) ? a.bias[(int64_t)t0 * 16 + cl] : 0.0f;
+    }
+    float yv[MT][NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[mt][nt][e] *= f;
-        colf[nt] = 256.0f / s_n;  // exact: s_n is a power of two
-        msrc[nt] = a.aux + ((size_t)tile * nblk_all + sb0) * 512 + c16 * 16;
+            for (int e = 0; e < 4; e++)
+                yv[mt][nt][e] = (tot[mt][nt][e] * f1[nt] + mins[mt][nt][e]) * f2[nt] * rb[mt][e] + bc[nt];
+    if (f32out) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    *reinterpret_cast<float *>(stg + (wm * C::WM + mt * 16 + 4 * G + e) * rs +
+                                               ((wn * NT + nt) * 16 + c16) * 4) = yv[mt][nt][e];
+    } else {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    *reinterpret_cast<uint16_t *>(stg + (wm * C::WM + mt * 16 + 4 * G + e) * rs +
+                                                  ((wn * NT + nt) * 16 + c16) * 2) =
+                        (uint16_t)f32_to_bf16_bits(yv[mt][nt][e]);
     }
-    // min-term steps: 32 sub-blocks each (lane group q: the 8 sub-blocks of super-block
-    // 4 it + q of this workgroup's range); B two steps ahead, A one step ahead
-    const int nsub = K / 32, nit = (nblk + 3) / 4;
-    auto load_b = [&](int it, u32x4 (&bh)[NT], u32x4 (&bl)[NT]) {
-        const int sb = min(4 * it + q, nblk - 1);
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            bh[nt] = ldg128(msrc[nt] + (size_t)sb * 512);
-            bl[nt] = ldg128(msrc[nt] + (size_t)sb * 512 + 256);
-        }
-    };
-    auto load_a = [&](int it, u32x4 (&ah)[MT], u32x4 (&al)[MT]) {
-        const int sb = sb0 + min(4 * it + q, nblk - 1);
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const int row = min(m0 + mt * 16 + c16, M - 1);
-            ah[mt] = *reinterpret_cast<const u32x4 *>(sc.xs + (size_t)row * nsub + 8 * sb);
-            al[mt] = *reinterpret_cast<const u32x4 *>(sc.xs + (size_t)M * nsub + (size_t)row * nsub + 8 * sb);
-        }
-    };
-    u32x4 bh0[NT], bl0[NT], bh1[NT], bl1[NT], ah[MT], al[MT];
-    load_b(0, bh0, bl0);
-    load_b(1, bh1, bl1);
-    load_a(0, ah, al);
-    for (int it = 0; it < nit; it++) {
-        u32x4 bh[NT], bl[NT], ahc[MT], alc[MT];
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            bh[nt] = bh0[nt];
-            bl[nt] = bl0[nt];
-            bh0[nt] = bh1[nt];
-            bl0[nt] = bl1[nt];
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            ahc[mt] = ah[mt];
-            alc[mt] = al[mt];
-        }
-        load_b(it + 2, bh1, bl1);  // clamped past the end: unused
-        load_a(it + 1, ah, al);
-        // sub-blocks past the range (a partial last step) and rows past M contribute zero
-        const bool kin = 4 * it + q < nblk;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const bool ok = kin && m0 + mt * 16 + c16 < M;
-            // negated: the min term is subtracted
-            const u32x4 a1 = ok ? (ahc[mt] ^ 0x80008000u) : u32x4{0u, 0u, 0u, 0u};
-            const u32x4 a2 = ok ? (alc[mt] ^ 0x80008000u) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                acc[mt][nt] = mfma16x16x32_f16(a1, bh[nt], acc[mt][nt]);
-                acc[mt][nt] = mfma16x16x32_f16(a1, bl[nt], acc[mt][nt]);
-                acc[mt][nt] = mfma16x16x32_f16(a2, bh[nt], acc[mt][nt]);
-            }
-        }
-    }
-
-    // store: lane holds rows 4q + e of each 16 x 16 tile, column c16
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int64_t col = (int64_t)(t0 + wn * NT + nt) * 16 + c16;
-        if (col >= a.n) continue;
-        const float bcol = (a.bias && KS == 1) ? a.bias[col] : 0.0f;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int64_t row = m0 + mt * 16 + 4 * q + e;
-                if (row >= M) continue;
-                const float y = acc[mt][nt][e] * colf[nt] * sc.rowback[row] + bcol;
-                if (KS > 1)
-                    sc.ysplit[((int64_t)ks * M + row) * a.n + col] = y;
-                else if (a.y_bf16)
-                    reinterpret_cast<uint16_t *>(a.y)[row * a.n + col] = (uint16_t)f32_to_bf16_bits(y);
-                else
-                    reinterpret_cast<float *>(a.y)[row * a.n + col] = y;
-            }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    const int cpr = BN * es / 16;  // 16-byte chunks per row
+    unsigned char *ybase = KS > 1 ? reinterpret_cast<unsigned char *>(sc.ysplit + (int64_t)ks * M * a.n)
+                                  : reinterpret_cast<unsigned char *>(a.y);
+    for (int c = tid; c < BM * cpr; c += NTH) {
+        const int rl = c / cpr, ch = c - rl * cpr;
+        if (m0 + rl >= M) break;  // rows run in order: the rest are past M as well
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + rl * rs + ch * 16);
+        *reinterpret_cast<u32x4 *>(ybase + ((int64_t)(m0 + rl) * a.n + (int64_t)t0 * 16) * es + ch * 16) = v;
     }
 }
 
@@ -408,18 +402,18 @@ __global__ __launch_bounds__(256) void gemm_finalize_kernel(const float *ys, int
         reinterpret_cast<float *>(y)[i] = v;
 }
 
-template <int BN, int NBUF>
-int launch_ws(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    using C = WS<BN, NBUF>;
+template <int BN, int NBUF, int WGN>
+int launch_rk(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
+    using C = RK<BN, NBUF, WGN>;
     static bool attr_set = false;  // idempotent attribute write; races only repeat it
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_ws_kernel<BN, NBUF>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_rk_kernel<BN, NBUF, WGN>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
     }
     const int nct = (int)((a.ntile * 16 + BN - 1) / BN), nrt = (int)((a.m + C::BM - 1) / C::BM);
-    hipLaunchKernelGGL((gemm_q4k_ws_kernel<BN, NBUF>), dim3((unsigned)(nct * nrt * sc.ksplit)), dim3(C::NTH), C::LDS,
+    hipLaunchKernelGGL((gemm_q4k_rk_kernel<BN, NBUF, WGN>), dim3((unsigned)(nct * nrt * sc.ksplit)), dim3(C::NTH), C::LDS,
                        st, a, sc);
     int e = (int)hipGetLastError();
     if (e || sc.ksplit == 1) return e;
@@ -437,7 +431,8 @@ int launch_ws(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
 // until there are at least 256 workgroups (one per CU), or as far as it goes.
 // Returns the K split, or 0 when the shape does not fit.
 int gemm_ring_plan(const GemmArgs &a, int *bn) {
-    if (!a.x_bf16 || a.m < 128 || a.nblk < 1) return 0;
+    // (the output tile is written in 16-byte chunks)
+    if (!a.x_bf16 || a.m < 128 || a.nblk < 1 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
     const int64_t ncols = a.ntile * 16, nrt = (a.m + 127) / 128;
     int b = 0;
     if (ncols % 192 == 0)
@@ -459,7 +454,9 @@ int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     const int ksplit = gemm_ring_plan(a, &bn);
     if (ksplit == 0 || sc.ksplit != ksplit || (ksplit > 1 && !sc.ysplit)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
-    return bn == 192 ? launch_ws<192, 4>(a, sc, st) : launch_ws<128, 4>(a, sc, st);
+    static const int wgn = getenv("NNQ_RK_WGN") ? atoi(getenv("NNQ_RK_WGN")) : 2;
+    if (wgn == 4) return bn == 192 ? launch_rk<192, 4, 4>(a, sc, st) : launch_rk<128, 4, 4>(a, sc, st);
+    return bn == 192 ? launch_rk<192, 4, 2>(a, sc, st) : launch_rk<128, 4, 2>(a, sc, st);
 }
 
 }  // namespace nnq

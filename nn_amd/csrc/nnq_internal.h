@@ -100,7 +100,7 @@ int launch_gemm_q4k(const GemmArgs &a, void *stream);
 size_t gemm_scratch_bytes(const GemmArgs &a);
 // staged activation (gemm_prep_kernel): P = 1 (bf16 x) or 2 (f32 x, hi + lo planes)
 struct GemmScratch {
-    uint16_t *xh;      // [P][m][k] f16 of x * 2^s_row (odd sub-blocks * 2^-4 for the ring kernel)
+    uint16_t *xh;      // [P][m][k] f16 of x * 2^s_row
     uint16_t *xs;      // [2][m][k / 32] f16 hi / lo of 2^-8 * sum(x * 2^s_row) per 32
     float *rowback;    // [m] 2^-s_row
     int ksplit;        // K split of the ring kernel (1: none)
