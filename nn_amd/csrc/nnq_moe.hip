@@ -23,6 +23,8 @@
 // and 8 scale bytes per lane and feeds two 16x16x32 bf16 MFMAs per 16 token rows.
 // Activations: bf16 input is used as is (exact); f32 input and the SwiGLU output h
 // are carried as bf16 hi + lo pairs (two MFMAs, ~2^-17 relative).
+#include <type_traits>
+
 #include "nnq_device.h"
 #include "nnq_internal.h"
 
@@ -112,6 +114,13 @@ __device__ __forceinline__ void fp4_b_operands(const uint8_t *codes, const uint8
 }
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+
+// s_waitcnt vmcnt(N) only (expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 }  // namespace
 
@@ -307,182 +316,244 @@ struct MoeRun {
     float limit;
 };
 
-constexpr int kMoeRows = 64;  // token rows per pass (4 MFMA row tiles)
-constexpr int kMoeKbc = 8;    // 32-row blocks of K staged in LDS per chunk
-constexpr int kMoeAst = kMoeKbc * 32 + 8;  // LDS row stride of a staged activation chunk (bf16)
+// Column streams.  gate_up: stream s = the pair of 32-column blocks (gate s, up I/32 + s),
+// both owned by one wave, so the SwiGLU epilogue needs no exchange; down: stream s =
+// block s.  Workgroup (expert, group g) takes streams [g S / G, (g + 1) S / G), one per
+// wave (rounds when a group has more streams than waves); every wave streams its
+// blocks' weights over all of K with the loads kPf k-blocks ahead in registers.
+// The expert's token rows (up to 64 per pass, P bf16 planes) are shared through an LDS
+// ring of kNbuf chunks of kCkb k-blocks, copied kNbuf - 1 chunks ahead with
+// global_load_lds (one barrier per chunk).
+constexpr int kMoeWaves = 12;
+constexpr int kMoeGroups = 8;  // groups per expert (E = 32: one workgroup per CU)
+constexpr int kCkb = 1;        // k-blocks (32 rows of K) per chunk
+constexpr int kNbuf = 4;       // LDS ring depth (chunks)
+constexpr int kPf = 3;         // weight prefetch distance (chunks)
 
-__host__ __device__ constexpr size_t moe_lds_bytes(int nw, int P, bool gu) {
-    return (size_t)P * kMoeRows * kMoeAst * 2 > (gu ? (size_t)(nw / 2) * kMoeRows * 33 * 4 : 0)
-               ? (size_t)P * kMoeRows * kMoeAst * 2
-               : (size_t)(nw / 2) * kMoeRows * 33 * 4;
+template <int P>
+struct MoeK {
+    static constexpr int NTH = kMoeWaves * 64;
+    static constexpr int ROWG = kCkb * 4;               // 16-byte granules per row and chunk
+    static constexpr int ACH = P * 64 * ROWG;           // granules per chunk
+    static constexpr int LPA = (ACH + NTH - 1) / NTH;   // copy instructions per thread and chunk
+    static constexpr int BUF = LPA * NTH * 16;
+    static constexpr size_t LDS = (size_t)kNbuf * BUF;
+    static_assert(ROWG == 4 || ROWG == 8, "row swizzle within the row's granules");
+};
+
+// slot of the 16-byte chunk kc of row r inside the row's ROWG granules: rows r and r + 2
+// (ROWG 8) or r + 2 .. r + 6 (ROWG 4) land in distinct banks
+template <int ROWG>
+__device__ __forceinline__ int moe_slot(int kc, int r) {
+    return kc ^ ((r >> 1) & (ROWG - 1));
 }
 
-// Workgroup = (expert, NW column blocks): for gate_up (GU) waves 0 .. NW/2 - 1 own gate
-// blocks and waves NW/2 .. NW - 1 the matching up blocks; for down wave w owns block w
-// of its group.  Per chunk of 8 K-blocks the workgroup stages the expert's token rows
-// (P bf16 planes) in LDS once; every wave then streams its own weight block and reuses
-// the staged rows.  The activation loads are issued before the weight loads, so the
-// wait before the LDS store does not cover the weights.
-template <int NW, int P, bool GU>
-__global__ __launch_bounds__(NW * 64) void moe_expert_kernel(MoeDev d, MoeScratch sc, MoeRun run) {
-    constexpr int NTH = NW * 64;
-    constexpr int APIECE = P * kMoeRows * kMoeKbc * 4;  // 16-byte activation pieces per chunk
-    constexpr int APT = (APIECE + NTH - 1) / NTH;
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    uint16_t *As = reinterpret_cast<uint16_t *>(smem);  // [P][kMoeRows][kMoeAst]
-    float *gbuf = reinterpret_cast<float *>(smem);      // gate_up epilogue: [NW/2][kMoeRows][33]
+__host__ __device__ constexpr int moe_streams(bool gu, int64_t H, int64_t I) { return (int)(gu ? I / 32 : H / 32); }
 
+template <int P, bool GU>
+__global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, MoeScratch sc, MoeRun run) {
+    using C = MoeK<P>;
+    constexpr int NBW = GU ? 2 : 1, NTH = C::NTH, LPA = C::LPA;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int64_t H = d.H, I = d.I;
-    const int64_t K = GU ? H : I, KB = K / 32;
-    const int64_t NB = GU ? 2 * I / 32 : H / 32;
-    const int64_t ngrp = GU ? (I / 32) / (NW / 2) : (NB + NW - 1) / NW;
-    const int64_t e = blockIdx.x / ngrp, grp = blockIdx.x % ngrp;
+    const int64_t K = GU ? H : I, KB = K / 32, NB = GU ? 2 * I / 32 : H / 32;
+    const int S = moe_streams(GU, H, I);
+    // Workgroup ids go round-robin over the 8 XCDs; when the count allows, XCD x gets a
+    // contiguous run of (expert, group) items, i.e. whole experts, so an expert's
+    // activation rows are read into one XCD's L2 only.
+    const int nwg = (int)gridDim.x, bid = (int)blockIdx.x;
+    const int item = (nwg % 8 == 0) ? (bid % 8) * (nwg / 8) + bid / 8 : bid;
+    const int64_t e = item / kMoeGroups, g = item % kMoeGroups;
     const int32_t r0 = sc.off[e], ne = sc.off[e + 1] - r0;
     if (ne == 0) return;  // workgroup-uniform
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int p = lane >> 4, l16 = lane & 15;
-    int64_t nb, col0;
-    int half = 0;
-    if (GU) {
-        half = wv / (NW / 2);
-        const int64_t cb = grp * (NW / 2) + wv % (NW / 2);
-        col0 = cb * 32;  // gate column of this wave's block
-        nb = half * (I / 32) + cb;
-    } else {
-        nb = grp * NW + wv;
-        col0 = nb * 32;
-    }
-    const bool active = nb < NB;  // tail waves of the last down group join the barriers only
-    const int64_t nbs = active ? nb : 0;
-    const uint8_t *cq = (GU ? d.gu_q : d.dn_q) + (e * NB + nbs) * KB * 512;
-    const uint8_t *cs = (GU ? d.gu_s : d.dn_s) + (e * NB + nbs) * KB * 32;
+    const int s_lo = (int)(g * S / kMoeGroups), s_hi = (int)((g + 1) * S / kMoeGroups);
+    const int nch = (int)(KB / kCkb);  // K / 32 is a multiple of kCkb (checked by the host)
 
-    for (int32_t m0 = 0; m0 < ne; m0 += kMoeRows) {
-        const int mtn = (ne - m0) >= kMoeRows ? 4 : (ne - m0 + 15) / 16;  // live row tiles
-        floatx4 acc[4][2];
+    for (int32_t m0 = 0; m0 < ne; m0 += 64) {
+        const int mtn = (ne - m0) >= 64 ? 4 : (ne - m0 + 15) / 16;  // live row tiles
+        // copy sources of this pass: granule c -> (plane, row, slot); chunk ch at + ch * 64 k
+        const uint16_t *asrc[LPA];
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) acc[mt][0] = acc[mt][1] = zero4();
-        for (int64_t kb0 = 0; kb0 < KB; kb0 += kMoeKbc) {
-            const int kbc = (KB - kb0) < kMoeKbc ? (int)(KB - kb0) : kMoeKbc;
-            // activation pieces of this chunk (zeros past the expert's rows / the chunk)
-            u32x4 ra[APT];
-#pragma unroll
-            for (int i = 0; i < APT; i++) {
-                const int c = tid + i * NTH;
-                ra[i] = u32x4{0u, 0u, 0u, 0u};
-                if (c < APIECE) {
-                    const int pl = c / (kMoeRows * kMoeKbc * 4), rem = c % (kMoeRows * kMoeKbc * 4);
-                    const int row = rem / (kMoeKbc * 4), c16 = rem % (kMoeKbc * 4);
-                    if (m0 + row < ne && c16 < 4 * kbc) {
-                        const int64_t kk = kb0 * 32 + c16 * 8;
-                        const uint16_t *src =
-                            GU ? run.xa[pl] + (int64_t)sc.stok[r0 + m0 + row] * H + kk
-                               : sc.hb + (int64_t)pl * run.A * I + (int64_t)(r0 + m0 + row) * I + kk;
-                        ra[i] = *reinterpret_cast<const u32x4 *>(src);
-                    }
-                }
-            }
-            // this wave's weight block for the chunk
-            u32x2 bcq[kMoeKbc], bcs[kMoeKbc];
-#pragma unroll
-            for (int j = 0; j < kMoeKbc; j++) {
-                bcq[j] = bcs[j] = u32x2{0u, 0u};
-                if (active && j < kbc) {
-                    bcq[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(cq + (kb0 + j) * 512 + 8 * lane));
-                    bcs[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(cs + (kb0 + j) * 32 + 8 * p));
-                }
-            }
-            __syncthreads();  // the previous chunk's rows have been read
-#pragma unroll
-            for (int i = 0; i < APT; i++) {
-                const int c = tid + i * NTH;
-                if (c < APIECE) {
-                    const int pl = c / (kMoeRows * kMoeKbc * 4), rem = c % (kMoeRows * kMoeKbc * 4);
-                    const int row = rem / (kMoeKbc * 4), c16 = rem % (kMoeKbc * 4);
-                    *reinterpret_cast<u32x4 *>(As + (pl * kMoeRows + row) * kMoeAst + c16 * 8) = ra[i];
-                }
-            }
-            __syncthreads();
-            if (active) {
-#pragma unroll
-                for (int j = 0; j < kMoeKbc; j++) {
-                    if (j >= kbc) break;
-                    uint32_t r[8];
-                    fp4_rows(bcq[j], bcs[j], r);
-                    u32x4 be, bo;
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        bo[q] = __builtin_amdgcn_perm(r[2 * q + 1], r[2 * q], 0x05040100u);  // column 2c + 1
-                        be[q] = __builtin_amdgcn_perm(r[2 * q + 1], r[2 * q], 0x07060302u);  // column 2c
-                    }
-#pragma unroll
-                    for (int mt = 0; mt < 4; mt++) {
-                        if (mt >= mtn) break;  // wave-uniform
-#pragma unroll
-                        for (int pl = 0; pl < P; pl++) {
-                            const u32x4 a = *reinterpret_cast<const u32x4 *>(
-                                As + (pl * kMoeRows + mt * 16 + l16) * kMoeAst + j * 32 + 8 * p);
-                            acc[mt][0] = mfma16x16x32_bf16(a, be, acc[mt][0]);
-                            acc[mt][1] = mfma16x16x32_bf16(a, bo, acc[mt][1]);
-                        }
-                    }
-                }
-            }
+        for (int j = 0; j < LPA; j++) {
+            const int c = min(j * NTH + tid, C::ACH - 1);
+            const int pl = c / (64 * C::ROWG), rem = c % (64 * C::ROWG);
+            const int r = rem / C::ROWG, slot = rem % C::ROWG;
+            const int kc = moe_slot<C::ROWG>(slot, r);  // the row's 16-byte chunk held at this slot
+            const int32_t rr = r0 + m0 + min(r, ne - m0 - 1);  // rows past the expert repeat its last row
+            asrc[j] = (GU ? run.xa[pl] + (int64_t)sc.stok[rr] * H : sc.hb + (int64_t)pl * run.A * I + (int64_t)rr * I) +
+                      8 * kc;
         }
-        // lane holds rows 4p + i of each tile; tile 0 = columns 2 * l16, tile 1 = 2 * l16 + 1
-        if (GU) {
-            __syncthreads();  // the staged rows are dead; gbuf reuses their LDS
-            if (half == 0) {
+        auto issue = [&](int ch) {
+            const int cv = min(ch, nch - 1);  // past the end: re-copy the last chunk
+            unsigned char *buf = smem + (size_t)(ch % kNbuf) * C::BUF;
 #pragma unroll
-                for (int mt = 0; mt < 4; mt++)
+            for (int j = 0; j < LPA; j++)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(asrc[j] + (int64_t)cv * kCkb * 32),
+                    (__attribute__((address_space(3))) void *)(buf + (size_t)(j * NTH + wv * 64) * 16), 16, 0, 0);
+        };
+        const int nround = (s_hi - s_lo + kMoeWaves - 1) / kMoeWaves;
+        for (int rd = 0; rd < nround; rd++) {
+            const int st = s_lo + rd * kMoeWaves + wv;
+            const bool active = st < s_hi;  // idle waves still copy and join the barriers
+            // buffer resources on the wave's blocks (scalar registers, range-checked): a
+            // per-lane offset plus a scalar per-k-block offset, no per-load address VALU
+            __amdgpu_buffer_rsrc_t rq[NBW], rs[NBW];
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-#pragma unroll
-                        for (int o = 0; o < 2; o++) {
-                            const int c = 2 * l16 + o;
-                            gbuf[((wv % (NW / 2)) * kMoeRows + mt * 16 + 4 * p + i) * 33 + c] =
-                                acc[mt][o][i] + d.gu_b[e * 2 * I + col0 + c];
-                        }
+            for (int b = 0; b < NBW; b++) {
+                const int64_t nb = active ? (GU ? (b == 0 ? st : I / 32 + st) : st) : 0;
+                rq[b] = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<uint8_t *>((GU ? d.gu_q : d.dn_q) + (e * NB + nb) * KB * 512), 0, (int)(KB * 512),
+                    0x00020000);
+                rs[b] = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<uint8_t *>((GU ? d.gu_s : d.dn_s) + (e * NB + nb) * KB * 32), 0, (int)(KB * 32),
+                    0x00020000);
             }
-            __syncthreads();
-            if (half == 1) {
+            const int qo = 8 * lane, so = 8 * p;
+            // weight ring in registers: slot (ch % (kPf + 1)) holds chunk ch
+            u32x2 wq[kPf + 1][kCkb][NBW], ws[kPf + 1][kCkb][NBW];
+            auto wload = [&](int ch, int slot) {
+                const int cv = min(ch, nch - 1);
 #pragma unroll
-                for (int mt = 0; mt < 4; mt++)
+                for (int j = 0; j < kCkb; j++)
+#pragma unroll
+                    for (int b = 0; b < NBW; b++) {
+                        const int kb = cv * kCkb + j;
+                        // cache policy 2: non-temporal (every weight byte is read once per call)
+                        wq[slot][j][b] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq[b], qo, kb * 512, 2));
+                        ws[slot][j][b] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs[b], so, kb * 32, 2));
+                    }
+            };
+            floatx4 acc[NBW][4][2];
+#pragma unroll
+            for (int b = 0; b < NBW; b++)
+#pragma unroll
+                for (int mt = 0; mt < 4; mt++) acc[b][mt][0] = acc[b][mt][1] = zero4();
+
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __syncthreads();  // the previous round / pass has finished reading the ring
+            // Every step issues the same batch on every wave: the weights of chunk t + kPf
+            // (clamped into range; idle waves load block 0), then the copies of chunk
+            // t + kNbuf - 1.  The prologue runs steps t = 1 - kNbuf .. -1 the same way, so
+            // before chunk ch is read exactly kNbuf - 2 batches follow its copies.
+            auto step = [&](int t, int wslot) {
+                wload(max(t + kPf, 0), wslot);
+                issue(t + kNbuf - 1);
+            };
+#pragma unroll
+            for (int t = 1 - kNbuf; t < 0; t++) step(t, ((t + kPf) % (kPf + 1) + (kPf + 1)) % (kPf + 1));
+            // MTN: live 16-row tiles of this pass (a constant per instantiation)
+            auto pass = [&](auto mtn_c) {
+                constexpr int MTN = decltype(mtn_c)::value;
+                auto body = [&](int ch, int slot) {
+                    wait_vmcnt<(kNbuf - 2) * (LPA + 2 * kCkb * NBW)>();  // this thread's copies of chunk ch
+                    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of chunk ch - 1
+                    __builtin_amdgcn_s_barrier();        // everyone's copies of chunk ch have landed
+                    __builtin_amdgcn_sched_barrier(0);
+                    step(ch, (slot + kPf) % (kPf + 1));
+                    if (!active) return;
+                    const unsigned char *buf = smem + (size_t)(ch % kNbuf) * C::BUF;
+                    u32x4 a[kCkb][MTN][P];
+#pragma unroll
+                    for (int j = 0; j < kCkb; j++)
+#pragma unroll
+                        for (int mt = 0; mt < MTN; mt++)
+#pragma unroll
+                            for (int pl = 0; pl < P; pl++) {
+                                const int rr = mt * 16 + l16, kc = 4 * j + p;
+                                a[j][mt][pl] = *reinterpret_cast<const u32x4 *>(
+                                    buf + (size_t)((pl * 64 + rr) * C::ROWG + moe_slot<C::ROWG>(kc, rr)) * 16);
+                            }
+#pragma unroll
+                    for (int j = 0; j < kCkb; j++) {
+                        u32x4 be[NBW], bo[NBW];
+#pragma unroll
+                        for (int b = 0; b < NBW; b++) {
+                            uint32_t r[8];
+                            fp4_rows(wq[slot][j][b], ws[slot][j][b], r);
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                bo[b][q] = __builtin_amdgcn_perm(r[2 * q + 1], r[2 * q], 0x05040100u);  // column 2c + 1
+                                be[b][q] = __builtin_amdgcn_perm(r[2 * q + 1], r[2 * q], 0x07060302u);  // column 2c
+                            }
+                        }
+#pragma unroll
+                        for (int mt = 0; mt < MTN; mt++)
+#pragma unroll
+                            for (int pl = 0; pl < P; pl++)
+#pragma unroll
+                                for (int b = 0; b < NBW; b++) {
+                                    acc[b][mt][0] = mfma16x16x32_bf16(a[j][mt][pl], be[b], acc[b][mt][0]);
+                                    acc[b][mt][1] = mfma16x16x32_bf16(a[j][mt][pl], bo[b], acc[b][mt][1]);
+                                }
+                    }
+                };
+                // full groups of kPf + 1 chunks (slot = position in the group), then the rest
+                const int nfull = nch - nch % (kPf + 1);
+                for (int c0 = 0; c0 < nfull; c0 += kPf + 1) {
+#pragma unroll
+                    for (int u = 0; u < kPf + 1; u++) body(c0 + u, u);
+                }
+#pragma unroll
+                for (int u = 0; u < kPf; u++)
+                    if (nfull + u < nch) body(nfull + u, u);
+            };
+            switch (mtn) {
+            case 1: pass(std::integral_constant<int, 1>{}); break;
+            case 2: pass(std::integral_constant<int, 2>{}); break;
+            case 3: pass(std::integral_constant<int, 3>{}); break;
+            default: pass(std::integral_constant<int, 4>{}); break;
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // trailing copies and weight loads (unused)
+            if (!active) continue;
+            // lane holds rows 4p + i of each tile; acc[.][.][0]: column 2 * l16 of the block, [1]: 2 * l16 + 1
+            if (GU) {
+                const int64_t col0 = (int64_t)st * 32;
+#pragma unroll
+                for (int mt = 0; mt < 4; mt++) {
+                    if (mt >= mtn) break;
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const int32_t r = m0 + mt * 16 + 4 * p + i;
                         if (r >= ne) continue;
+                        uint32_t hh = 0, hl = 0;
 #pragma unroll
                         for (int o = 0; o < 2; o++) {
-                            const int c = 2 * l16 + o;
-                            const float g = gbuf[((wv % (NW / 2)) * kMoeRows + mt * 16 + 4 * p + i) * 33 + c];
-                            const float u = acc[mt][o][i] + d.gu_b[e * 2 * I + I + col0 + c];
+                            const int64_t c = col0 + 2 * l16 + o;
+                            const float gt = acc[0][mt][o][i] + d.gu_b[e * 2 * I + c];
+                            const float up = acc[1][mt][o][i] + d.gu_b[e * 2 * I + I + c];
                             // silu (crates/nn-core/src/dyn_tensor/ops/math.rs:140), clamped to +-limit
-                            float sg = g / (1.0f + expf(-g));
+                            float sg = gt / (1.0f + expf(-gt));
                             sg = sg < -run.limit ? -run.limit : (sg > run.limit ? run.limit : sg);
-                            const float h = sg * u;
-                            const uint16_t hh = bf16_rne(h);
-                            const int64_t o2 = (int64_t)(r0 + r) * I + col0 + c;
-                            sc.hb[o2] = hh;
-                            sc.hb[run.A * I + o2] = bf16_rne(h - bf16_to_f32(hh));
+                            const float h = sg * up;
+                            const uint32_t bh = bf16_rne(h);
+                            hh |= bh << (16 * o);
+                            hl |= (uint32_t)bf16_rne(h - bf16_to_f32(bh)) << (16 * o);
                         }
-                    }
-            }
-        } else if (active) {
-#pragma unroll
-            for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int32_t r = m0 + mt * 16 + 4 * p + i;
-                    if (r >= ne) continue;
-#pragma unroll
-                    for (int o = 0; o < 2; o++) {
-                        const int64_t col = col0 + 2 * l16 + o;
-                        sc.yb[(int64_t)(r0 + r) * H + col] = acc[mt][o][i] + d.dn_b[e * H + col];
+                        const int64_t o2 = (int64_t)(r0 + r) * I + col0 + 2 * l16;
+                        *reinterpret_cast<uint32_t *>(sc.hb + o2) = hh;
+                        *reinterpret_cast<uint32_t *>(sc.hb + run.A * I + o2) = hl;
                     }
                 }
+            } else {
+                const int64_t col0 = (int64_t)st * 32 + 2 * l16;
+                const float b0 = d.dn_b[e * H + col0], b1 = d.dn_b[e * H + col0 + 1];
+#pragma unroll
+                for (int mt = 0; mt < 4; mt++) {
+                    if (mt >= mtn) break;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int32_t r = m0 + mt * 16 + 4 * p + i;
+                        if (r >= ne) continue;
+                        *reinterpret_cast<float2 *>(sc.yb + (int64_t)(r0 + r) * H + col0) =
+                            float2{acc[0][mt][0][i] + b0, acc[0][mt][1][i] + b1};
+                    }
+                }
+            }
         }
-        __syncthreads();  // LDS is restaged by the next row pass
     }
 }
 
@@ -574,33 +645,19 @@ size_t moe_scratch_bytes(int64_t T, int64_t E, int64_t H, int64_t I, int k, int 
            al256((size_t)2 * A * I * 2) + al256(A * H * 4) + 256;
 }
 
-template <int NW, int P, bool GU>
-static int launch_expert_nw(const MoeDev &d, const MoeScratch &sc, const MoeRun &run, hipStream_t st) {
-    constexpr size_t lds = moe_lds_bytes(NW, P, GU);
+template <int P, bool GU>
+static int launch_stream(const MoeDev &d, const MoeScratch &sc, const MoeRun &run, hipStream_t st) {
+    constexpr size_t lds = MoeK<P>::LDS;
     static bool attr_set = false;  // idempotent attribute write; races only repeat it
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_expert_kernel<NW, P, GU>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_stream_kernel<P, GU>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
     }
-    const int64_t NB = GU ? 2 * d.I / 32 : d.H / 32;
-    const int64_t ngrp = GU ? (d.I / 32) / (NW / 2) : (NB + NW - 1) / NW;
-    hipLaunchKernelGGL((moe_expert_kernel<NW, P, GU>), dim3((unsigned)(d.E * ngrp)), dim3(NW * 64), lds, st, d, sc,
-                       run);
+    hipLaunchKernelGGL((moe_stream_kernel<P, GU>), dim3((unsigned)(d.E * kMoeGroups)), dim3(kMoeWaves * 64), lds, st,
+                       d, sc, run);
     return (int)hipGetLastError();
-}
-
-// gate_up: NW / 2 column-block pairs, the largest of 3, 2, 1 dividing I / 32; down: 6 blocks
-template <int P, bool GU>
-static int launch_expert(const MoeDev &d, const MoeScratch &sc, const MoeRun &run, hipStream_t st) {
-    if (GU) {
-        const int64_t cb = d.I / 32;
-        if (cb % 3 == 0) return launch_expert_nw<6, P, GU>(d, sc, run, st);
-        if (cb % 2 == 0) return launch_expert_nw<4, P, GU>(d, sc, run, st);
-        return launch_expert_nw<2, P, GU>(d, sc, run, st);
-    }
-    return launch_expert_nw<6, P, GU>(d, sc, run, st);
 }
 
 int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const float *logits, int k, float limit,
@@ -635,11 +692,11 @@ int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const floa
         run.xa[1] = sc.xb + n;
     }
     if (x_bf16)
-        e = launch_expert<1, true>(d, sc, run, st);
+        e = launch_stream<1, true>(d, sc, run, st);
     else
-        e = launch_expert<2, true>(d, sc, run, st);
+        e = launch_stream<2, true>(d, sc, run, st);
     if (e) return e;
-    e = launch_expert<2, false>(d, sc, run, st);
+    e = launch_stream<2, false>(d, sc, run, st);
     if (e) return e;
     switch (k) {
 #define NNQ_COMB(K)                                                                                  \
