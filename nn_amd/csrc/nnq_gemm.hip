@@ -38,10 +38,8 @@ namespace {
 
 inline size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
-bool use_ring(const GemmArgs &a) {
-    static const int ring = getenv("NNQ_GEMM_OLD") ? 0 : 1;
-    return ring && gemm_ring_plan(a, nullptr) > 0;
-}
+// the LDS-ring kernel (nnq_gemm_ring.hip) takes every shape its plan accepts
+bool use_ring(const GemmArgs &a) { return gemm_ring_plan(a, nullptr) > 0; }
 
 // scratch layout: xh | xs | rowback | ysplit; base null: offsets from 0 (sizing)
 GemmScratch carve(void *base, const GemmArgs &a, size_t *bytes) {
@@ -91,9 +89,11 @@ __device__ __forceinline__ uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
 }  // namespace
 
 // ---------------------------------------------------------------------------------
-// Activation staging: one workgroup per row.
+// Activation staging: one workgroup per row.  NG > 0: the row is read once into
+// registers (NG groups of 8 per thread, K <= 2048 NG), its max found, then converted
+// from the registers; NG = 0: any K, the row is read twice.
 // ---------------------------------------------------------------------------------
-template <int P>
+template <int P, int NG>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf16, int64_t m, int64_t k,
                                                         GemmScratch sc) {
     const int64_t row = blockIdx.x;
@@ -102,17 +102,38 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf1
     __shared__ float scale_s;
     const int64_t ng = k / 8;
     const int64_t xoff = row * k;
+    constexpr int NR = NG > 0 ? NG : 1;
+    float vr[NR][8];
     float amax = 0.0f;
-    for (int64_t g = tid; g < ng; g += 256) {
-        float v[8];
-        load8(x, x_bf16, xoff + 8 * g, v);
-        float sum = 0.0f;
+    if (NG > 0) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            amax = fmaxf(amax, fabsf(v[i]));
-            sum += v[i];
+        for (int j = 0; j < NR; j++) {
+            const int64_t g = tid + 256 * j;
+            if (g < ng) load8(x, x_bf16, xoff + 8 * g, vr[j]);
         }
-        if (!(fabsf(sum) <= 3.0e38f)) amax = INFINITY;  // NaN / inf in the row
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            if (tid + 256 * j >= ng) break;
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                amax = fmaxf(amax, fabsf(vr[j][i]));
+                sum += vr[j][i];
+            }
+            if (!(fabsf(sum) <= 3.0e38f)) amax = INFINITY;  // NaN / inf in the row
+        }
+    } else {
+        for (int64_t g = tid; g < ng; g += 256) {
+            float v[8];
+            load8(x, x_bf16, xoff + 8 * g, v);
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                amax = fmaxf(amax, fabsf(v[i]));
+                sum += v[i];
+            }
+            if (!(fabsf(sum) <= 3.0e38f)) amax = INFINITY;
+        }
     }
     amax = wave_max(amax);
     if (lane == 0) wred[wv] = amax;
@@ -131,9 +152,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf1
     const int64_t nsub = k / 32;
     // the four lanes of a quad hold one 32-element block (ng is a multiple of 4 and the
     // stride 256 keeps quads aligned), so the DPP sum only reads lanes of the same quad
-    for (int64_t g = tid; g < ng; g += 256) {
-        float v[8];
-        load8(x, x_bf16, xoff + 8 * g, v);
+    auto convert = [&](int64_t g, const float (&v)[8]) {
         u32x4 H, L;
         float sum = 0.0f;
 #pragma unroll
@@ -155,6 +174,20 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf1
             split_f16(tot * 0.00390625f, th, tl);  // 2^-8 keeps 32 * 2^15 inside f16
             sc.xs[row * nsub + g / 4] = (uint16_t)th;
             sc.xs[m * nsub + row * nsub + g / 4] = (uint16_t)tl;
+        }
+    };
+    if (NG > 0) {
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int64_t g = tid + 256 * j;
+            if (g >= ng) break;  // uniform across each quad (ng % 4 == 0)
+            convert(g, vr[j]);
+        }
+    } else {
+        for (int64_t g = tid; g < ng; g += 256) {
+            float v[8];
+            load8(x, x_bf16, xoff + 8 * g, v);
+            convert(g, v);
         }
     }
 }
@@ -450,9 +483,17 @@ static int launch_p(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
     return launch_cfg<32, 64, 2, 2, P>(a, sc, st);
 }
 
+template <int P, int NG>
+static void launch_prep_ng(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_prep_kernel<P, NG>), dim3((unsigned)a.m), dim3(256), 0, st, a.x, a.x_bf16, a.m, a.k, sc);
+}
+// the row in registers when K <= 2048 * 6 (Qwen3-8B: 4096 and 12288)
 template <int P>
 static void launch_prep(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_prep_kernel<P>), dim3((unsigned)a.m), dim3(256), 0, st, a.x, a.x_bf16, a.m, a.k, sc);
+    const int64_t per = (a.k / 8 + 255) / 256;  // groups of 8 per thread
+    if (per <= 2) return launch_prep_ng<P, 2>(a, sc, st);
+    if (per <= 6) return launch_prep_ng<P, 6>(a, sc, st);
+    return launch_prep_ng<P, 0>(a, sc, st);
 }
 
 int launch_gemm_q4k(const GemmArgs &a, void *stream) {
