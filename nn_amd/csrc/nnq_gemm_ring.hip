@@ -24,9 +24,10 @@
 // The per-super-block factor d: the MFMAs of a super-block accumulate from zero into
 // AGPR partial sums (so the dequantization VALU work issues beside the MFMAs), and at the
 // super-block's end every lane adds d_n * partial into its f32 totals.  The min term
-// dmin * m_j * sum(x over the sub-block) runs after the main loop on the MFMA from the
-// weight's aux plane (dmin * m_j * s_n precomputed at upload as exact f16 hi + lo) and
-// the staged sub-block sums of x (hi + lo).
+// dmin * m_j * sum(x over the sub-block) is one more MFMA per tile and super-block
+// (in its third stage), into accumulators of its own, from the weight's aux plane
+// (dmin * m_j * s_n precomputed at upload as exact f16 hi + lo) and the staged
+// sub-block sums of x (hi + lo), both carried by the super-block's first stage.
 //
 // Split-K (KS > 1, when the output tiles alone would leave CUs idle): workgroup (tile,
 // ks) covers super-blocks [ks * nblk / KS, (ks + 1) * nblk / KS) and stores its partial
