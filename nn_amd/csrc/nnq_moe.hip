@@ -320,43 +320,54 @@ struct MoeRun {
 // both owned by one wave, so the SwiGLU epilogue needs no exchange; down: stream s =
 // block s.  Workgroup (expert, group g) takes streams [g S / G, (g + 1) S / G), one per
 // wave (rounds when a group has more streams than waves); every wave streams its
-// blocks' weights over all of K with the loads kPf k-blocks ahead in registers.
+// blocks' weight codes over all of K, PF chunks ahead in registers.
 // The expert's token rows (up to 64 per pass, P bf16 planes) are shared through an LDS
-// ring of kNbuf chunks of kCkb k-blocks, copied kNbuf - 1 chunks ahead with
-// global_load_lds (one barrier per chunk).
+// ring of NBUF chunks of CKB k-blocks (32 rows of K each), copied NBUF - 1 chunks ahead
+// with global_load_lds (one barrier per chunk).  With CKB = 3 a chunk's copies are
+// exactly one 16-byte granule per thread and plane, so no copy is wasted.
+// Scales (SL): each wave stages the E8M0 scales of its blocks for all of K in its own
+// LDS area at the start of a round (1 KB per load instruction) and reads the 8 bytes
+// of its rows per k-block from there, so the per-k-block loads are the codes alone.
 constexpr int kMoeWaves = 12;
 constexpr int kMoeGroups = 8;  // groups per expert (E = 32: one workgroup per CU)
-constexpr int kCkb = 1;        // k-blocks (32 rows of K) per chunk
-constexpr int kNbuf = 4;       // LDS ring depth (chunks)
-constexpr int kPf = 3;         // weight prefetch distance (chunks)
+constexpr size_t kMoeLdsMax = 160 * 1024;
 
-template <int P>
+template <int P, int CKB>
 struct MoeK {
     static constexpr int NTH = kMoeWaves * 64;
-    static constexpr int ROWG = kCkb * 4;               // 16-byte granules per row and chunk
-    static constexpr int ACH = P * 64 * ROWG;           // granules per chunk
-    static constexpr int LPA = (ACH + NTH - 1) / NTH;   // copy instructions per thread and chunk
+    static constexpr int NBUF = CKB == 3 ? 3 : 4;  // LDS ring depth (chunks)
+    static constexpr int PF = NBUF - 1;            // weight prefetch distance (chunks)
+    static constexpr int ROWG = CKB * 4;           // 16-byte granules per row and chunk
+    static constexpr int ACH = P * 64 * ROWG;      // granules per chunk
+    static constexpr int LPA = (ACH + NTH - 1) / NTH;  // copy instructions per thread and chunk
     static constexpr int BUF = LPA * NTH * 16;
-    static constexpr size_t LDS = (size_t)kNbuf * BUF;
-    static_assert(ROWG == 4 || ROWG == 8, "row swizzle within the row's granules");
+    static constexpr size_t RING = (size_t)NBUF * BUF;
+    static_assert(CKB == 1 || CKB == 3, "chunk widths");
 };
 
-// slot of the 16-byte chunk kc of row r inside the row's ROWG granules: rows r and r + 2
-// (ROWG 8) or r + 2 .. r + 6 (ROWG 4) land in distinct banks
-template <int ROWG>
-__device__ __forceinline__ int moe_slot(int kc, int r) {
-    return kc ^ ((r >> 1) & (ROWG - 1));
+// k-blocks of scales staged per block: K / 32 rounded up to whole 1 KB loads
+__host__ __device__ constexpr int64_t moe_kbp(int64_t KB) { return (KB + 31) / 32 * 32; }
+
+template <int P, bool GU, int CKB, bool SL>
+constexpr size_t moe_lds(int64_t KB) {
+    return MoeK<P, CKB>::RING + (SL ? (size_t)kMoeWaves * (GU ? 2 : 1) * moe_kbp(KB) * 32 : 0);
 }
+
+// slot of the 16-byte granule kc of row r among the row's granules of a chunk: rows r
+// and r + 2 .. r + 6 land in different banks; the xor stays inside aligned groups of 4
+__device__ __forceinline__ int moe_slot(int kc, int r) { return kc ^ ((r >> 1) & 3); }
 
 __host__ __device__ constexpr int moe_streams(bool gu, int64_t H, int64_t I) { return (int)(gu ? I / 32 : H / 32); }
 
-template <int P, bool GU>
+template <int P, bool GU, int CKB, bool SL>
 __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, MoeScratch sc, MoeRun run) {
-    using C = MoeK<P>;
-    constexpr int NBW = GU ? 2 : 1, NTH = C::NTH, LPA = C::LPA;
+    using C = MoeK<P, CKB>;
+    constexpr int NBW = GU ? 2 : 1, NTH = C::NTH, LPA = C::LPA, NBUF = C::NBUF, PF = C::PF;
+    constexpr int WPS = CKB * NBW * (SL ? 1 : 2);  // weight loads per thread and chunk
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int64_t H = d.H, I = d.I;
     const int64_t K = GU ? H : I, KB = K / 32, NB = GU ? 2 * I / 32 : H / 32;
+    const int KBP = (int)moe_kbp(KB);
     const int S = moe_streams(GU, H, I);
     // Workgroup ids go round-robin over the 8 XCDs; when the count allows, XCD x gets a
     // contiguous run of (expert, group) items, i.e. whole experts, so an expert's
@@ -370,29 +381,30 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int p = lane >> 4, l16 = lane & 15;
     const int s_lo = (int)(g * S / kMoeGroups), s_hi = (int)((g + 1) * S / kMoeGroups);
-    const int nch = (int)(KB / kCkb);  // K / 32 is a multiple of kCkb (checked by the host)
+    const int nch = (int)(KB / CKB);  // K / 32 is a multiple of CKB (the host picks CKB)
+    unsigned char *scl = smem + C::RING + (size_t)wv * NBW * KBP * 32;  // this wave's scales (SL)
 
     for (int32_t m0 = 0; m0 < ne; m0 += 64) {
         const int mtn = (ne - m0) >= 64 ? 4 : (ne - m0 + 15) / 16;  // live row tiles
-        // copy sources of this pass: granule c -> (plane, row, slot); chunk ch at + ch * 64 k
+        // copy sources of this pass: granule c -> (plane, row, slot); chunk ch at + ch * CKB * 32 k
         const uint16_t *asrc[LPA];
 #pragma unroll
         for (int j = 0; j < LPA; j++) {
             const int c = min(j * NTH + tid, C::ACH - 1);
             const int pl = c / (64 * C::ROWG), rem = c % (64 * C::ROWG);
             const int r = rem / C::ROWG, slot = rem % C::ROWG;
-            const int kc = moe_slot<C::ROWG>(slot, r);  // the row's 16-byte chunk held at this slot
+            const int kc = moe_slot(slot, r);  // the row's 16-byte granule held at this slot
             const int32_t rr = r0 + m0 + min(r, ne - m0 - 1);  // rows past the expert repeat its last row
             asrc[j] = (GU ? run.xa[pl] + (int64_t)sc.stok[rr] * H : sc.hb + (int64_t)pl * run.A * I + (int64_t)rr * I) +
                       8 * kc;
         }
         auto issue = [&](int ch) {
             const int cv = min(ch, nch - 1);  // past the end: re-copy the last chunk
-            unsigned char *buf = smem + (size_t)(ch % kNbuf) * C::BUF;
+            unsigned char *buf = smem + (size_t)(ch % NBUF) * C::BUF;
 #pragma unroll
             for (int j = 0; j < LPA; j++)
                 __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)(asrc[j] + (int64_t)cv * kCkb * 32),
+                    (const __attribute__((address_space(1))) void *)(asrc[j] + (int64_t)cv * CKB * 32),
                     (__attribute__((address_space(3))) void *)(buf + (size_t)(j * NTH + wv * 64) * 16), 16, 0, 0);
         };
         const int nround = (s_hi - s_lo + kMoeWaves - 1) / kMoeWaves;
@@ -402,29 +414,33 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
             // buffer resources on the wave's blocks (scalar registers, range-checked): a
             // per-lane offset plus a scalar per-k-block offset, no per-load address VALU
             __amdgpu_buffer_rsrc_t rq[NBW], rs[NBW];
+            int64_t nbv[NBW];
 #pragma unroll
             for (int b = 0; b < NBW; b++) {
-                const int64_t nb = active ? (GU ? (b == 0 ? st : I / 32 + st) : st) : 0;
+                nbv[b] = active ? (GU ? (b == 0 ? st : I / 32 + st) : st) : 0;
                 rq[b] = __builtin_amdgcn_make_buffer_rsrc(
-                    const_cast<uint8_t *>((GU ? d.gu_q : d.dn_q) + (e * NB + nb) * KB * 512), 0, (int)(KB * 512),
+                    const_cast<uint8_t *>((GU ? d.gu_q : d.dn_q) + (e * NB + nbv[b]) * KB * 512), 0, (int)(KB * 512),
                     0x00020000);
                 rs[b] = __builtin_amdgcn_make_buffer_rsrc(
-                    const_cast<uint8_t *>((GU ? d.gu_s : d.dn_s) + (e * NB + nb) * KB * 32), 0, (int)(KB * 32),
+                    const_cast<uint8_t *>((GU ? d.gu_s : d.dn_s) + (e * NB + nbv[b]) * KB * 32), 0, (int)(KB * 32),
                     0x00020000);
             }
             const int qo = 8 * lane, so = 8 * p;
-            // weight ring in registers: slot (ch % (kPf + 1)) holds chunk ch
-            u32x2 wq[kPf + 1][kCkb][NBW], ws[kPf + 1][kCkb][NBW];
+            // weight ring in registers: slot (ch % (PF + 1)) holds chunk ch
+            u32x2 wq[PF + 1][CKB][NBW], ws[SL ? 1 : PF + 1][CKB][NBW];
             auto wload = [&](int ch, int slot) {
                 const int cv = min(ch, nch - 1);
 #pragma unroll
-                for (int j = 0; j < kCkb; j++)
+                for (int j = 0; j < CKB; j++)
 #pragma unroll
                     for (int b = 0; b < NBW; b++) {
-                        const int kb = cv * kCkb + j;
+                        const int kb = cv * CKB + j;
                         // cache policy 2: non-temporal (every weight byte is read once per call)
-                        wq[slot][j][b] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq[b], qo, kb * 512, 2));
-                        ws[slot][j][b] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs[b], so, kb * 32, 2));
+                        wq[slot][j][b] =
+                            __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq[b], qo, kb * 512, 2));
+                        if constexpr (!SL)
+                            ws[slot][j][b] =
+                                __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs[b], so, kb * 32, 2));
                     }
             };
             floatx4 acc[NBW][4][2];
@@ -435,45 +451,62 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
 
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __syncthreads();  // the previous round / pass has finished reading the ring
-            // Every step issues the same batch on every wave: the weights of chunk t + kPf
+            if constexpr (SL) {
+                // this wave's scales for all of K: 1 KB per load (the last one clamped inside
+                // the block's KB * 32 bytes); complete before the first chunk's wait
+#pragma unroll
+                for (int b = 0; b < NBW; b++)
+                    for (int i = 0; i < KBP / 32; i++) {
+                        const int64_t off = min((int64_t)i * 1024 + 16 * lane, KB * 32 - 16);
+                        __builtin_amdgcn_global_load_lds(
+                            (const __attribute__((address_space(1))) void *)((GU ? d.gu_s : d.dn_s) +
+                                                                             (e * NB + nbv[b]) * KB * 32 + off),
+                            (__attribute__((address_space(3))) void *)(scl + (size_t)b * KBP * 32 + (size_t)i * 1024),
+                            16, 0, 0);
+                    }
+            }
+            // Every step issues the same batch on every wave: the weights of chunk t + PF
             // (clamped into range; idle waves load block 0), then the copies of chunk
-            // t + kNbuf - 1.  The prologue runs steps t = 1 - kNbuf .. -1 the same way, so
-            // before chunk ch is read exactly kNbuf - 2 batches follow its copies.
+            // t + NBUF - 1.  The prologue runs steps t = 1 - NBUF .. -1 the same way, so
+            // before chunk ch is read exactly NBUF - 2 batches follow its copies.
             auto step = [&](int t, int wslot) {
-                wload(max(t + kPf, 0), wslot);
-                issue(t + kNbuf - 1);
+                wload(max(t + PF, 0), wslot);
+                issue(t + NBUF - 1);
             };
 #pragma unroll
-            for (int t = 1 - kNbuf; t < 0; t++) step(t, ((t + kPf) % (kPf + 1) + (kPf + 1)) % (kPf + 1));
+            for (int t = 1 - NBUF; t < 0; t++) step(t, ((t + PF) % (PF + 1) + (PF + 1)) % (PF + 1));
             // MTN: live 16-row tiles of this pass (a constant per instantiation)
             auto pass = [&](auto mtn_c) {
                 constexpr int MTN = decltype(mtn_c)::value;
                 auto body = [&](int ch, int slot) {
-                    wait_vmcnt<(kNbuf - 2) * (LPA + 2 * kCkb * NBW)>();  // this thread's copies of chunk ch
-                    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of chunk ch - 1
-                    __builtin_amdgcn_s_barrier();        // everyone's copies of chunk ch have landed
+                    wait_vmcnt<(NBUF - 2) * (LPA + WPS)>();  // this thread's copies of chunk ch
+                    __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): this wave's reads of chunk ch - 1
+                    __builtin_amdgcn_s_barrier();            // everyone's copies of chunk ch have landed
                     __builtin_amdgcn_sched_barrier(0);
-                    step(ch, (slot + kPf) % (kPf + 1));
+                    step(ch, (slot + PF) % (PF + 1));
                     if (!active) return;
-                    const unsigned char *buf = smem + (size_t)(ch % kNbuf) * C::BUF;
-                    u32x4 a[kCkb][MTN][P];
+                    const unsigned char *buf = smem + (size_t)(ch % NBUF) * C::BUF;
 #pragma unroll
-                    for (int j = 0; j < kCkb; j++)
+                    for (int j = 0; j < CKB; j++) {
+                        u32x4 a[MTN][P];
 #pragma unroll
                         for (int mt = 0; mt < MTN; mt++)
 #pragma unroll
                             for (int pl = 0; pl < P; pl++) {
                                 const int rr = mt * 16 + l16, kc = 4 * j + p;
-                                a[j][mt][pl] = *reinterpret_cast<const u32x4 *>(
-                                    buf + (size_t)((pl * 64 + rr) * C::ROWG + moe_slot<C::ROWG>(kc, rr)) * 16);
+                                a[mt][pl] = *reinterpret_cast<const u32x4 *>(
+                                    buf + (size_t)((pl * 64 + rr) * C::ROWG + moe_slot(kc, rr)) * 16);
                             }
-#pragma unroll
-                    for (int j = 0; j < kCkb; j++) {
                         u32x4 be[NBW], bo[NBW];
 #pragma unroll
                         for (int b = 0; b < NBW; b++) {
+                            u32x2 sw;
+                            if constexpr (SL)
+                                sw = *reinterpret_cast<const u32x2 *>(scl + ((size_t)b * KBP + ch * CKB + j) * 32 + 8 * p);
+                            else
+                                sw = ws[slot][j][b];
                             uint32_t r[8];
-                            fp4_rows(wq[slot][j][b], ws[slot][j][b], r);
+                            fp4_rows(wq[slot][j][b], sw, r);
 #pragma unroll
                             for (int q = 0; q < 4; q++) {
                                 bo[b][q] = __builtin_amdgcn_perm(r[2 * q + 1], r[2 * q], 0x05040100u);  // column 2c + 1
@@ -486,19 +519,19 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
                             for (int pl = 0; pl < P; pl++)
 #pragma unroll
                                 for (int b = 0; b < NBW; b++) {
-                                    acc[b][mt][0] = mfma16x16x32_bf16(a[j][mt][pl], be[b], acc[b][mt][0]);
-                                    acc[b][mt][1] = mfma16x16x32_bf16(a[j][mt][pl], bo[b], acc[b][mt][1]);
+                                    acc[b][mt][0] = mfma16x16x32_bf16(a[mt][pl], be[b], acc[b][mt][0]);
+                                    acc[b][mt][1] = mfma16x16x32_bf16(a[mt][pl], bo[b], acc[b][mt][1]);
                                 }
                     }
                 };
-                // full groups of kPf + 1 chunks (slot = position in the group), then the rest
-                const int nfull = nch - nch % (kPf + 1);
-                for (int c0 = 0; c0 < nfull; c0 += kPf + 1) {
+                // full groups of PF + 1 chunks (slot = position in the group), then the rest
+                const int nfull = nch - nch % (PF + 1);
+                for (int c0 = 0; c0 < nfull; c0 += PF + 1) {
 #pragma unroll
-                    for (int u = 0; u < kPf + 1; u++) body(c0 + u, u);
+                    for (int u = 0; u < PF + 1; u++) body(c0 + u, u);
                 }
 #pragma unroll
-                for (int u = 0; u < kPf; u++)
+                for (int u = 0; u < PF; u++)
                     if (nfull + u < nch) body(nfull + u, u);
             };
             switch (mtn) {
@@ -556,7 +589,6 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
         }
     }
 }
-
 // y[t] = ((0 + w_a * y_a) + w_b * y_b) + ... over the token's experts a < b < ...
 template <int k>
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeScratch sc, int64_t H, float *y) {
@@ -645,19 +677,30 @@ size_t moe_scratch_bytes(int64_t T, int64_t E, int64_t H, int64_t I, int k, int 
            al256((size_t)2 * A * I * 2) + al256(A * H * 4) + 256;
 }
 
-template <int P, bool GU>
-static int launch_stream(const MoeDev &d, const MoeScratch &sc, const MoeRun &run, hipStream_t st) {
-    constexpr size_t lds = MoeK<P>::LDS;
+template <int P, bool GU, int CKB, bool SL>
+static int launch_stream_t(const MoeDev &d, const MoeScratch &sc, const MoeRun &run, hipStream_t st, size_t lds) {
     static bool attr_set = false;  // idempotent attribute write; races only repeat it
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_stream_kernel<P, GU>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_stream_kernel<P, GU, CKB, SL>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMoeLdsMax);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((moe_stream_kernel<P, GU>), dim3((unsigned)(d.E * kMoeGroups)), dim3(kMoeWaves * 64), lds, st,
-                       d, sc, run);
+    hipLaunchKernelGGL((moe_stream_kernel<P, GU, CKB, SL>), dim3((unsigned)(d.E * kMoeGroups)), dim3(kMoeWaves * 64),
+                       lds, st, d, sc, run);
     return (int)hipGetLastError();
+}
+
+// Chunks of 3 k-blocks when K / 32 allows, scales staged in LDS when they fit beside
+// the ring (hidden / intermediate up to 5120 for gate_up with bf16 input).
+template <int P, bool GU>
+static int launch_stream(const MoeDev &d, const MoeScratch &sc, const MoeRun &run, hipStream_t st) {
+    const int64_t KB = (GU ? d.H : d.I) / 32;
+    if (KB % 3 == 0 && moe_lds<P, GU, 3, true>(KB) <= kMoeLdsMax)
+        return launch_stream_t<P, GU, 3, true>(d, sc, run, st, moe_lds<P, GU, 3, true>(KB));
+    if (moe_lds<P, GU, 1, true>(KB) <= kMoeLdsMax)
+        return launch_stream_t<P, GU, 1, true>(d, sc, run, st, moe_lds<P, GU, 1, true>(KB));
+    return launch_stream_t<P, GU, 1, false>(d, sc, run, st, moe_lds<P, GU, 1, false>(KB));
 }
 
 int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const float *logits, int k, float limit,

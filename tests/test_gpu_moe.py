@@ -68,9 +68,13 @@ def ref_f64(O, x, logits, k, L, E, H, I, limit=7.0):
     return out.astype(np.float32), ti, tw
 
 
+# Shapes cover the expert kernel's variants: chunks of 3 k-blocks (K / 32 divisible by
+# 3) or 1, scales staged in LDS or (K too long for LDS: 5120-wide gate_up input,
+# 9600-wide down input) loaded beside the codes, bf16 and f32 (hi + lo) activations.
 @pytest.mark.parametrize("E,H,I,T,k,xdt", [(4, 64, 64, 24, 2, "f32"), (8, 256, 320, 64, 4, "bf16"),
                                           (8, 256, 320, 64, 4, "f32"), (6, 128, 96, 40, 3, "bf16"),
-                                          (16, 96, 64, 150, 4, "bf16")])
+                                          (16, 96, 64, 150, 4, "bf16"), (3, 96, 96, 70, 2, "f32"),
+                                          (2, 5120, 64, 8, 2, "bf16"), (1, 64, 9600, 4, 1, "f32")])
 def test_moe_small_vs_oracle(O, dev, E, H, I, T, k, xdt):
     import nn_amd
     L = make_layer(E, H, I, seed=E * 7 + H)
