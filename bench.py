@@ -187,6 +187,34 @@ def bench_gemm(m, n, k, steps, warmup, min_bytes=256 << 20):
     return dict(sec=sec, steps=nsteps, tflops=flops / sec / 1e12, copies=len(copies))
 
 
+def bench_mlp(steps, warmup, m=1, seed=8, min_bytes=512 << 20):
+    """Qwen3-8B SwiGLU MLP decode (hidden 4096, intermediate 12288, Q4_K gate / up /
+    down, bf16 x [m, 4096] -> f32 y): nnq_mlp_forward, rotating copies of the layer."""
+    import torch
+
+    import nn_amd
+    H, I = 4096, 12288
+    bg = nn_amd.quantize_q4_k(nn_amd.synth_normal(seed, 1, (I, H), 0.02))
+    bu = nn_amd.quantize_q4_k(nn_amd.synth_normal(seed, 2, (I, H), 0.02))
+    bd = nn_amd.quantize_q4_k(nn_amd.synth_normal(seed, 3, (H, I), 0.02))
+    per = len(bg) + len(bu) + len(bd)
+    copies = [nn_amd.QuantizedMLP(bg, bu, bd, nn_amd.QuantType.Q4_K, H, I) for _ in range(max(1, -(-min_bytes // per)))]
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(nn_amd.synth_normal(seed, 4, (m, H), 1.0)).to(dev).to(torch.bfloat16)
+    ys = [torch.empty((m, H), device=dev) for _ in copies]
+    st = torch.zeros(1, dtype=torch.int32, device=dev)
+    L = lib()
+
+    def launcher(c, y):
+        def f():
+            check(L.nnq_mlp_forward(c._h, vp(x), 2, m, H, vp(y), 0, vp(st), cur_stream()))
+        return f
+
+    sec, nsteps = time_graph([launcher(c, y) for c, y in zip(copies, ys)], steps, warmup, min_graph_calls=40)
+    algo = per + m * H * 2 + m * H * 4 + 2 * (m * 2 * I * 4)  # weights, x, y, gate | up written and read
+    return dict(sec=sec, steps=nsteps, gbs=algo / sec / 1e9, tokens_per_s=m / sec, copies=len(copies))
+
+
 def bench_moe(steps, warmup, seed=20):
     """Config 5: GPT-OSS-20B-style MXFP4 MoE, 32 experts, top-4, hidden = intermediate
     = 2880, 256 bf16 tokens, router logits ~ N(0,1).  One copy of the 423 MB expert
@@ -282,6 +310,11 @@ def main():
         g = bench_gemv("q4_k", 24576, 4096, few, 20, seed=5)
         configs["q4_k_gemv_24576x4096"] = {"us": round(g["sec"] * 1e6, 3), "GBps": round(g["gbs"], 1),
                                            "frac_hbm": round(g["gbs"] / HBM_PEAK_GBS, 4)}
+        log("bench: Qwen3-8B MLP decode (Q4_K gate | up GEMV + SwiGLU-staging down GEMV)")
+        g = bench_mlp(few, 20)
+        configs["q4_k_qwen3_8b_mlp_decode_m1"] = {"us": round(g["sec"] * 1e6, 3), "GBps": round(g["gbs"], 1),
+                                                  "frac_hbm": round(g["gbs"] / HBM_PEAK_GBS, 4),
+                                                  "tokens_per_s": round(g["tokens_per_s"], 1)}
         log("bench: Q6_K LM head 151936x4096 + argmax")
         g = bench_lm_head(max(40, args.steps // 40), 10)
         configs["q6_k_lm_head_151936x4096_argmax"] = {"us": round(g["sec"] * 1e6, 3), "GBps": round(g["gbs"], 1),

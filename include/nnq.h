@@ -82,6 +82,7 @@ typedef enum nnq_dtype {
 
 typedef struct nnq_weight nnq_weight;   /* opaque: device-resident, repacked block weight */
 typedef struct nnq_moe nnq_moe;         /* opaque: device-resident MXFP4 expert weights + biases */
+typedef struct nnq_mlp nnq_mlp;         /* opaque: device-resident SwiGLU MLP (gate | up, down) */
 
 /* ---- device ------------------------------------------------------------------- */
 
@@ -146,6 +147,30 @@ int nnq_argmax_f32(const float *logits, int64_t n, uint32_t *idx, int32_t *statu
  * crates/nn-core/src/dyn_tensor/ops_ext/argreduce.rs:105-118). */
 int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const float *bias, int64_t bias_len,
                       float *logits, uint32_t *idx, int32_t *status_dev, void *stream);
+
+/* ---- Qwen3 SwiGLU MLP ----------------------------------------------------------- */
+
+/* Upload one layer's MLP: gate_proj and up_proj W[inter, hidden] (block bytes of one
+ * format / layout, gu_nbytes each) and down_proj W[hidden, inter].  gate and up are
+ * stacked into one W[2 * inter, hidden] so that one GEMV computes both.  Validation
+ * as nnq_weight_create.  Replaces Qwen3MLP::load (crates/nn-qwen3/src/layers.rs:26-38)
+ * over quantized Linear weights. */
+int nnq_mlp_create(nnq_format gu_fmt, nnq_layout gu_layout, const uint8_t *gate, const uint8_t *up,
+                   size_t gu_nbytes, nnq_format down_fmt, nnq_layout down_layout, const uint8_t *down,
+                   size_t down_nbytes, int64_t hidden, int64_t inter, nnq_mlp **out);
+
+int nnq_mlp_destroy(nnq_mlp *mlp);
+
+/* y[m, hidden] = down(silu(gate(x)) * up(x)) for x[m, k] (k = hidden; NNQ_F32 or
+ * NNQ_BF16, 16-byte aligned); y NNQ_F32 or NNQ_BF16.  silu(v) = v / (1 + e^-v) and the
+ * product in f32.  Decode (m <= 2): two launches, the gate | up GEMV, then the down GEMV
+ * forming silu(gate) * up as it stages its input.  Larger m: gate | up linear, SwiGLU,
+ * down linear.  status_dev (device int, may be NULL): NNQ_OK, or NNQ_ERR_NON_FINITE
+ * when an output is NaN or infinite, as check_output_finite reports it
+ * (crates/nn-core/src/layers/nan_check.rs:113-140).
+ * Replaces Qwen3MLP::forward (crates/nn-qwen3/src/layers.rs:40-47). */
+int nnq_mlp_forward(const nnq_mlp *mlp, const void *x, nnq_dtype x_dtype, int64_t m, int64_t k, void *y,
+                    nnq_dtype y_dtype, int32_t *status_dev, void *stream);
 
 /* ---- GPT-OSS MXFP4 mixture of experts ----------------------------------------- */
 

@@ -7,7 +7,7 @@ operator surface in Python.
 """
 from .quantized import (  # noqa: F401
     BiasMismatch, DataLengthMismatch, InvalidShape, Layout, NonFiniteData, NotQuantized, QuantizedMatmulError,
-    QuantizedMoE, QuantizedWeight, QuantType, RankMismatch, ShapeMismatch, TensorError, Unsupported, WeightRank,
+    QuantizedMLP, QuantizedMoE, QuantizedWeight, QuantType, RankMismatch, ShapeMismatch, TensorError, Unsupported, WeightRank,
     WrongQuantType, argmax, device_count, init, linear_argmax, quantize_mxfp4, quantize_q4_k, quantize_q6_k,
     quantize_q8_0, quantized_linear, quantized_matmul_q4_k, quantized_matmul_q6_k, quantized_matmul_q8_0,
     synth_normal)

@@ -38,6 +38,10 @@ SIGNATURES = {
     "nnq_moe_forward": (c_int, [c_void_p, c_void_p, c_int, c_i64, c_void_p, c_int, c_float, c_void_p, c_void_p,
                                 c_void_p, c_void_p]),
     "nnq_moe_dequant_expert": (c_int, [c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),
+    "nnq_mlp_create": (c_int, [c_int, c_int, c_void_p, c_void_p, c_sz, c_int, c_int, c_void_p, c_sz, c_i64, c_i64,
+                               ctypes.POINTER(c_void_p)]),
+    "nnq_mlp_destroy": (c_int, [c_void_p]),
+    "nnq_mlp_forward": (c_int, [c_void_p, c_void_p, c_int, c_i64, c_i64, c_void_p, c_int, c_void_p, c_void_p]),
     "nnq_quantize_q4_k": (c_int, [c_void_p, c_sz, c_void_p]),
     "nnq_quantize_mxfp4": (c_int, [c_void_p, c_sz, c_void_p, c_void_p]),
     "nnq_quantize_q8_0": (c_int, [c_void_p, c_sz, c_void_p]),

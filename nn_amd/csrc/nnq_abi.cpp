@@ -22,6 +22,12 @@ struct nnq_weight {
     int device = 0;
 };
 
+struct nnq_mlp {
+    nnq_weight *gu = nullptr;    // [2 * inter, hidden]: gate rows, then up rows
+    nnq_weight *down = nullptr;  // [hidden, inter]
+    int64_t hidden = 0, inter = 0;
+};
+
 struct nnq_moe {
     MoeDev d;
     int device = 0;
@@ -64,16 +70,82 @@ size_t block_bytes(int fmt) {
     return 0;
 }
 
-// Stream-ordered scratch owned by one call.
+// Per-(device, stream) workspace: calls on one stream run in order, so they can share
+// one buffer.  It grows by allocating a larger buffer; a replaced buffer is kept until
+// the process ends, because a graph captured earlier may still replay with it.  While a
+// stream is being captured it grows with the capture's ban on allocation relaxed for
+// this thread; where that is refused, the call takes a stream-ordered allocation.
+struct Workspace {
+    int dev;
+    hipStream_t st;
+    void *p;
+    size_t n;
+};
+std::mutex g_ws_mu;
+std::vector<Workspace> g_ws;
+std::vector<void *> g_ws_retired;
+
+hipError_t stream_workspace(hipStream_t st, size_t n, void **out, bool *owned) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> g(g_ws_mu);
+    Workspace *w = nullptr;
+    for (auto &x : g_ws)
+        if (x.dev == dev && x.st == st) w = &x;
+    if (w && w->n >= n) {
+        *out = w->p;
+        *owned = false;
+        return hipSuccess;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) return e;
+    size_t sz = std::max<size_t>(n, (size_t)1 << 20);
+    if (w) sz = std::max(sz, 2 * w->n);
+    void *p = nullptr;
+    if (cs != hipStreamCaptureStatusNone) {
+        // under capture this thread opts out of the capture's ban on allocation calls
+        // for the one hipMalloc (relaxed mode); if that is refused, a stream-ordered
+        // allocation of the call's own becomes a node of the graph
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        (void)hipThreadExchangeStreamCaptureMode(&mode);
+        e = hipMalloc(&p, sz);
+        (void)hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            *owned = true;
+            return hipMallocAsync(out, n, st);
+        }
+    } else {
+        e = hipMalloc(&p, sz);
+        if (e != hipSuccess) return e;
+    }
+    if (w) {
+        g_ws_retired.push_back(w->p);
+        w->p = p;
+        w->n = sz;
+    } else {
+        g_ws.push_back(Workspace{dev, st, p, sz});
+    }
+    *out = p;
+    *owned = false;
+    return hipSuccess;
+}
+
+// Scratch of one call: the stream's workspace (or, under capture when that is too
+// small, a stream-ordered allocation freed after the call's work).  Calls that overlap
+// on one stream cannot happen (stream order), so one call holds the workspace at a time.
 struct Scratch {
     void *p = nullptr;
     hipStream_t s = nullptr;
+    bool owned = false;
     ~Scratch() {
-        if (p) (void)hipFreeAsync(p, s);
+        if (owned && p) (void)hipFreeAsync(p, s);
     }
     hipError_t alloc(size_t n, hipStream_t st) {
         s = st;
-        return hipMallocAsync(&p, n ? n : 16, st);
+        return stream_workspace(st, n ? n : 16, &p, &owned);
     }
 };
 
@@ -232,43 +304,68 @@ static int check_linear(const nnq_weight *w, const void *x, nnq_dtype xd, int64_
     return NNQ_OK;
 }
 
-int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m, int64_t k, const float *bias,
-               int64_t bias_len, void *y, nnq_dtype y_dtype, void *stream) {
-    int rc = check_linear(w, x, x_dtype, m, k, bias, bias_len, y, y_dtype);
-    if (rc) return rc;
+}  // extern "C"
+
+// One validated linear call: the prefill GEMM (Q4_K, m > 8) or GEMV passes of up to
+// 8 tokens.  GEMV-only options: x_swiglu (x holds gate | up rows of 2k f32, the input
+// is silu(gate) * up; m <= 2 so one pass) and a status (mode 1 clears it in the
+// first pass, mode 2 flags non-finite outputs in every pass).
+static GemmArgs gemm_args(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m, const float *bias, void *y,
+                          nnq_dtype y_dtype) {
+    const Layout &L = w->L;
+    GemmArgs g{};
+    g.qs = w->dev;
+    g.hdr = w->dev + L.qs_bytes;
+    g.aux = w->dev + L.qs_bytes + L.hdr_bytes;
+    g.x = x;
+    g.x_bf16 = x_dtype == NNQ_BF16;
+    g.bias = bias;
+    g.y = y;
+    g.y_bf16 = y_dtype == NNQ_BF16;
+    g.n = L.n;
+    g.k = L.k;
+    g.m = m;
+    g.ntile = L.ntile;
+    g.nblk = L.nblk;
+    return g;
+}
+
+// scratch a linear call of m tokens needs (the prefill GEMM's staging and split-K slabs)
+static size_t linear_scratch_bytes(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
+    if (w->L.fmt != NNQ_FMT_Q4_K || m <= 8) return 0;
+    return gemm_scratch_bytes(gemm_args(w, nullptr, x_dtype, m, nullptr, nullptr, NNQ_F32));
+}
+
+static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m, const float *bias,
+                           void *y, nnq_dtype y_dtype, void *stream, int x_swiglu = 0, int32_t *status = nullptr,
+                           int status_mode = 0, void *ext_scratch = nullptr) {
     if (m == 0) return NNQ_OK;
     const Layout &L = w->L;
+    const int64_t k = L.k;
     const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, ye = y_dtype == NNQ_BF16 ? 2 : 4;
-    if (L.fmt == NNQ_FMT_Q4_K && m > 8) {
+    if (L.fmt == NNQ_FMT_Q4_K && m > 8 && !x_swiglu) {
         // prefill: LDS-staged MFMA GEMM
-        GemmArgs g{};
-        g.qs = w->dev;
-        g.hdr = w->dev + L.qs_bytes;
-        g.aux = w->dev + L.qs_bytes + L.hdr_bytes;
-        g.x = x;
-        g.x_bf16 = x_dtype == NNQ_BF16;
-        g.bias = bias;
-        g.y = y;
-        g.y_bf16 = y_dtype == NNQ_BF16;
-        g.n = L.n;
-        g.k = L.k;
-        g.m = m;
-        g.ntile = L.ntile;
-        g.nblk = L.nblk;
+        GemmArgs g = gemm_args(w, x, x_dtype, m, bias, y, y_dtype);
         Scratch s;
-        HIP_TRY(s.alloc(gemm_scratch_bytes(g), (hipStream_t)stream), "scratch alloc");
-        g.scratch = s.p;
+        if (ext_scratch)
+            g.scratch = ext_scratch;
+        else {
+            HIP_TRY(s.alloc(gemm_scratch_bytes(g), (hipStream_t)stream), "scratch alloc");
+            g.scratch = s.p;
+        }
         int e = launch_gemm_q4k(g, stream);
         if (e) return hip_fail((hipError_t)e, "gemm launch");
         return NNQ_OK;
     }
     const int64_t mmax = L.fmt == NNQ_FMT_Q6_K ? 4 : 8;
+    const int64_t xrow = x_swiglu ? 2 * k : k;
     for (int64_t m0 = 0; m0 < m; m0 += mmax) {
         GemvArgs a{};
         a.qs = w->dev;
         a.hdr = w->dev + L.qs_bytes;
-        a.x = (const uint8_t *)x + (size_t)m0 * k * xe;
+        a.x = (const uint8_t *)x + (size_t)m0 * xrow * xe;
         a.x_bf16 = x_dtype == NNQ_BF16;
+        a.x_swiglu = x_swiglu;
         a.bias = bias;
         a.y = (uint8_t *)y + (size_t)m0 * L.n * ye;
         a.y_bf16 = y_dtype == NNQ_BF16;
@@ -277,10 +374,23 @@ int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m,
         a.m = std::min(mmax, m - m0);
         a.ntile = L.ntile;
         a.nblk = L.nblk;
+        if (status && (status_mode == 2 || m0 == 0)) {
+            a.status = status;
+            a.status_mode = status_mode;
+        }
         int e = launch_gemv(L.fmt, a, stream);
         if (e) return hip_fail((hipError_t)e, "gemv launch");
     }
     return NNQ_OK;
+}
+
+extern "C" {
+
+int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m, int64_t k, const float *bias,
+               int64_t bias_len, void *y, nnq_dtype y_dtype, void *stream) {
+    int rc = check_linear(w, x, x_dtype, m, k, bias, bias_len, y, y_dtype);
+    if (rc) return rc;
+    return dispatch_linear(w, x, x_dtype, m, bias, y, y_dtype, stream);
 }
 
 int nnq_argmax_f32(const float *logits, int64_t n, uint32_t *idx, int32_t *status_dev, void *stream) {
@@ -413,6 +523,79 @@ int nnq_moe_dequant_expert(const nnq_moe *m, int64_t expert, float *gate_up, flo
     if (expert < 0 || expert >= m->d.E) return fail(NNQ_ERR_INVALID_ARGUMENT, "expert %lld", (long long)expert);
     int e = launch_moe_dequant(m->d, expert, gate_up, down, stream);
     if (e) return hip_fail((hipError_t)e, "moe dequant launch");
+    return NNQ_OK;
+}
+
+// ---- Qwen3 SwiGLU MLP -------------------------------------------------------------
+
+int nnq_mlp_create(nnq_format gu_fmt, nnq_layout gu_layout, const uint8_t *gate, const uint8_t *up,
+                   size_t gu_nbytes, nnq_format down_fmt, nnq_layout down_layout, const uint8_t *down,
+                   size_t down_nbytes, int64_t hidden, int64_t inter, nnq_mlp **out) {
+    if (!out) return fail(NNQ_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (!gate || !up || !down) return fail(NNQ_ERR_INVALID_ARGUMENT, "weight bytes are null");
+    if (hidden <= 0 || inter <= 0)
+        return fail(NNQ_ERR_INVALID_ARGUMENT, "MLP shape hidden=%lld inter=%lld", (long long)hidden, (long long)inter);
+    // gate_proj and up_proj are W[inter, hidden]: stacked they are one W[2 * inter, hidden]
+    // (block rows are independent), so a single GEMV computes both
+    std::vector<uint8_t> cat(2 * gu_nbytes);
+    std::memcpy(cat.data(), gate, gu_nbytes);
+    std::memcpy(cat.data() + gu_nbytes, up, gu_nbytes);
+    nnq_weight *gu = nullptr, *dn = nullptr;
+    int rc = nnq_weight_create(gu_fmt, gu_layout, cat.data(), cat.size(), 2 * inter, hidden, &gu);
+    if (rc) return rc;
+    rc = nnq_weight_create(down_fmt, down_layout, down, down_nbytes, hidden, inter, &dn);
+    if (rc) {
+        nnq_weight_destroy(gu);
+        return rc;
+    }
+    nnq_mlp *p = new nnq_mlp;
+    p->gu = gu;
+    p->down = dn;
+    p->hidden = hidden;
+    p->inter = inter;
+    *out = p;
+    return NNQ_OK;
+}
+
+int nnq_mlp_destroy(nnq_mlp *p) {
+    if (!p) return NNQ_OK;
+    nnq_weight_destroy(p->gu);
+    nnq_weight_destroy(p->down);
+    delete p;
+    return NNQ_OK;
+}
+
+int nnq_mlp_forward(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t m, int64_t k, void *y,
+                    nnq_dtype y_dtype, int32_t *status_dev, void *stream) {
+    if (!p) return fail(NNQ_ERR_INVALID_ARGUMENT, "MLP handle is null");
+    int rc = check_linear(p->gu, x, x_dtype, m, k, nullptr, 0, y, y_dtype);
+    if (rc) return rc;
+    if (m == 0) return NNQ_OK;
+    const int64_t I = p->inter;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const bool fused = m <= 2;  // the down GEMV takes gate | up and applies SwiGLU while staging
+    // one scratch: gate | up [m, 2I] f32, h [m, I] f32, then the GEMM scratch of either linear
+    const size_t gu_bytes = al((size_t)m * 2 * I * 4), h_bytes = fused ? 0 : al((size_t)m * I * 4);
+    const size_t lin_bytes =
+        std::max(linear_scratch_bytes(p->gu, m, x_dtype), fused ? 0 : linear_scratch_bytes(p->down, m, NNQ_F32));
+    Scratch s;
+    HIP_TRY(s.alloc(gu_bytes + h_bytes + lin_bytes, (hipStream_t)stream), "scratch alloc");
+    uint8_t *base = reinterpret_cast<uint8_t *>(s.p);
+    float *gu = reinterpret_cast<float *>(base);
+    void *lin = lin_bytes ? base + gu_bytes + h_bytes : nullptr;
+    rc = dispatch_linear(p->gu, x, x_dtype, m, nullptr, gu, NNQ_F32, stream, 0, status_dev, fused ? 1 : 0, lin);
+    if (rc) return rc;
+    if (fused) return dispatch_linear(p->down, gu, NNQ_F32, m, nullptr, y, y_dtype, stream, 1, status_dev, 2);
+    float *h = reinterpret_cast<float *>(base + gu_bytes);
+    int e = launch_swiglu(gu, m, I, h, status_dev, stream);
+    if (e) return hip_fail((hipError_t)e, "swiglu launch");
+    rc = dispatch_linear(p->down, h, NNQ_F32, m, nullptr, y, y_dtype, stream, 0, nullptr, 0, lin);
+    if (rc) return rc;
+    if (status_dev) {
+        e = launch_nonfinite_check(y, y_dtype == NNQ_BF16, m * p->hidden, status_dev, stream);
+        if (e) return hip_fail((hipError_t)e, "output check launch");
+    }
     return NNQ_OK;
 }
 

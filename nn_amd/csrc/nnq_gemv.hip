@@ -15,10 +15,32 @@
 //
 // A-operand rows: Q4_K / Q8_0 use rows (2t, 2t+1) = (hi, lo) of token t (8 tokens);
 // Q6_K uses rows 4t..4t+3 = (hi, lo) x (first / second 16-value sub-block).
+#include <algorithm>
+
 #include "nnq_device.h"
 #include "nnq_internal.h"
 
 namespace nnq {
+
+// silu(g) * u for four f32 values (g, u as raw bits): SiLU as x / (1 + e^-x)
+// (crates/nn-core/src/dyn_tensor/ops/math.rs:140), the product in f32, as
+// Qwen3MLP::forward (crates/nn-qwen3/src/layers.rs:40-47) forms it.
+__device__ __forceinline__ u32x4 swiglu4(const u32x4 &g, const u32x4 &u) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float gv = __uint_as_float(g[i]);
+        r[i] = __float_as_uint(gv / (1.0f + expf(-gv)) * __uint_as_float(u[i]));
+    }
+    return r;
+}
+
+// Output status of a GEMV pass: mode 1 clears it (one thread of the grid), mode 2
+// flags a non-finite output (every writer stores the same value).
+__device__ __forceinline__ void gemv_status(const GemvArgs &a, float y, bool first) {
+    if (a.status_mode == 1 && first) *a.status = NNQ_OK;
+    if (a.status_mode == 2 && !(fabsf(y) <= 3.402823466e38f)) *a.status = NNQ_ERR_NON_FINITE;
+}
 
 enum { FQ4K = 12, FQ80 = 8, FQ6K = 14 };
 
@@ -449,6 +471,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         const int64_t row = tile * 16 + nn;
         if (row < a.n) {
             if (a.bias) y += a.bias[row];
+            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
             if (a.y_bf16)
                 reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
             else
@@ -519,7 +542,8 @@ __device__ __forceinline__ void stage_unit(const u32x4 &raw, bool x_bf16, bool i
     if ((lane & 7) == 0) ub.backs[t * 8 + lane / 8] = back;
 }
 
-template <int FMT, int WAVES, int UPW>
+// SW: x is f32 [m, 2k] gate | up pairs and the GEMV input is silu(gate) * up
+template <int FMT, int WAVES, int UPW, bool SW>
 __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
     using Unit = typename UnitOf<FMT>::T;
     constexpr int GRAN = Fmt<FMT>::kSumGran;
@@ -533,11 +557,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
     __syncthreads();
 
     const int64_t units = FMT == FQ80 ? a.nblk / 8 : a.nblk;
-    const size_t xe = a.x_bf16 ? 2 : 4;
+    const size_t xe = (!SW && a.x_bf16) ? 2 : 4;
     float acc1[4][2] = {}, acc2[4][2] = {};
     for (int64_t ub0 = 0; ub0 < units; ub0 += WAVES * UPW) {
         // activation slices first (their wait then does not cover the weight loads)
-        u32x4 xr[UPW][2];
+        u32x4 xr[UPW][2], xu[SW ? UPW : 1][2];
         bool xin[UPW];
         int64_t uu[UPW];
 #pragma unroll
@@ -548,14 +572,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
             xin[i] = kk < a.k;
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-                const int64_t off = xin[i] ? (int64_t)(t < mt ? t : 0) * a.k + kk : 0;
+                const int64_t off = xin[i] ? (int64_t)(t < mt ? t : 0) * (SW ? 2 * a.k : a.k) + kk : 0;
                 const uint8_t *p = reinterpret_cast<const uint8_t *>(a.x) + off * xe;
-                if (a.x_bf16) {
+                if (!SW && a.x_bf16) {
                     const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
                     xr[i][t] = u32x4{w2[0], w2[1], 0u, 0u};
                 } else {
                     xr[i][t] = *reinterpret_cast<const u32x4 *>(p);
                 }
+                if constexpr (SW) xu[i][t] = *reinterpret_cast<const u32x4 *>(p + (size_t)a.k * 4);
             }
         }
         Unit w[UPW];
@@ -565,8 +590,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
         for (int i = 0; i < UPW; i++) {
             if (ub0 + wv + i * WAVES >= units) break;  // wave-uniform
             UnitBuf &b = ubuf[wv][i & 1];
-            stage_unit<GRAN, FMT == FQ80>(xr[i][0], a.x_bf16, xin[i], 0, b);
-            if (mt > 1) stage_unit<GRAN, FMT == FQ80>(xr[i][1], a.x_bf16, xin[i], 1, b);
+            if constexpr (SW) {
+                stage_unit<GRAN, FMT == FQ80>(swiglu4(xr[i][0], xu[i][0]), 0, xin[i], 0, b);
+                if (mt > 1) stage_unit<GRAN, FMT == FQ80>(swiglu4(xr[i][1], xu[i][1]), 0, xin[i], 1, b);
+            } else {
+                stage_unit<GRAN, FMT == FQ80>(xr[i][0], a.x_bf16, xin[i], 0, b);
+                if (mt > 1) stage_unit<GRAN, FMT == FQ80>(xr[i][1], a.x_bf16, xin[i], 1, b);
+            }
             // the wave's own LDS writes are read back by other lanes of the same wave
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -629,6 +659,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
         const int64_t row = tile * 16 + nn;
         if (row < a.n) {
             if (a.bias) y += a.bias[row];
+            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
             if (a.y_bf16)
                 reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
             else
@@ -752,8 +783,10 @@ __device__ __forceinline__ void stage_q4k(const u32x4 &raw, uint16_t *hi_plane, 
     st.xs_hi = first ? sum_o : sum;
 }
 
-template <int WAVES, int UPW, int R, bool XB, int MT>
+// XM: activation kind, 0 f32, 1 bf16, 2 f32 gate | up pairs (SwiGLU prologue)
+template <int WAVES, int UPW, int R, int XM, int MT>
 __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a) {
+    constexpr bool XB = XM == 1;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tile0 = (int)blockIdx.x * R;  // this workgroup's tiles: tile0 .. tile0 + R - 1
@@ -780,6 +813,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
         hbase[r] = a.hdr + (size_t)tile * units * 256 + 16 * n;
     }
     constexpr int xe = XB ? 2 : 4;
+    const int xrow = XM == 2 ? 2 * k : k;  // elements per token row of x
     const uint8_t *xbase = reinterpret_cast<const uint8_t *>(a.x) + 4 * lane * xe;
     float acc1[R][MT], acc2[R][MT];
 #pragma unroll
@@ -789,20 +823,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
     int ub0 = 0;
     do {  // passes over K (units >= 1: the host checks k >= 256)
         // activation slices first (L2 hits), then the weights of every unit of the pass
-        u32x4 xr[UPW][MT];
+        u32x4 xr[UPW][MT], xu[XM == 2 ? UPW : 1][MT];
         UnitQ4K w[UPW][R];
 #pragma unroll
         for (int j = 0; j < UPW; j++) {
             const uint32_t u = (uint32_t)min(ub0 + wv + j * WAVES, units - 1);
 #pragma unroll
             for (int t = 0; t < MT; t++) {
-                const uint8_t *p = xbase + (uint32_t)(t * k + (int)u * 256) * (uint32_t)xe;
+                const uint8_t *p = xbase + (uint32_t)(t * xrow + (int)u * 256) * (uint32_t)xe;
                 if (XB) {
                     const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
                     xr[j][t] = u32x4{w2[0], w2[1], 0u, 0u};
                 } else {
                     xr[j][t] = *reinterpret_cast<const u32x4 *>(p);
                 }
+                if constexpr (XM == 2) xu[j][t] = *reinterpret_cast<const u32x4 *>(p + (size_t)k * 4);
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // keep this issue order
@@ -823,7 +858,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
             uint16_t *buf = xbuf[wv][j & 1];
             XStat st[MT];
 #pragma unroll
-            for (int t = 0; t < MT; t++) stage_q4k<XB>(xr[j][t], buf + 512 * t, buf + 512 * t + 256, st[t]);
+            for (int t = 0; t < MT; t++) {
+                u32x4 xv = xr[j][t];
+                if constexpr (XM == 2) xv = swiglu4(xv, xu[j][t]);
+                stage_q4k<XB>(xv, buf + 512 * t, buf + 512 * t + 256, st[t]);
+            }
             // the wave's own LDS writes are read back by other lanes of the same wave
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -888,6 +927,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
         const int64_t row = tile * 16 + nn;
         if (row < a.n) {
             if (a.bias) y += a.bias[row];
+            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
             if (a.y_bf16)
                 reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
             else
@@ -1060,6 +1100,46 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int
 }
 
 // ---------------------------------------------------------------------------------
+// SwiGLU glue of the MLP when the down projection does not take gate | up directly
+// (more than 2 tokens): h[t, i] = silu(gu[t, i]) * gu[t, I + i]; thread 0 of block
+// 0 clears the status that the output check sets afterwards.
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void swiglu_kernel(const float *gu, int64_t m, int64_t inter, float *h,
+                                                     int32_t *status) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (status && i == 0) *status = NNQ_OK;
+    if (i >= m * inter) return;
+    const int64_t t = i / inter, c = i % inter;
+    const float g = gu[t * 2 * inter + c];
+    h[i] = g / (1.0f + expf(-g)) * gu[t * 2 * inter + inter + c];
+}
+
+// check_output_finite (crates/nn-core/src/layers/nan_check.rs:113-140) on the device:
+// any NaN or infinite value of y sets *status to NNQ_ERR_NON_FINITE
+__global__ __launch_bounds__(256) void nonfinite_kernel(const void *y, int y_bf16, int64_t count, int32_t *status) {
+    bool bad = false;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+        const float v = y_bf16 ? bf16_to_f32(reinterpret_cast<const uint16_t *>(y)[i]) : reinterpret_cast<const float *>(y)[i];
+        bad |= !(fabsf(v) <= 3.402823466e38f);
+    }
+    if (__any(bad) && (threadIdx.x & 63) == 0) *status = NNQ_ERR_NON_FINITE;
+}
+
+int launch_swiglu(const float *gu, int64_t m, int64_t inter, float *h, int32_t *status, void *stream) {
+    const int64_t n = m * inter;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, gu, m,
+                       inter, h, status);
+    return (int)hipGetLastError();
+}
+
+int launch_nonfinite_check(const void *y, int y_bf16, int64_t count, int32_t *status, void *stream) {
+    const int64_t blocks = std::min<int64_t>((count + 255) / 256, 1024);
+    hipLaunchKernelGGL(nonfinite_kernel, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0,
+                       (hipStream_t)stream, y, y_bf16, count, status);
+    return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------
 template <int FMT, int WAVES, int NTP, int UPW>
@@ -1110,8 +1190,12 @@ static int launch_gemv_w(const GemvArgs &a, int64_t units, void *stream) {
 
 template <int FMT, int WAVES, int UPW>
 static int launch_wave_t(const GemvArgs &a, void *stream) {
-    hipLaunchKernelGGL((gemv_wave_kernel<FMT, WAVES, UPW>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
-                       (hipStream_t)stream, a);
+    if (a.x_swiglu)
+        hipLaunchKernelGGL((gemv_wave_kernel<FMT, WAVES, UPW, true>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL((gemv_wave_kernel<FMT, WAVES, UPW, false>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
@@ -1133,21 +1217,22 @@ static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
     return (int)hipErrorInvalidValue;
 }
 
-template <int WAVES, int UPW, int R, bool XB>
+template <int WAVES, int UPW, int R, int XM>
 static int launch_q4k_decode_x(const GemvArgs &a, void *stream) {
     const dim3 grid((unsigned)((a.ntile + R - 1) / R));
     if (a.m == 1)
-        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, R, XB, 1>), grid, dim3(WAVES * 64), 0,
+        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, R, XM, 1>), grid, dim3(WAVES * 64), 0,
                            (hipStream_t)stream, a);
     else
-        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, R, XB, 2>), grid, dim3(WAVES * 64), 0,
+        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, R, XM, 2>), grid, dim3(WAVES * 64), 0,
                            (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 template <int WAVES, int UPW, int R>
 static int launch_q4k_decode_t(const GemvArgs &a, void *stream) {
-    return a.x_bf16 ? launch_q4k_decode_x<WAVES, UPW, R, true>(a, stream)
-                    : launch_q4k_decode_x<WAVES, UPW, R, false>(a, stream);
+    if (a.x_swiglu) return launch_q4k_decode_x<WAVES, UPW, R, 2>(a, stream);
+    return a.x_bf16 ? launch_q4k_decode_x<WAVES, UPW, R, 1>(a, stream)
+                    : launch_q4k_decode_x<WAVES, UPW, R, 0>(a, stream);
 }
 
 // Q4_K decode shapes, from sweeps on MI355X: K of up to 16 units takes 8 waves of

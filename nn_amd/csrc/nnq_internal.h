@@ -70,6 +70,9 @@ struct GemvArgs {
     int kc;               // K elements staged in LDS per chunk (multiple of 256)
     float *logits_out;    // optional copy (argmax fusion)
     unsigned long long *argmax_partial;  // optional per-tile (orderable value, index) keys
+    int x_swiglu;         // x is f32 [m, 2k] (gate | up); the GEMV input is silu(gate) * up (m <= 2)
+    int32_t *status;      // optional: status_mode 1 stores NNQ_OK (one thread), 2 stores
+    int status_mode;      //   NNQ_ERR_NON_FINITE when an output is NaN or infinite
 };
 
 int launch_gemv(int fmt, const GemvArgs &a, void *stream);      // returns hipError_t
@@ -79,6 +82,10 @@ int launch_argmax_reduce(const float *v, int64_t n, uint32_t *idx, int32_t *stat
                          size_t scratch_bytes, void *stream);
 int launch_argmax_final(const unsigned long long *partial, int64_t count, uint32_t *idx, int32_t *status,
                         void *stream);
+// MLP glue: h = silu(gate) * up from gu [m, 2 * inter] (clears *status when given), and
+// the non-finite output check (sets *status to NNQ_ERR_NON_FINITE)
+int launch_swiglu(const float *gu, int64_t m, int64_t inter, float *h, int32_t *status, void *stream);
+int launch_nonfinite_check(const void *y, int y_bf16, int64_t count, int32_t *status, void *stream);
 
 // GEMM (prefill) for Q4_K: x bf16/f32 [m, k] -> y [m, n].  `scratch` holds the
 // staged activation and split-K partials (gemm_scratch_bytes(args) bytes, 256-byte

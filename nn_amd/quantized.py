@@ -329,6 +329,64 @@ def linear_argmax(x: torch.Tensor, weight: QuantizedWeight, bias: Optional[torch
 
 
 # ---------------------------------------------------------------------------------
+# Qwen3 SwiGLU MLP
+# ---------------------------------------------------------------------------------
+
+
+class QuantizedMLP:
+    """Device-resident Qwen3 MLP over quantized weights: gate_proj and up_proj
+    W[inter, hidden] in one format / layout, down_proj W[hidden, inter]
+    (crates/nn-qwen3/src/layers.rs:19-48).  ``forward`` raises NonFiniteData when an
+    output is NaN or infinite, as check_output_finite does (it synchronizes to read
+    the status; ``check=False`` skips that)."""
+
+    def __init__(self, gate, up, down, quant_type: QuantType, hidden: int, inter: int,
+                 down_type: Optional[QuantType] = None, layout: Layout = Layout.GGUF,
+                 down_layout: Optional[Layout] = None, device: int = 0):
+        qt = QuantType(quant_type)
+        dt = QuantType(down_type if down_type is not None else quant_type)
+        dl = Layout(down_layout if down_layout is not None else layout)
+        g, u, d = _as_u8(gate), _as_u8(up), _as_u8(down)
+        if g.size != u.size:
+            raise DataLengthMismatch(f"gate ({g.size} bytes) and up ({u.size} bytes) differ")
+        init(device)
+        h = ctypes.c_void_p()
+        vp = ctypes.c_void_p
+        with torch.cuda.device(device):
+            _check(_lib.load().nnq_mlp_create(int(qt), int(layout), g.ctypes.data_as(vp), u.ctypes.data_as(vp), g.size,
+                                              int(dt), int(dl), d.ctypes.data_as(vp), d.size, int(hidden), int(inter),
+                                              ctypes.byref(h)))
+        self._h = h
+        self.hidden, self.inter, self.device = int(hidden), int(inter), device
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                _lib.load().nnq_mlp_destroy(h)
+            except Exception:
+                pass
+            self._h = None
+
+    def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None, check: bool = True) -> torch.Tensor:
+        """down(silu(gate(x)) * up(x)) over the last dimension of x (Qwen3MLP::forward)."""
+        _validate_input(x, self.hidden)
+        xx = x if x.dtype in (torch.float32, torch.bfloat16) else x.float()
+        xx = xx.reshape(-1, self.hidden).contiguous()
+        m = xx.shape[0]
+        od = out_dtype if out_dtype is not None else torch.float32
+        y = torch.empty((m, self.hidden), dtype=od, device=xx.device)
+        st = torch.zeros(1, dtype=torch.int32, device=xx.device)
+        _check(_lib.load().nnq_mlp_forward(self._h, _ptr(xx), _DTYPE[xx.dtype], m, self.hidden, _ptr(y), _DTYPE[od],
+                                           _ptr(st), _stream(xx)))
+        if check and m > 0 and int(st.item()) != 0:
+            raise NonFiniteData("Qwen3MLP output contains NaN or Inf")
+        return y.reshape(*x.shape[:-1], self.hidden)
+
+    __call__ = forward
+
+
+# ---------------------------------------------------------------------------------
 # GPT-OSS MXFP4 mixture of experts
 # ---------------------------------------------------------------------------------
 

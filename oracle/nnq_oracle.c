@@ -817,3 +817,25 @@ uint64_t orc_splitmix64(uint64_t z) {
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
     return z ^ (z >> 31);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Qwen3 SwiGLU MLP glue (crates/nn-qwen3/src/layers.rs:40-47):              */
+/*   gate = silu(gate_proj(x)), up = up_proj(x), out = down_proj(gate * up), */
+/* silu(x) = x / (1 + exp(-x)) in f32 (crates/nn-core/src/dyn_tensor/ops/    */
+/* math.rs:140), the product elementwise in f32 (broadcast_mul).             */
+/* ------------------------------------------------------------------------ */
+
+void orc_silu_mul(const float *g, const float *u, size_t n, float *h) {
+    for (size_t i = 0; i < n; i++) {
+        const float s = g[i] / (1.0f + expf(-g[i]));
+        h[i] = s * u[i];
+    }
+}
+
+/* check_output_finite (crates/nn-core/src/layers/nan_check.rs:113): 1 when any value is NaN or infinite */
+int orc_any_nonfinite(const float *v, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        if (!isfinite(v[i])) return 1;
+    return 0;
+}
+

@@ -87,6 +87,10 @@ int orc_moe_forward_mxfp4(const float *x, size_t n_tokens, size_t hidden, const 
 /* ---- build-independent splitmix64 (for known-answer checks of the generator) */
 uint64_t orc_splitmix64(uint64_t z);
 
+/* Qwen3 MLP glue: h = silu(g) * u elementwise; non-finite scan of an output */
+void orc_silu_mul(const float *g, const float *u, size_t n, float *h);
+int orc_any_nonfinite(const float *v, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

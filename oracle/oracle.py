@@ -81,6 +81,8 @@ def lib():
                  ctypes.c_int, _f32p, _u32p, _f32p],
             ),
             "orc_splitmix64": (ctypes.c_uint64, [ctypes.c_uint64]),
+            "orc_silu_mul": (None, [_f32p, _f32p, _sz, _f32p]),
+            "orc_any_nonfinite": (ctypes.c_int, [_f32p, _sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -306,6 +308,30 @@ def moe_forward(x, router_logits, top_k, gu_packed, gu_scales, gu_bias, dn_packe
     if rc:
         raise OracleError(f"moe_forward failed ({rc})")
     return out, ti, tw
+
+
+def silu_mul(g, u):
+    g, u = _f32(g), _f32(u)
+    h = np.empty_like(g)
+    lib().orc_silu_mul(_p(g, _f32p), _p(u, _f32p), g.size, _p(h, _f32p))
+    return h
+
+
+_LINEAR = {8: lambda x, b, n: q8_0_matmul(x, b, n), 12: lambda x, b, n: q4k_linear(x, b, n),
+           14: lambda x, b, n: q6k_linear(x, b, n)}
+
+
+def mlp_forward(x, gate, up, down, hidden, inter):
+    """Qwen3MLP::forward (crates/nn-qwen3/src/layers.rs:40-47) over quantized weights:
+    each of gate / up / down is (format id, block bytes) with W[out, in] rows, the
+    linear layers as QLinear::forward / quantized_matmul restate them.  Returns the
+    output and whether check_output_finite would fail."""
+    x = _f32(x)
+    g = _LINEAR[gate[0]](x, gate[1], inter)
+    u = _LINEAR[up[0]](x, up[1], inter)
+    h = silu_mul(g, u)
+    y = _LINEAR[down[0]](h, down[1], hidden)
+    return y, bool(lib().orc_any_nonfinite(_p(y, _f32p), y.size))
 
 
 def splitmix64(z: int) -> int:

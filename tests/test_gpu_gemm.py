@@ -130,3 +130,28 @@ def test_gemm_ring_edges(O, dev, m, n, k):
     check_close(ref, y.cpu().numpy(), f"gemm ring {m}x{n}x{k}")
     yb = nn_amd.quantized_linear(x, w, bias, out_dtype=torch.bfloat16).float().cpu().numpy()
     assert np.array_equal(yb, y.to(torch.bfloat16).float().cpu().numpy()), "bf16 output: the f32 result rounded once"
+
+
+def test_gemm_graph_replay(O, dev):
+    """The prefill GEMM (staging, ring kernel, split-K finalize) captured into a HIP graph
+    replays to the eager result every time, with eager GEMMs between the replays."""
+    import nn_amd
+    m, n, k = 256, 4096, 4096
+    wb = q4k_bytes(n, k, seed=12)
+    w = make_weight("q4_k", wb, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(12, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    ref = nn_amd.quantized_linear(x, w)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            y = nn_amd.quantized_linear(x, w)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {i}"
+        other = nn_amd.quantized_linear(x, w)  # eager call on another stream's workspace
+        torch.cuda.synchronize()
+        assert torch.equal(other, ref)

@@ -511,3 +511,44 @@ def test_q6_k_encoder_round_trip_bound(O):
     err = np.abs(dec - v).reshape(-1, 256).max(axis=1)
     assert np.all(err <= rng_blk * 0.05)
     assert np.corrcoef(dec, v)[0, 1] > 0.999
+
+
+# ---- Qwen3 SwiGLU MLP glue (crates/nn-qwen3/src/layers.rs:40-47) ----------------------
+
+
+def test_silu_mul_closed_form(O):
+    """silu(g) * u = g / (1 + e^-g) * u (ops/math.rs:140): against f64, plus the fixed
+    points silu(0) = 0, silu(-inf) = -0 and silu(+inf) = +inf."""
+    rng = np.random.default_rng(7)
+    g = np.concatenate([rng.normal(0, 4, 4000), [0.0, -0.0, 30.0, -30.0, 88.0, -88.0, 1e-30]]).astype(np.float32)
+    u = rng.normal(0, 2, g.size).astype(np.float32)
+    h = O.silu_mul(g, u)
+    ref = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64))) * u.astype(np.float64)
+    err = np.abs(h - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert err.max() < 4e-7, err.max()
+    # swapping gate and up must change the result (the oracle is not symmetric)
+    assert not np.allclose(O.silu_mul(u, g), h, rtol=1e-3)
+    assert O.silu_mul(np.array([0.0], np.float32), np.array([5.0], np.float32))[0] == 0.0
+    assert np.isinf(O.silu_mul(np.array([np.inf], np.float32), np.array([1.0], np.float32))[0])
+
+
+def test_mlp_forward_matches_f64(O):
+    """The composed MLP (quantized gate / up / down) against f64 math on the oracle's
+    bit-exact dequantized weights; Q4_K gate / up, Q6_K down (the Q4_K_M mix)."""
+    import nn_amd
+    H, I, m = 256, 512, 3
+    wg, wu = nn_amd.synth_normal(3, 1, (I, H), 0.05), nn_amd.synth_normal(3, 2, (I, H), 0.05)
+    wd = nn_amd.synth_normal(3, 3, (H, I), 0.05)
+    bg, bu, bd = O.quantize_q4_k(wg), O.quantize_q4_k(wu), O.quantize_q6_k(wd)
+    x = nn_amd.synth_normal(3, 4, (m, H), 1.0)
+    y, bad = O.mlp_forward(x, (12, bg), (12, bu), (14, bd), H, I)
+    assert not bad
+    Wg = O.dequant_q4_k(bg, I * H).reshape(I, H).astype(np.float64)
+    Wu = O.dequant_q4_k(bu, I * H).reshape(I, H).astype(np.float64)
+    Wd = O.dequant_q6_k(bd, H * I).reshape(H, I).astype(np.float64)
+    g, u = x @ Wg.T, x @ Wu.T
+    ref = (g / (1.0 + np.exp(-g)) * u) @ Wd.T
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    x[1, 7] = np.nan
+    y2, bad2 = O.mlp_forward(x, (12, bg), (12, bu), (14, bd), H, I)
+    assert bad2 and np.isnan(y2[1]).all() and np.isfinite(y2[[0, 2]]).all()
