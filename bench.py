@@ -239,13 +239,24 @@ def bench_moe(steps, warmup, seed=20):
                                 cur_stream()))
 
     sec, nsteps = time_graph([f], steps, warmup, min_graph_calls=20)
+    # the whole block: router Linear on the device, then the same layer
+    rmoe = nn_amd.QuantizedMoE(E, H, I, gp, gs, gb, dp, ds, db, router_weight=nn_amd.synth_normal(seed, 7, (E, H), 0.02),
+                               router_bias=nn_amd.synth_normal(seed, 8, (E,), 0.1))
+    st = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def fb():
+        check(L.nnq_moe_block_forward(rmoe._h, rmoe._router, vp(x), 2, T, K, ctypes.c_float(7.0), vp(y), None, None,
+                                      vp(st), cur_stream()))
+
+    sec_block, _ = time_graph([fb], steps, warmup, min_graph_calls=20)
+    del rmoe
     _, ti, _ = moe.forward(x, logits, top_k=K, return_routing=True)
     used = len(np.unique(ti.cpu().numpy()))
     per_expert = (H * 2 * I + I * H) * 17 // 32 + (2 * I + H) * 4  # MXFP4 codes + scales + biases
     algo = used * per_expert + T * H * 2 + T * E * 4 + T * H * 4
     flops = 2.0 * T * K * (H * 2 * I + I * H)
     return dict(sec=sec, steps=nsteps, gbs=algo / sec / 1e9, tflops=flops / sec / 1e12, tokens_per_s=T / sec,
-                experts_used=used, algo_bytes=algo)
+                experts_used=used, algo_bytes=algo, sec_block=sec_block)
 
 
 def cpu_baseline_q4k(wb, xnp, n, k, budget_s=10.0):
@@ -332,7 +343,7 @@ def main():
         configs["mxfp4_moe_e32_k4_h2880_t256"] = {
             "us": round(g["sec"] * 1e6, 3), "GBps": round(g["gbs"], 1), "frac_hbm": round(g["gbs"] / HBM_PEAK_GBS, 4),
             "TFLOPs": round(g["tflops"], 2), "tokens_per_s": round(g["tokens_per_s"], 1),
-            "experts_used": g["experts_used"]}
+            "experts_used": g["experts_used"], "with_router_us": round(g["sec_block"] * 1e6, 3)}
         for name, c in configs.items():
             log(f"  {name}: {c}")
 

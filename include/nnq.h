@@ -83,6 +83,7 @@ typedef enum nnq_dtype {
 typedef struct nnq_weight nnq_weight;   /* opaque: device-resident, repacked block weight */
 typedef struct nnq_moe nnq_moe;         /* opaque: device-resident MXFP4 expert weights + biases */
 typedef struct nnq_mlp nnq_mlp;         /* opaque: device-resident SwiGLU MLP (gate | up, down) */
+typedef struct nnq_router nnq_router;   /* opaque: device-resident f32 router Linear */
 
 /* ---- device ------------------------------------------------------------------- */
 
@@ -202,6 +203,31 @@ int nnq_moe_destroy(nnq_moe *moe);
 int nnq_moe_forward(const nnq_moe *moe, const void *x, nnq_dtype x_dtype, int64_t tokens,
                     const float *router_logits, int top_k, float swiglu_limit, float *y, uint32_t *topk_idx,
                     float *topk_w, void *stream);
+
+/* Upload the GPT-OSS router Linear: weight f32 [num_experts, hidden], bias f32
+ * [num_experts] or NULL (host).  hidden a multiple of 32, at most 256 experts.
+ * Replaces QuantizedDecoderLayer::load's router (crates/nn-gptoss/src/quantized_model.rs:63-67),
+ * which keeps it at full precision. */
+int nnq_router_create(int64_t num_experts, int64_t hidden, const float *weight, const float *bias, nnq_router **out);
+
+int nnq_router_destroy(nnq_router *router);
+
+/* logits[t, E] (f32) = x[t, hidden] @ W^T + bias, f32 products and sums; x NNQ_F32 or
+ * NNQ_BF16 (16-byte aligned).  Replaces the router's Linear::forward
+ * (crates/nn-core/src/layers/core_layers.rs:118-140, called at quantized_model.rs:138). */
+int nnq_router_logits(const nnq_router *router, const void *x, nnq_dtype x_dtype, int64_t tokens, float *logits,
+                      void *stream);
+
+/* The whole MoE block of one layer: router logits on the device, then nnq_moe_forward's
+ * routing, experts and combine, then the output check — QuantizedDecoderLayer::moe_forward
+ * with its router (crates/nn-gptoss/src/quantized_model.rs:132-194).  Nothing returns to
+ * the host between the steps.  status_dev (device int, may be NULL): NNQ_OK, or
+ * NNQ_ERR_NON_FINITE when an output is NaN or infinite (check_output_finite,
+ * crates/nn-core/src/layers/nan_check.rs:113-140).  Other arguments as nnq_moe_forward;
+ * the router must match the MoE's experts and hidden size (NNQ_ERR_SHAPE_MISMATCH). */
+int nnq_moe_block_forward(const nnq_moe *moe, const nnq_router *router, const void *x, nnq_dtype x_dtype,
+                          int64_t tokens, int top_k, float swiglu_limit, float *y, uint32_t *topk_idx, float *topk_w,
+                          int32_t *status_dev, void *stream);
 
 /* Decode expert e's weights to f32 (device): gate_up [hidden, 2*inter] and down
  * [inter, hidden] — bit-exact with Mxfp4Tensor::dequantize

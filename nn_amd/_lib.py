@@ -38,6 +38,11 @@ SIGNATURES = {
     "nnq_moe_forward": (c_int, [c_void_p, c_void_p, c_int, c_i64, c_void_p, c_int, c_float, c_void_p, c_void_p,
                                 c_void_p, c_void_p]),
     "nnq_moe_dequant_expert": (c_int, [c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),
+    "nnq_router_create": (c_int, [c_i64, c_i64, c_void_p, c_void_p, ctypes.POINTER(c_void_p)]),
+    "nnq_router_destroy": (c_int, [c_void_p]),
+    "nnq_router_logits": (c_int, [c_void_p, c_void_p, c_int, c_i64, c_void_p, c_void_p]),
+    "nnq_moe_block_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_i64, c_int, c_float, c_void_p, c_void_p,
+                                      c_void_p, c_void_p, c_void_p]),
     "nnq_mlp_create": (c_int, [c_int, c_int, c_void_p, c_void_p, c_sz, c_int, c_int, c_void_p, c_sz, c_i64, c_i64,
                                ctypes.POINTER(c_void_p)]),
     "nnq_mlp_destroy": (c_int, [c_void_p]),

@@ -28,6 +28,12 @@ struct nnq_mlp {
     int64_t hidden = 0, inter = 0;
 };
 
+struct nnq_router {
+    float *w = nullptr;     // [E, hidden] f32
+    float *b = nullptr;     // [E] f32 or null
+    int64_t E = 0, H = 0;
+};
+
 struct nnq_moe {
     MoeDev d;
     int device = 0;
@@ -512,8 +518,8 @@ int nnq_moe_forward(const nnq_moe *m, const void *x, nnq_dtype x_dtype, int64_t 
     HIP_TRY(s.alloc(moe_scratch_bytes(tokens, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16),
                     (hipStream_t)stream),
             "scratch alloc");
-    int e = launch_moe(m->d, x, x_dtype == NNQ_BF16, tokens, router_logits, top_k, swiglu_limit, y, topk_idx, topk_w,
-                       s.p, stream);
+    int e = launch_moe(m->d, x, x_dtype == NNQ_BF16, tokens, router_logits, 1, nullptr, top_k, swiglu_limit, y,
+                       topk_idx, topk_w, nullptr, s.p, stream);
     if (e) return hip_fail((hipError_t)e, "moe launch");
     return NNQ_OK;
 }
@@ -596,6 +602,108 @@ int nnq_mlp_forward(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t 
         e = launch_nonfinite_check(y, y_dtype == NNQ_BF16, m * p->hidden, status_dev, stream);
         if (e) return hip_fail((hipError_t)e, "output check launch");
     }
+    return NNQ_OK;
+}
+
+// ---- GPT-OSS router and the whole MoE block ---------------------------------------
+
+int nnq_router_create(int64_t num_experts, int64_t hidden, const float *weight, const float *bias, nnq_router **out) {
+    if (!out) return fail(NNQ_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (!weight) return fail(NNQ_ERR_INVALID_ARGUMENT, "router weight is null");
+    if (num_experts <= 0 || num_experts > 256)
+        return fail(NNQ_ERR_INVALID_SHAPE, "router experts %lld (1..256)", (long long)num_experts);
+    if (hidden <= 0 || hidden % 32)
+        return fail(NNQ_ERR_INVALID_SHAPE, "router hidden %lld is not a positive multiple of 32", (long long)hidden);
+    nnq_router *r = new nnq_router;
+    r->E = num_experts;
+    r->H = hidden;
+    const size_t wb = (size_t)num_experts * hidden * 4;
+    hipError_t e = hipMalloc(&r->w, wb);
+    if (e == hipSuccess) e = hipMemcpy(r->w, weight, wb, hipMemcpyHostToDevice);
+    if (e == hipSuccess && bias) {
+        e = hipMalloc(&r->b, (size_t)num_experts * 4);
+        if (e == hipSuccess) e = hipMemcpy(r->b, bias, (size_t)num_experts * 4, hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+        if (r->w) hipFree(r->w);
+        if (r->b) hipFree(r->b);
+        delete r;
+        return hip_fail(e, "router upload");
+    }
+    *out = r;
+    return NNQ_OK;
+}
+
+int nnq_router_destroy(nnq_router *r) {
+    if (!r) return NNQ_OK;
+    if (r->w) hipFree(r->w);
+    if (r->b) hipFree(r->b);
+    delete r;
+    return NNQ_OK;
+}
+
+static int check_router_input(const nnq_router *r, const void *x, nnq_dtype x_dtype, int64_t tokens) {
+    if (!r) return fail(NNQ_ERR_INVALID_ARGUMENT, "router handle is null");
+    if (tokens < 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "tokens < 0");
+    if (x_dtype != NNQ_F32 && x_dtype != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d", (int)x_dtype);
+    if (tokens > 0 && !x) return fail(NNQ_ERR_INVALID_ARGUMENT, "x is null");
+    if ((uintptr_t)x & 15) return fail(NNQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    return NNQ_OK;
+}
+
+int nnq_router_logits(const nnq_router *r, const void *x, nnq_dtype x_dtype, int64_t tokens, float *logits,
+                      void *stream) {
+    int rc = check_router_input(r, x, x_dtype, tokens);
+    if (rc) return rc;
+    if (tokens == 0) return NNQ_OK;
+    if (!logits) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits is null");
+    const size_t pb = router_partial_bytes(tokens, r->H, (int)r->E);
+    Scratch s;
+    if (pb) HIP_TRY(s.alloc(pb, (hipStream_t)stream), "scratch alloc");
+    int ks = 1;
+    int e = launch_router_logits(x, x_dtype == NNQ_BF16, tokens, r->H, r->w, r->b, (int)r->E,
+                                 pb ? reinterpret_cast<float *>(s.p) : logits, &ks, nullptr, stream);
+    if (e) return hip_fail((hipError_t)e, "router launch");
+    if (ks > 1) {
+        e = launch_router_finalize(reinterpret_cast<float *>(s.p), ks, tokens, (int)r->E, r->b, logits, stream);
+        if (e) return hip_fail((hipError_t)e, "router finalize launch");
+    }
+    return NNQ_OK;
+}
+
+int nnq_moe_block_forward(const nnq_moe *m, const nnq_router *r, const void *x, nnq_dtype x_dtype, int64_t tokens,
+                          int top_k, float swiglu_limit, float *y, uint32_t *topk_idx, float *topk_w,
+                          int32_t *status_dev, void *stream) {
+    if (!m) return fail(NNQ_ERR_INVALID_ARGUMENT, "MoE handle is null");
+    int rc = check_router_input(r, x, x_dtype, tokens);
+    if (rc) return rc;
+    if (r->E != m->d.E || r->H != m->d.H)
+        return fail(NNQ_ERR_SHAPE_MISMATCH, "router [%lld, %lld] does not match the MoE's %lld experts x hidden %lld",
+                    (long long)r->E, (long long)r->H, (long long)m->d.E, (long long)m->d.H);
+    if (top_k <= 0 || top_k > m->d.E || top_k > 8)
+        return fail(NNQ_ERR_INVALID_SHAPE, "topk k=%d out of range for %lld experts", top_k, (long long)m->d.E);
+    if (tokens == 0) return NNQ_OK;
+    if (!y) return fail(NNQ_ERR_INVALID_ARGUMENT, "y is null");
+    if (tokens * top_k > 16384)
+        return fail(NNQ_ERR_UNSUPPORTED, "at most 16384 token-expert assignments per call (%lld)",
+                    (long long)(tokens * top_k));
+    const size_t lg_bytes =
+        (std::max(router_partial_bytes(tokens, r->H, (int)r->E), (size_t)tokens * m->d.E * 4) + 255) & ~(size_t)255;
+    Scratch s;
+    HIP_TRY(s.alloc(lg_bytes + moe_scratch_bytes(tokens, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16),
+                    (hipStream_t)stream),
+            "scratch alloc");
+    float *logits = reinterpret_cast<float *>(s.p);
+    int ks = 1;
+    int e = launch_router_logits(x, x_dtype == NNQ_BF16, tokens, r->H, r->w, r->b, (int)r->E, logits, &ks, status_dev,
+                                 stream);
+    if (e) return hip_fail((hipError_t)e, "router launch");
+    // the routing kernel sums the K-part slabs and adds the bias (with one part the
+    // router kernel already did)
+    e = launch_moe(m->d, x, x_dtype == NNQ_BF16, tokens, logits, ks, ks > 1 ? r->b : nullptr, top_k, swiglu_limit, y,
+                   topk_idx, topk_w, status_dev, reinterpret_cast<uint8_t *>(s.p) + lg_bytes, stream);
+    if (e) return hip_fail((hipError_t)e, "moe launch");
     return NNQ_OK;
 }
 

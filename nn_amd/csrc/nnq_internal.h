@@ -134,9 +134,20 @@ struct MoeDev {
     const float *dn_b;      // [E, H]
 };
 size_t moe_scratch_bytes(int64_t T, int64_t E, int64_t H, int64_t I, int top_k, int x_bf16);
-int launch_moe(const MoeDev &m, const void *x, int x_bf16, int64_t T, const float *logits, int top_k, float limit,
-               float *y, uint32_t *topk_idx, float *topk_w, void *scratch, void *stream);
+// logits: nsplit slabs [T][E] summed in order, plus bias when given (nsplit 1, no bias: the logits);
+// status (optional, cleared beforehand by the caller) flags a non-finite output
+int launch_moe(const MoeDev &m, const void *x, int x_bf16, int64_t T, const float *logits, int nsplit,
+               const float *bias, int top_k, float limit, float *y, uint32_t *topk_idx, float *topk_w,
+               int32_t *status, void *scratch, void *stream);
 int launch_moe_dequant(const MoeDev &m, int64_t e, float *gate_up, float *down, void *stream);
+// router Linear x[T, H] @ W[E, H]^T (+ bias), H a multiple of 16, over *nsplit K parts: with one
+// part `partial` receives the logits (bias added), else nsplit slabs [T][E] of partial sums
+// (router_partial_bytes; the bias is left to the consumer).  Clears *status when given.
+size_t router_partial_bytes(int64_t T, int64_t H, int E);
+int launch_router_logits(const void *x, int x_bf16, int64_t T, int64_t H, const float *W, const float *bias, int E,
+                         float *partial, int *nsplit, int32_t *status, void *stream);
+int launch_router_finalize(const float *partial, int ks, int64_t T, int E, const float *bias, float *logits,
+                           void *stream);
 // host repack of one weight (codes and scales of E experts, K rows, N columns)
 void moe_repack(const uint8_t *packed, const uint8_t *scales, int64_t E, int64_t K, int64_t N, uint8_t *dst_codes,
                 uint8_t *dst_scales);

@@ -23,6 +23,7 @@
 // and 8 scale bytes per lane and feeds two 16x16x32 bf16 MFMAs per 16 token rows.
 // Activations: bf16 input is used as is (exact); f32 input and the SwiGLU output h
 // are carried as bf16 hi + lo pairs (two MFMAs, ~2^-17 relative).
+#include <algorithm>
 #include <type_traits>
 
 #include "nnq_device.h"
@@ -136,20 +137,29 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
-__global__ __launch_bounds__(256) void moe_route_kernel(const float *logits, int64_t T, int E, int k, uint32_t *ti,
-                                                        float *tw, uint32_t *ti_out, float *tw_out) {
+// `logits` holds nsplit slabs [T][E] whose sum in slab order, plus `bias` when given,
+// are the logits (the router's K parts; nsplit = 1 and no bias: logits given)
+__global__ __launch_bounds__(256) void moe_route_kernel(const float *logits, int nsplit, const float *bias, int64_t T,
+                                                        int E, int k, uint32_t *ti, float *tw, uint32_t *ti_out,
+                                                        float *tw_out) {
     __shared__ float ex[4][256];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int64_t t = (int64_t)blockIdx.x * 4 + wv;
     if (t >= T) return;  // wave-uniform; no barrier below
-    const float *x = logits + t * E;
     float v[4];
     float mx = -INFINITY;
     int ninf = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int c = lane + 64 * j;
-        v[j] = c < E ? x[c] : -INFINITY;
+        if (c < E) {
+            float lv = logits[t * E + c];
+            for (int sp = 1; sp < nsplit; sp++) lv += logits[((int64_t)sp * T + t) * E + c];
+            if (bias) lv += bias[c];
+            v[j] = lv;
+        } else {
+            v[j] = -INFINITY;
+        }
         mx = fmaxf(mx, v[j]);
         ninf += (c < E && v[j] == INFINITY);
     }
@@ -295,6 +305,91 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, i
         pos[i] = p;
         stok[p] = (int32_t)(i / k);
     }
+}
+
+// ---------------------------------------------------------------------------------
+// router Linear: logits[t, e] = x[t, :] . W[e, :] + b[e] (Linear::forward, x @ W^T + bias,
+// crates/nn-core/src/layers/core_layers.rs:118-140, as moe_forward calls it at
+// crates/nn-gptoss/src/quantized_model.rs:138), f32 products and sums on the
+// 16x16x4 f32 MFMA.  Workgroup (token tile, expert tile, K part z) = 16 tokens x 16
+// experts over K part z of KS; its 4 waves take quarters of the part and are summed
+// in wave order; a part's sum goes to slab z of `out` (KS > 1, the routing kernel
+// adds the slabs in order and the bias) or, with the bias, straight to the logits
+// (KS = 1).  Lane 16g + r loads 4 consecutive k of token r and of expert r, and MFMA
+// j takes element j, so every k meets its own pair once.  Block (0, 0, 0) clears the
+// call's status (set later by the output check).
+// ---------------------------------------------------------------------------------
+constexpr int kRouterBatch = 4;  // 16-k chunks whose loads a wave issues together
+
+template <bool XB>
+__global__ __launch_bounds__(256) void router_logits_kernel(const void *x, int64_t T, int64_t H, const float *W,
+                                                            const float *bias, int E, float *out, int32_t *status) {
+    __shared__ floatx4 red[4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t t0 = (int64_t)blockIdx.x * 16;
+    const int e0 = (int)blockIdx.y * 16, KS = (int)gridDim.z, z = (int)blockIdx.z;
+    if (status && blockIdx.x == 0 && blockIdx.y == 0 && z == 0 && threadIdx.x == 0) *status = NNQ_OK;
+    const int64_t trow = min(t0 + r, T - 1);
+    const int erow = min(e0 + r, E - 1);
+    const int nch = (int)(H / 16);
+    const int p0 = z * nch / KS, p1 = (z + 1) * nch / KS;  // this part's chunks
+    const int c0 = p0 + wv * (p1 - p0) / 4, c1 = p0 + (wv + 1) * (p1 - p0) / 4;
+    const float *wp = W + (int64_t)erow * H + 4 * g;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int cb = c0; cb < c1; cb += kRouterBatch) {
+        float xv[kRouterBatch][4];
+        floatx4 wv4[kRouterBatch];
+#pragma unroll
+        for (int u = 0; u < kRouterBatch; u++) {
+            const int c = min(cb + u, c1 - 1);  // past the wave's range: a repeat, not used
+            if (XB) {
+                const u32x2 b2 = *reinterpret_cast<const u32x2 *>(reinterpret_cast<const uint16_t *>(x) + trow * H +
+                                                                  (int64_t)c * 16 + 4 * g);
+                xv[u][0] = __uint_as_float(b2[0] << 16);
+                xv[u][1] = __uint_as_float(b2[0] & 0xFFFF0000u);
+                xv[u][2] = __uint_as_float(b2[1] << 16);
+                xv[u][3] = __uint_as_float(b2[1] & 0xFFFF0000u);
+            } else {
+                const floatx4 f = *reinterpret_cast<const floatx4 *>(reinterpret_cast<const float *>(x) + trow * H +
+                                                                     (int64_t)c * 16 + 4 * g);
+                xv[u][0] = f[0], xv[u][1] = f[1], xv[u][2] = f[2], xv[u][3] = f[3];
+            }
+            wv4[u] = *reinterpret_cast<const floatx4 *>(wp + (int64_t)c * 16);
+        }
+#pragma unroll
+        for (int u = 0; u < kRouterBatch; u++) {
+            if (cb + u >= c1) break;  // wave-uniform
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[u][j], wv4[u][j], acc, 0, 0, 0);
+        }
+    }
+    red[wv][lane] = acc;
+    __syncthreads();
+    if (wv == 0) {
+        floatx4 sum = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < 4; w++) sum += red[w][lane];
+        // lane 16g + r holds D[4g + i][r]: token t0 + 4g + i, expert e0 + r
+        const int e = e0 + r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t t = t0 + 4 * g + i;
+            if (t < T && e < E) {
+                if (KS == 1)
+                    out[t * E + e] = sum[i] + (bias ? bias[e] : 0.0f);
+                else
+                    out[((int64_t)z * T + t) * E + e] = sum[i];
+            }
+        }
+    }
+}
+
+// K parts of the router: enough workgroups to spread the loads, at most 4 batches per wave
+inline int router_parts(int64_t T, int64_t H, int E) {
+    const int64_t tiles = ((T + 15) / 16) * ((E + 15) / 16), nch = H / 16;
+    int64_t ks = std::max<int64_t>((256 + tiles - 1) / tiles, (nch + 4 * 4 * kRouterBatch - 1) / (4 * 4 * kRouterBatch));
+    return (int)std::min<int64_t>(std::min<int64_t>(ks, nch), 64);
 }
 
 // f32 activations -> bf16 hi / lo planes
@@ -590,8 +685,10 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
     }
 }
 // y[t] = ((0 + w_a * y_a) + w_b * y_b) + ... over the token's experts a < b < ...
+// A NaN or infinite output sets *status (when given) to NNQ_ERR_NON_FINITE, the
+// check_output_finite of moe_forward (crates/nn-core/src/layers/nan_check.rs:113-140).
 template <int k>
-__global__ __launch_bounds__(256) void moe_combine_kernel(MoeScratch sc, int64_t H, float *y) {
+__global__ __launch_bounds__(256) void moe_combine_kernel(MoeScratch sc, int64_t H, float *y, int32_t *status) {
     const int64_t t = blockIdx.x;
     uint32_t ex[k];
     int32_t ps[k];
@@ -617,12 +714,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeScratch sc, int64_t
             ws[q] = sw ? w1 : w0;
             ws[q + 1] = sw ? w0 : w1;
         }
+    bool bad = false;
     for (int64_t c = threadIdx.x; c < H; c += 256) {
         float acc = 0.0f;
 #pragma unroll
         for (int s = 0; s < k; s++) acc = acc + sc.yb[(int64_t)ps[s] * H + c] * ws[s];
         y[t * H + c] = acc;
+        bad |= !(fabsf(acc) <= 3.402823466e38f);
     }
+    if (status && __any(bad) && (threadIdx.x & 63) == 0) *status = NNQ_ERR_NON_FINITE;
 }
 
 // ---------------------------------------------------------------------------------
@@ -703,16 +803,17 @@ static int launch_stream(const MoeDev &d, const MoeScratch &sc, const MoeRun &ru
     return launch_stream_t<P, GU, 1, false>(d, sc, run, st, moe_lds<P, GU, 1, false>(KB));
 }
 
-int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const float *logits, int k, float limit,
-               float *y, uint32_t *topk_idx, float *topk_w, void *scratch, void *stream) {
+int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const float *logits, int nsplit,
+               const float *bias, int k, float limit, float *y, uint32_t *topk_idx, float *topk_w, int32_t *status,
+               void *scratch, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     int e = 0;
     const MoeScratch sc = carve(scratch, T, d.E, d.H, d.I, k, x_bf16);
     MoeRun run;
     run.A = T * k;
     run.limit = limit;
-    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, T, (int)d.E, k,
-                       sc.ti, sc.tw, topk_idx, topk_w);
+    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, nsplit, bias, T,
+                       (int)d.E, k, sc.ti, sc.tw, topk_idx, topk_w);
     switch (k) {
 #define NNQ_PERM(K)                                                                                              \
     case K:                                                                                                      \
@@ -744,13 +845,49 @@ int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const floa
     switch (k) {
 #define NNQ_COMB(K)                                                                                  \
     case K:                                                                                          \
-        hipLaunchKernelGGL(moe_combine_kernel<K>, dim3((unsigned)T), dim3(256), 0, st, sc, d.H, y); \
+        hipLaunchKernelGGL(moe_combine_kernel<K>, dim3((unsigned)T), dim3(256), 0, st, sc, d.H, y, status); \
         break;
         NNQ_COMB(1) NNQ_COMB(2) NNQ_COMB(3) NNQ_COMB(4) NNQ_COMB(5) NNQ_COMB(6) NNQ_COMB(7) NNQ_COMB(8)
 #undef NNQ_COMB
     default:
         return (int)hipErrorInvalidValue;
     }
+    return (int)hipGetLastError();
+}
+
+size_t router_partial_bytes(int64_t T, int64_t H, int E) {
+    const int ks = router_parts(T, H, E);
+    return ks > 1 ? (size_t)ks * T * E * 4 : 0;
+}
+
+int launch_router_logits(const void *x, int x_bf16, int64_t T, int64_t H, const float *W, const float *bias, int E,
+                         float *partial, int *nsplit, int32_t *status, void *stream) {
+    const int ks = router_parts(T, H, E);
+    const dim3 grid((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16), (unsigned)ks);
+    if (x_bf16)
+        hipLaunchKernelGGL(router_logits_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, x, T, H, W, bias, E,
+                           partial, status);
+    else
+        hipLaunchKernelGGL(router_logits_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, x, T, H, W, bias, E,
+                           partial, status);
+    *nsplit = ks;
+    return (int)hipGetLastError();
+}
+
+// logits[t, e] = sum of the K-part slabs in order + bias (the standalone router call)
+__global__ __launch_bounds__(256) void router_finalize_kernel(const float *partial, int ks, int64_t T, int E,
+                                                              const float *bias, float *logits) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= T * E) return;
+    float v = partial[i];
+    for (int s = 1; s < ks; s++) v += partial[(int64_t)s * T * E + i];
+    logits[i] = v + (bias ? bias[i % E] : 0.0f);
+}
+
+int launch_router_finalize(const float *partial, int ks, int64_t T, int E, const float *bias, float *logits,
+                           void *stream) {
+    hipLaunchKernelGGL(router_finalize_kernel, dim3((unsigned)((T * E + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, partial, ks, T, E, bias, logits);
     return (int)hipGetLastError();
 }
 

@@ -400,7 +400,7 @@ class QuantizedMoE:
     """
 
     def __init__(self, num_experts, hidden, inter, gu_packed, gu_scales, gu_bias, dn_packed, dn_scales, dn_bias,
-                 device: int = 0):
+                 device: int = 0, router_weight=None, router_bias=None):
         E, H, I = int(num_experts), int(hidden), int(inter)
         gp, gs, dp, ds = (_as_u8(a) for a in (gu_packed, gu_scales, dn_packed, dn_scales))
         if gp.size != E * H * 2 * I // 2 or gs.size != E * H * 2 * I // 32:
@@ -417,28 +417,79 @@ class QuantizedMoE:
                                               gb.ctypes.data_as(vp), dp.ctypes.data_as(vp), ds.ctypes.data_as(vp),
                                               db.ctypes.data_as(vp), ctypes.byref(h)))
         self._h = h
+        self._router = None
         self.num_experts, self.hidden, self.inter, self.device = E, H, I, device
+        if router_weight is not None:
+            rw = np.ascontiguousarray(np.asarray(router_weight, np.float32))
+            if rw.shape != (E, H):
+                raise ShapeMismatch(f"router weight must be [{E}, {H}], got {list(rw.shape)}")
+            rb = None if router_bias is None else np.ascontiguousarray(np.asarray(router_bias, np.float32))
+            if rb is not None and rb.shape != (E,):
+                raise BiasMismatch(f"router bias must be [{E}], got {list(rb.shape)}")
+            r = ctypes.c_void_p()
+            with torch.cuda.device(device):
+                _check(_lib.load().nnq_router_create(E, H, rw.ctypes.data_as(vp),
+                                                     None if rb is None else rb.ctypes.data_as(vp), ctypes.byref(r)))
+            self._router = r
 
     def __del__(self):
-        h = getattr(self, "_h", None)
-        if h is not None and h.value:
-            try:
-                _lib.load().nnq_moe_destroy(h)
-            except Exception:
-                pass
-            self._h = None
+        for name, fn in (("_router", "nnq_router_destroy"), ("_h", "nnq_moe_destroy")):
+            h = getattr(self, name, None)
+            if h is not None and h.value:
+                try:
+                    getattr(_lib.load(), fn)(h)
+                except Exception:
+                    pass
+                setattr(self, name, None)
+
+    def _input(self, x):
+        if x.dim() != 2 or x.shape[1] != self.hidden:
+            raise ShapeMismatch(f"x must be [tokens, {self.hidden}]")
+        return x.contiguous() if x.dtype in (torch.float32, torch.bfloat16) else x.float().contiguous()
+
+    def router_logits(self, x: torch.Tensor) -> torch.Tensor:
+        """The router Linear alone: x @ W^T + b in f32 (quantized_model.rs:138)."""
+        if self._router is None:
+            raise Unsupported("this MoE was created without a router")
+        xx = self._input(x)
+        lg = torch.empty((xx.shape[0], self.num_experts), dtype=torch.float32, device=xx.device)
+        _check(_lib.load().nnq_router_logits(self._router, _ptr(xx), _DTYPE[xx.dtype], xx.shape[0], _ptr(lg),
+                                             _stream(xx)))
+        return lg
+
+    def block_forward(self, x: torch.Tensor, top_k: int = 4, swiglu_limit: float = 7.0,
+                      return_routing: bool = False, check: bool = True):
+        """moe_forward with its router (quantized_model.rs:132-194): logits, routing,
+        experts and combine on the device; NonFiniteData when an output is NaN or
+        infinite (check_output_finite; synchronizes to read the status unless check=False)."""
+        if self._router is None:
+            raise Unsupported("this MoE was created without a router")
+        xx = self._input(x)
+        T = xx.shape[0]
+        if top_k <= 0 or top_k > self.num_experts:
+            raise InvalidShape(f"topk k={top_k} out of range for dim 1 (size {self.num_experts})")
+        y = torch.empty((T, self.hidden), dtype=torch.float32, device=xx.device)
+        ti = torch.empty((T, top_k), dtype=torch.int32, device=xx.device) if return_routing else None
+        tw = torch.empty((T, top_k), dtype=torch.float32, device=xx.device) if return_routing else None
+        st = torch.zeros(1, dtype=torch.int32, device=xx.device)
+        _check(_lib.load().nnq_moe_block_forward(self._h, self._router, _ptr(xx), _DTYPE[xx.dtype], T, int(top_k),
+                                                 float(swiglu_limit), _ptr(y), _ptr(ti), _ptr(tw), _ptr(st),
+                                                 _stream(xx)))
+        if check and T > 0 and int(st.item()) != 0:
+            raise NonFiniteData("QuantizedMoeBlock output contains NaN or Inf")
+        if return_routing:
+            return y, ti, tw
+        return y
 
     def forward(self, x: torch.Tensor, router_logits: torch.Tensor, top_k: int = 4, swiglu_limit: float = 7.0,
                 return_routing: bool = False):
         """moe_forward (quantized_model.rs:132-194) with router logits given."""
-        if x.dim() != 2 or x.shape[1] != self.hidden:
-            raise ShapeMismatch(f"x must be [tokens, {self.hidden}]")
-        T = x.shape[0]
+        xx = self._input(x)
+        T = xx.shape[0]
         if router_logits.shape != (T, self.num_experts):
             raise ShapeMismatch(f"router logits must be [{T}, {self.num_experts}]")
         if top_k <= 0 or top_k > self.num_experts:
             raise InvalidShape(f"topk k={top_k} out of range for dim 1 (size {self.num_experts})")
-        xx = x.contiguous() if x.dtype in (torch.float32, torch.bfloat16) else x.float().contiguous()
         lg = router_logits.float().contiguous()
         y = torch.empty((T, self.hidden), dtype=torch.float32, device=xx.device)
         ti = torch.empty((T, top_k), dtype=torch.int32, device=xx.device) if return_routing else None

@@ -310,6 +310,15 @@ def moe_forward(x, router_logits, top_k, gu_packed, gu_scales, gu_bias, dn_packe
     return out, ti, tw
 
 
+def router_logits(x, weight, bias=None):
+    """The router Linear (crates/nn-core/src/layers/core_layers.rs:118-140): x @ W^T,
+    then + bias, in f32."""
+    y = matmul_xwt(x, weight)
+    if bias is not None:
+        y = (y + _f32(bias)[None, :]).astype(np.float32)
+    return y
+
+
 def silu_mul(g, u):
     g, u = _f32(g), _f32(u)
     h = np.empty_like(g)

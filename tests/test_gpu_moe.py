@@ -141,3 +141,67 @@ def test_moe_baseline_config(O, dev):
     counts = np.bincount(rti.ravel(), minlength=E)
     print(f"expert loads min {counts.min()} max {counts.max()}")
     check_close(ref, y.cpu().numpy(), "moe config 5")
+
+
+def make_router(E, H, seed):
+    import nn_amd
+    return nn_amd.synth_normal(seed, 7, (E, H), 0.02), nn_amd.synth_normal(seed, 8, (E,), 0.1)
+
+
+@pytest.mark.parametrize("E,H,T,xdt", [(32, 2880, 256, "bf16"), (32, 2880, 37, "f32"), (20, 96, 5, "bf16")])
+def test_router_logits_vs_oracle(O, dev, E, H, T, xdt):
+    """The router Linear on the f32 MFMA against the oracle's f32 x @ W^T + b (same
+    products, another summation order): max abs difference <= 1e-5 of the peak."""
+    import nn_amd
+    I = 32
+    L = make_layer(E, H, I, seed=E + H)
+    rw, rb = make_router(E, H, seed=T)
+    moe = nn_amd.QuantizedMoE(E, H, I, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"],
+                              router_weight=rw, router_bias=rb)
+    x = torch.from_numpy(nn_amd.synth_normal(T, 5, (T, H), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    got = moe.router_logits(x).cpu().numpy()
+    ref = O.router_logits(x.float().cpu().numpy(), rw, rb)
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max(), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("E,H,I,T,k,xdt", [(8, 256, 320, 64, 4, "bf16"), (16, 96, 64, 150, 4, "f32"),
+                                          (32, 2880, 2880, 256, 4, "bf16")])
+def test_moe_block_vs_oracle(O, dev, E, H, I, T, k, xdt):
+    """moe_forward with its router: device logits, routing, experts and combine against
+    the oracle's router Linear followed by its moe_forward restatement."""
+    import nn_amd
+    L = make_layer(E, H, I, seed=E * 3 + H)
+    rw, rb = make_router(E, H, seed=E + T)
+    moe = nn_amd.QuantizedMoE(E, H, I, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"],
+                              router_weight=rw, router_bias=rb)
+    x = torch.from_numpy(nn_amd.synth_normal(T + 1, 5, (T, H), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    y, ti, tw = moe.block_forward(x, top_k=k, return_routing=True)
+    xf = x.float().cpu().numpy()
+    logits = O.router_logits(xf, rw, rb)
+    if H * I > 100000:
+        ref, rti, rtw = ref_f64(O, xf, logits, k, L, E, H, I)
+    else:
+        ref, rti, rtw = O.moe_forward(xf, logits, k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    assert np.array_equal(ti.cpu().numpy().astype(np.uint32), rti), "routing differs"
+    assert np.allclose(tw.cpu().numpy(), rtw, rtol=1e-5, atol=1e-6)
+    check_close(ref, y.cpu().numpy(), f"moe block E={E} H={H} I={I} T={T} k={k} x={xdt}")
+
+
+def test_moe_block_nonfinite_raises(O, dev):
+    import nn_amd
+    E, H, I, T = 4, 64, 64, 6
+    L = make_layer(E, H, I, seed=3)
+    rw, rb = make_router(E, H, seed=3)
+    moe = nn_amd.QuantizedMoE(E, H, I, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"],
+                              router_weight=rw, router_bias=rb)
+    x = torch.from_numpy(nn_amd.synth_normal(3, 5, (T, H), 1.0)).to(dev)
+    moe.block_forward(x, top_k=2)
+    x[2, 5] = float("nan")
+    with pytest.raises(nn_amd.NonFiniteData):
+        moe.block_forward(x, top_k=2)
+    x[2, 5] = 1.0
+    moe.block_forward(x, top_k=2)  # the status is cleared by every call

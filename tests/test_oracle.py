@@ -552,3 +552,16 @@ def test_mlp_forward_matches_f64(O):
     x[1, 7] = np.nan
     y2, bad2 = O.mlp_forward(x, (12, bg), (12, bu), (14, bd), H, I)
     assert bad2 and np.isnan(y2[1]).all() and np.isfinite(y2[[0, 2]]).all()
+
+
+def test_router_logits_matches_f64(O):
+    """Router Linear (core_layers.rs:118-140): x @ W^T + b against f64; the bias is added
+    after the product (a missing or doubled bias fails)."""
+    import nn_amd
+    x = nn_amd.synth_normal(11, 1, (5, 96), 1.0)
+    w = nn_amd.synth_normal(11, 2, (8, 96), 0.1)
+    b = nn_amd.synth_normal(11, 3, (8,), 1.0)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + b.astype(np.float64)
+    got = O.router_logits(x, w, b)
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+    assert np.abs(O.router_logits(x, w) + b - ref).max() <= 1e-5 * np.abs(ref).max()
