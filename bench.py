@@ -160,8 +160,20 @@ def bench_lm_head(steps, warmup, seed=3):
         return f
 
     sec, nsteps = time_graph([launcher(i) for i in range(len(copies))], steps, warmup)
+    # the same LM head followed by sampling (temperature 0.7, top-k 50, top-p 0.9, the
+    # SamplingConfig defaults) over the 151936 logits, on the device
+    from nn_amd import _lib as NL
+    cfg = NL.Sampling(0.7, 50, 1, 0.9, 1.0, 0.0, 12345)
+
+    def sampler(i):
+        def f():
+            check(L.nnq_linear_sample(copies[i].handle, vp(x), k, None, 0, vp(logits[i]), None, 0, ctypes.byref(cfg),
+                                      ctypes.c_void_p(idx.data_ptr() + 4 * i), cur_stream()))
+        return f
+
+    sec_s, _ = time_graph([sampler(i) for i in range(len(copies))], steps, warmup)
     algo = len(wb) + k * 4 + n * 4 + 4
-    return dict(sec=sec, steps=nsteps, gbs=algo / sec / 1e9, algo_bytes=algo, copies=len(copies))
+    return dict(sec=sec, steps=nsteps, gbs=algo / sec / 1e9, algo_bytes=algo, copies=len(copies), sec_sample=sec_s)
 
 
 def bench_gemm(m, n, k, steps, warmup, min_bytes=256 << 20):
@@ -330,7 +342,8 @@ def main():
         g = bench_lm_head(max(40, args.steps // 40), 10)
         configs["q6_k_lm_head_151936x4096_argmax"] = {"us": round(g["sec"] * 1e6, 3), "GBps": round(g["gbs"], 1),
                                                       "frac_hbm": round(g["gbs"] / HBM_PEAK_GBS, 4),
-                                                      "tokens_per_s": round(1.0 / g["sec"], 1)}
+                                                      "tokens_per_s": round(1.0 / g["sec"], 1),
+                                                      "with_sampling_us": round(g["sec_sample"] * 1e6, 3)}
         for (m, n, k) in [(512, 12288, 4096), (512, 4096, 12288)]:
             log(f"bench: Q4_K prefill GEMM M={m} N={n} K={k} (bf16 in/out)")
             g = bench_gemm(m, n, k, max(50, args.steps // 20), 10)

@@ -149,6 +149,39 @@ int nnq_argmax_f32(const float *logits, int64_t n, uint32_t *idx, int32_t *statu
 int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const float *bias, int64_t bias_len,
                       float *logits, uint32_t *idx, int32_t *status_dev, void *stream);
 
+/* ---- token sampling ------------------------------------------------------------- */
+
+/* SamplingConfig (crates/nn-gptoss/src/sampling.rs:27-49) with the seed of sample_token.
+ * The Option fields become flags: top_k < 0 is None, use_top_p = 0 is None. */
+typedef struct nnq_sampling {
+    float temperature;        /* > 0 and finite */
+    int32_t top_k;            /* < 0: None (keep all finite logits); 0: no candidate (argmax fallback) */
+    int32_t use_top_p;        /* 0: top_p is None */
+    float top_p;
+    float repetition_penalty; /* 1.0: none */
+    float frequency_penalty;  /* 0.0: none */
+    uint64_t seed;            /* selector = (seed % 10000) / 10000 */
+} nnq_sampling;
+
+/* token (device u32) = sample_token(logits[n], cfg, past_tokens, seed) on the device:
+ * repetition and frequency penalties per occurrence of past_tokens (device u32[n_past],
+ * may be NULL when n_past = 0; indices >= n are ignored), temperature, top-k, top-p,
+ * softmax and the seed's selector walk; with no candidate left, the last maximal index
+ * of the original logits (argmax_slice).  logits is left unchanged.  Equal logits at the
+ * k-th place keep the lower index (the reference's unstable sort leaves that open).
+ * NNQ_ERR_INVALID_ARGUMENT for n = 0 or a temperature that is not positive and finite
+ * (sample_token panics there); NNQ_ERR_UNSUPPORTED when ceil(n / 2048) * min(k, 2048)
+ * exceeds 16384 (k = min(top_k, n), n with top_k None).
+ * Replaces sample_token (crates/nn-gptoss/src/sampling.rs:136-185). */
+int nnq_sample_token(const float *logits, int64_t n, const uint32_t *past_tokens, int64_t n_past,
+                     const nnq_sampling *cfg, uint32_t *token, void *stream);
+
+/* LM head + sampling: logits[n] = x[k] @ W^T (+ bias), then nnq_sample_token on them,
+ * with no host round trip.  Replaces lm_head Linear + sample_token (decode step). */
+int nnq_linear_sample(const nnq_weight *w, const float *x, int64_t k, const float *bias, int64_t bias_len,
+                      float *logits, const uint32_t *past_tokens, int64_t n_past, const nnq_sampling *cfg,
+                      uint32_t *token, void *stream);
+
 /* ---- Qwen3 SwiGLU MLP ----------------------------------------------------------- */
 
 /* Upload one layer's MLP: gate_proj and up_proj W[inter, hidden] (block bytes of one

@@ -8,6 +8,6 @@ operator surface in Python.
 from .quantized import (  # noqa: F401
     BiasMismatch, DataLengthMismatch, InvalidShape, Layout, NonFiniteData, NotQuantized, QuantizedMatmulError,
     QuantizedMLP, QuantizedMoE, QuantizedWeight, QuantType, RankMismatch, ShapeMismatch, TensorError, Unsupported, WeightRank,
-    WrongQuantType, argmax, device_count, init, linear_argmax, quantize_mxfp4, quantize_q4_k, quantize_q6_k,
+    WrongQuantType, argmax, device_count, init, linear_argmax, linear_sample, sample_token, quantize_mxfp4, quantize_q4_k, quantize_q6_k,
     quantize_q8_0, quantized_linear, quantized_matmul_q4_k, quantized_matmul_q6_k, quantized_matmul_q8_0,
     synth_normal)

@@ -18,6 +18,13 @@ c_float = ctypes.c_float
 c_u64 = ctypes.c_uint64
 c_double = ctypes.c_double
 
+
+class Sampling(ctypes.Structure):
+    """nnq_sampling (include/nnq.h)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("use_top_p", ctypes.c_int32),
+                ("top_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float),
+                ("frequency_penalty", ctypes.c_float), ("seed", ctypes.c_uint64)]
+
 # name -> (restype, argtypes); every symbol declared in include/nnq.h
 SIGNATURES = {
     "nnq_device_count": (c_int, [ctypes.POINTER(c_int)]),
@@ -47,6 +54,9 @@ SIGNATURES = {
                                ctypes.POINTER(c_void_p)]),
     "nnq_mlp_destroy": (c_int, [c_void_p]),
     "nnq_mlp_forward": (c_int, [c_void_p, c_void_p, c_int, c_i64, c_i64, c_void_p, c_int, c_void_p, c_void_p]),
+    "nnq_sample_token": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),
+    "nnq_linear_sample": (c_int, [c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_void_p,
+                                  c_void_p, c_void_p]),
     "nnq_quantize_q4_k": (c_int, [c_void_p, c_sz, c_void_p]),
     "nnq_quantize_mxfp4": (c_int, [c_void_p, c_sz, c_void_p, c_void_p]),
     "nnq_quantize_q8_0": (c_int, [c_void_p, c_sz, c_void_p]),

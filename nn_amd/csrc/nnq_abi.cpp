@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -705,6 +706,54 @@ int nnq_moe_block_forward(const nnq_moe *m, const nnq_router *r, const void *x, 
                    topk_idx, topk_w, status_dev, reinterpret_cast<uint8_t *>(s.p) + lg_bytes, stream);
     if (e) return hip_fail((hipError_t)e, "moe launch");
     return NNQ_OK;
+}
+
+// ---- token sampling ------------------------------------------------------------------
+
+static int run_sample(const float *logits, int64_t n, const uint32_t *past, int64_t n_past, const nnq_sampling *cfg,
+                      uint32_t *token, void *stream) {
+    const int64_t k = cfg->top_k < 0 ? n : std::min<int64_t>(cfg->top_k, n);
+    if (!sample_supported(n, k))
+        return fail(NNQ_ERR_UNSUPPORTED, "top_k %lld over %lld logits exceeds the device top-k capacity",
+                    (long long)k, (long long)n);
+    Scratch s;
+    HIP_TRY(s.alloc(sample_scratch_bytes(n, k), (hipStream_t)stream), "scratch alloc");
+    // sample_token's conditions for applying the penalties (sampling.rs:155-162)
+    const int rep_on = std::fabs(cfg->repetition_penalty - 1.0f) > 1.1920929e-7f;
+    const int freq_on = std::fabs(cfg->frequency_penalty) > 1.1920929e-7f;
+    int e = launch_sample(logits, n, past, n_past, cfg->temperature, k, cfg->use_top_p != 0, cfg->top_p,
+                          cfg->repetition_penalty, rep_on, cfg->frequency_penalty, freq_on, cfg->seed, token, s.p,
+                          stream);
+    if (e) return hip_fail((hipError_t)e, "sample launch");
+    return NNQ_OK;
+}
+
+static int check_sampling(const nnq_sampling *cfg, const uint32_t *past, int64_t n_past, const uint32_t *token) {
+    if (!cfg || !token) return fail(NNQ_ERR_INVALID_ARGUMENT, "sampling config or token is null");
+    if (!(cfg->temperature > 0.0f) || !std::isfinite(cfg->temperature))
+        return fail(NNQ_ERR_INVALID_ARGUMENT, "temperature must be positive and finite");
+    if (n_past < 0 || (n_past > 0 && !past)) return fail(NNQ_ERR_INVALID_ARGUMENT, "past tokens");
+    return NNQ_OK;
+}
+
+int nnq_sample_token(const float *logits, int64_t n, const uint32_t *past_tokens, int64_t n_past,
+                     const nnq_sampling *cfg, uint32_t *token, void *stream) {
+    if (!logits || n <= 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits must be non-empty");
+    int rc = check_sampling(cfg, past_tokens, n_past, token);
+    if (rc) return rc;
+    return run_sample(logits, n, past_tokens, n_past, cfg, token, stream);
+}
+
+int nnq_linear_sample(const nnq_weight *w, const float *x, int64_t k, const float *bias, int64_t bias_len,
+                      float *logits, const uint32_t *past_tokens, int64_t n_past, const nnq_sampling *cfg,
+                      uint32_t *token, void *stream) {
+    int rc = check_linear(w, x, NNQ_F32, 1, k, bias, bias_len, logits, NNQ_F32);
+    if (rc) return rc;
+    rc = check_sampling(cfg, past_tokens, n_past, token);
+    if (rc) return rc;
+    rc = dispatch_linear(w, x, NNQ_F32, 1, bias, logits, NNQ_F32, stream);
+    if (rc) return rc;
+    return run_sample(logits, w->L.n, past_tokens, n_past, cfg, token, stream);
 }
 
 }  // extern "C"

@@ -87,6 +87,14 @@ int launch_argmax_final(const unsigned long long *partial, int64_t count, uint32
 int launch_swiglu(const float *gu, int64_t m, int64_t inter, float *h, int32_t *status, void *stream);
 int launch_nonfinite_check(const void *y, int y_bf16, int64_t count, int32_t *status, void *stream);
 
+// Token sampling over device logits[n] (k = min(top_k, n), 0: none): scratch bytes, whether
+// the shape fits the two-pass top-k (ceil(n / 2048) * min(k, 2048) <= 16384), and the launch
+size_t sample_scratch_bytes(int64_t n, int64_t k);
+bool sample_supported(int64_t n, int64_t k);
+int launch_sample(const float *logits, int64_t n, const uint32_t *past, int64_t n_past, float temperature, int64_t k,
+                  int use_top_p, float top_p, float rep, int rep_on, float freq, int freq_on, uint64_t seed,
+                  uint32_t *token, void *scratch, void *stream);
+
 // GEMM (prefill) for Q4_K: x bf16/f32 [m, k] -> y [m, n].  `scratch` holds the
 // staged activation and split-K partials (gemm_scratch_bytes(args) bytes, 256-byte
 // aligned; every field but scratch set).

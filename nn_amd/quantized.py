@@ -329,6 +329,64 @@ def linear_argmax(x: torch.Tensor, weight: QuantizedWeight, bias: Optional[torch
 
 
 # ---------------------------------------------------------------------------------
+# token sampling (crates/nn-gptoss/src/sampling.rs)
+# ---------------------------------------------------------------------------------
+
+
+def _sampling(temperature, top_k, top_p, repetition_penalty, frequency_penalty, seed):
+    return _lib.Sampling(float(temperature), -1 if top_k is None else int(top_k), 0 if top_p is None else 1,
+                         0.0 if top_p is None else float(top_p), float(repetition_penalty), float(frequency_penalty),
+                         int(seed) & 0xFFFFFFFFFFFFFFFF)
+
+
+def _past(past_tokens, device):
+    if past_tokens is None or len(past_tokens) == 0:
+        return None, 0
+    if isinstance(past_tokens, torch.Tensor):
+        p = past_tokens.to(device=device, dtype=torch.int32).contiguous()
+    else:
+        p = torch.tensor(np.asarray(past_tokens, np.int64).astype(np.uint32).view(np.int32), device=device)
+    return p, p.numel()
+
+
+def sample_token(logits: torch.Tensor, temperature: float = 0.7, top_k: Optional[int] = 50,
+                 top_p: Optional[float] = 0.9, repetition_penalty: float = 1.0, frequency_penalty: float = 0.0,
+                 past_tokens=None, seed: int = 0) -> torch.Tensor:
+    """sample_token (sampling.rs:136-185) over a 1-D device f32 logits tensor; returns the
+    token as a device int64 scalar tensor (no host synchronisation)."""
+    v = logits.reshape(-1).float().contiguous()
+    if v.numel() == 0:
+        raise InvalidShape("logits must be non-empty")
+    past, n_past = _past(past_tokens, v.device)
+    tok = torch.empty(1, dtype=torch.int32, device=v.device)
+    cfg = _sampling(temperature, top_k, top_p, repetition_penalty, frequency_penalty, seed)
+    _check(_lib.load().nnq_sample_token(_ptr(v), v.numel(), _ptr(past), n_past, ctypes.byref(cfg), _ptr(tok),
+                                        _stream(v)))
+    return tok.view(torch.int32)[0].to(torch.int64)
+
+
+def linear_sample(x: torch.Tensor, weight: QuantizedWeight, bias: Optional[torch.Tensor] = None,
+                  temperature: float = 0.7, top_k: Optional[int] = 50, top_p: Optional[float] = 0.9,
+                  repetition_penalty: float = 1.0, frequency_penalty: float = 0.0, past_tokens=None, seed: int = 0):
+    """LM head + sampling: logits = x @ W^T (+bias), then sample_token on the device."""
+    n, k = weight.shape
+    xv = x.reshape(-1).float().contiguous()
+    if xv.numel() != k:
+        raise ShapeMismatch(f"input has {xv.numel()} elements, weight in_features {k}")
+    if bias is not None:
+        if bias.dim() != 1 or bias.shape[0] != n:
+            raise BiasMismatch(f"bias shape mismatch: expected [{n}], got {list(bias.shape)}")
+        bias = bias.float().contiguous()
+    logits = torch.empty(n, dtype=torch.float32, device=xv.device)
+    past, n_past = _past(past_tokens, xv.device)
+    tok = torch.empty(1, dtype=torch.int32, device=xv.device)
+    cfg = _sampling(temperature, top_k, top_p, repetition_penalty, frequency_penalty, seed)
+    _check(_lib.load().nnq_linear_sample(weight.handle, _ptr(xv), k, _ptr(bias), n if bias is not None else 0,
+                                         _ptr(logits), _ptr(past), n_past, ctypes.byref(cfg), _ptr(tok), _stream(xv)))
+    return logits, tok.view(torch.int32)[0].to(torch.int64)
+
+
+# ---------------------------------------------------------------------------------
 # Qwen3 SwiGLU MLP
 # ---------------------------------------------------------------------------------
 

@@ -839,3 +839,135 @@ int orc_any_nonfinite(const float *v, size_t n) {
     return 0;
 }
 
+/* ------------------------------------------------------------------------ */
+/* Token sampling: sample_token (crates/nn-gptoss/src/sampling.rs:136-185)   */
+/* and its steps.  top_k < 0 means None; use_top_p = 0 means None.           */
+/* Top-k ties: the reference sorts with sort_unstable_by, whose order among  */
+/* equal logits is unspecified; here equal values keep the lower index       */
+/* first (parity unpinned for exact ties at the k-th place).  NaN logits are */
+/* ordered below -inf for the selection and never become candidates (the     */
+/* reference keeps only finite candidates; its NaN sort order is unspecified).*/
+/* ------------------------------------------------------------------------ */
+
+typedef struct { uint32_t idx; float v; } orc_cand;
+
+/* descending value, then ascending index; NaN last */
+static int cand_desc(const void *a, const void *b) {
+    const orc_cand *x = (const orc_cand *)a, *y = (const orc_cand *)b;
+    const int xn = x->v != x->v, yn = y->v != y->v;
+    if (xn != yn) return xn - yn;
+    if (!xn && x->v != y->v) return x->v > y->v ? -1 : 1;
+    return x->idx < y->idx ? -1 : (x->idx > y->idx);
+}
+
+/* softmax_candidates (sampling.rs:371-391): probabilities in candidate order */
+static void softmax_cands(const orc_cand *c, size_t n, float *p) {
+    float mx = -INFINITY;
+    for (size_t i = 0; i < n; i++) mx = fmaxf(mx, c[i].v);
+    if (!isfinite(mx)) {
+        for (size_t i = 0; i < n; i++) p[i] = 1.0f / (float)n;
+        return;
+    }
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        p[i] = expf(c[i].v - mx);
+        sum += p[i];
+    }
+    if (!isfinite(sum) || sum == 0.0f) {
+        for (size_t i = 0; i < n; i++) p[i] = 1.0f / (float)n;
+        return;
+    }
+    for (size_t i = 0; i < n; i++) p[i] = p[i] / sum;
+}
+
+/* argmax_slice (sampling.rs:394-400): Iterator::max_by with partial_cmp, i.e. the
+ * running maximum is replaced unless it compares Greater (ties and NaN move on) */
+size_t orc_argmax_slice(const float *v, size_t n) {
+    size_t best = 0;
+    for (size_t j = 1; j < n; j++)
+        if (!(v[best] > v[j])) best = j;
+    return best;
+}
+
+/* softmax_sample (sampling.rs:340-365) */
+static uint32_t softmax_sample_c(const orc_cand *c, size_t n, uint64_t seed) {
+    if (n == 1) return c[0].idx;
+    float *p = (float *)malloc(n * sizeof(float));
+    softmax_cands(c, n, p);
+    const float selector = (float)(seed % 10000u) / 10000.0f;
+    float cum = 0.0f;
+    uint32_t out = c[n - 1].idx;
+    for (size_t i = 0; i < n; i++) {
+        cum += p[i];
+        if (selector < cum) {
+            out = c[i].idx;
+            break;
+        }
+    }
+    free(p);
+    return out;
+}
+
+int orc_sample_token(const float *logits, size_t n, const uint32_t *past, size_t n_past, float temperature,
+                     int64_t top_k, int use_top_p, float top_p, float rep_penalty, float freq_penalty, uint64_t seed,
+                     uint32_t *token) {
+    if (n == 0 || !(temperature > 0.0f) || !isfinite(temperature)) return -1;
+    float *s = (float *)malloc(n * sizeof(float));
+    memcpy(s, logits, n * sizeof(float));
+    /* apply_repetition_penalty (:277-290), per occurrence */
+    if (fabsf(rep_penalty - 1.0f) > 1.1920929e-7f)
+        for (size_t i = 0; i < n_past; i++)
+            if (past[i] < n) {
+                const float l = s[past[i]];
+                if (l > 0.0f) s[past[i]] = l / rep_penalty;
+                else if (l < 0.0f) s[past[i]] = l * rep_penalty;
+            }
+    /* apply_frequency_penalty (:297-306) */
+    if (fabsf(freq_penalty) > 1.1920929e-7f)
+        for (size_t i = 0; i < n_past; i++)
+            if (past[i] < n) s[past[i]] -= freq_penalty;
+    /* apply_temperature (:193-199) */
+    for (size_t i = 0; i < n; i++)
+        if (isfinite(s[i])) s[i] /= temperature;
+    /* apply_top_k (:245-275): the k largest, then candidates in index order, finite only */
+    orc_cand *c = (orc_cand *)malloc(n * sizeof(orc_cand));
+    size_t nc = 0;
+    if (top_k < 0 || (size_t)top_k >= n) {
+        for (size_t i = 0; i < n; i++)
+            if (isfinite(s[i])) c[nc++] = (orc_cand){(uint32_t)i, s[i]};
+    } else if (top_k > 0) {
+        orc_cand *all = (orc_cand *)malloc(n * sizeof(orc_cand));
+        for (size_t i = 0; i < n; i++) all[i] = (orc_cand){(uint32_t)i, s[i]};
+        qsort(all, n, sizeof(orc_cand), cand_desc);
+        unsigned char *keep = (unsigned char *)calloc(n, 1);
+        for (int64_t i = 0; i < top_k; i++) keep[all[i].idx] = 1;
+        for (size_t i = 0; i < n; i++)
+            if (keep[i] && isfinite(s[i])) c[nc++] = (orc_cand){(uint32_t)i, s[i]};
+        free(keep);
+        free(all);
+    }
+    /* apply_top_p_candidates (:211-238) */
+    if (use_top_p && nc > 0) {
+        qsort(c, nc, sizeof(orc_cand), cand_desc); /* stable order: ties keep index order */
+        float *p = (float *)malloc(nc * sizeof(float));
+        softmax_cands(c, nc, p);
+        float cum = 0.0f;
+        size_t keepn = 0;
+        for (size_t i = 0; i < nc; i++) {
+            cum += p[i];
+            keepn = i + 1;
+            if (cum >= top_p) break;
+        }
+        nc = keepn;
+        free(p);
+    }
+    /* Step 6 (:178-184) */
+    if (nc == 0)
+        *token = (uint32_t)orc_argmax_slice(logits, n);
+    else
+        *token = softmax_sample_c(c, nc, seed);
+    free(c);
+    free(s);
+    return 0;
+}
+

@@ -91,6 +91,12 @@ uint64_t orc_splitmix64(uint64_t z);
 void orc_silu_mul(const float *g, const float *u, size_t n, float *h);
 int orc_any_nonfinite(const float *v, size_t n);
 
+/* Token sampling: sample_token (crates/nn-gptoss/src/sampling.rs:136-185); top_k < 0 = None */
+size_t orc_argmax_slice(const float *v, size_t n);
+int orc_sample_token(const float *logits, size_t n, const uint32_t *past, size_t n_past, float temperature,
+                     int64_t top_k, int use_top_p, float top_p, float rep_penalty, float freq_penalty, uint64_t seed,
+                     uint32_t *token);
+
 #ifdef __cplusplus
 }
 #endif

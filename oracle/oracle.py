@@ -82,6 +82,10 @@ def lib():
             ),
             "orc_splitmix64": (ctypes.c_uint64, [ctypes.c_uint64]),
             "orc_silu_mul": (None, [_f32p, _f32p, _sz, _f32p]),
+            "orc_argmax_slice": (_sz, [_f32p, _sz]),
+            "orc_sample_token": (ctypes.c_int, [_f32p, _sz, _u32p, _sz, ctypes.c_float, ctypes.c_int64, ctypes.c_int,
+                                                ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_uint64,
+                                                _u32p]),
             "orc_any_nonfinite": (ctypes.c_int, [_f32p, _sz]),
         }
         for name, (res, args) in sig.items():
@@ -341,6 +345,28 @@ def mlp_forward(x, gate, up, down, hidden, inter):
     h = silu_mul(g, u)
     y = _LINEAR[down[0]](h, down[1], hidden)
     return y, bool(lib().orc_any_nonfinite(_p(y, _f32p), y.size))
+
+
+def argmax_slice(v):
+    v = _f32(v).ravel()
+    return int(lib().orc_argmax_slice(_p(v, _f32p), v.size))
+
+
+def sample_token(logits, temperature=0.7, top_k=50, top_p=0.9, repetition_penalty=1.0, frequency_penalty=0.0,
+                 past_tokens=(), seed=0):
+    """sample_token (crates/nn-gptoss/src/sampling.rs:136-185); top_k / top_p None disable
+    the step, as the reference's Option fields do."""
+    lg = _f32(logits).ravel()
+    past = np.ascontiguousarray(np.asarray(past_tokens, np.uint32).ravel())
+    out = ctypes.c_uint32()
+    rc = lib().orc_sample_token(_p(lg, _f32p), lg.size, _p(past, _u32p) if past.size else None, past.size,
+                                ctypes.c_float(temperature), -1 if top_k is None else int(top_k),
+                                0 if top_p is None else 1, ctypes.c_float(0.0 if top_p is None else top_p),
+                                ctypes.c_float(repetition_penalty), ctypes.c_float(frequency_penalty),
+                                ctypes.c_uint64(seed), ctypes.byref(out))
+    if rc:
+        raise OracleError("sample_token: empty logits or temperature not positive and finite")
+    return out.value
 
 
 def splitmix64(z: int) -> int:

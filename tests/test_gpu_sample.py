@@ -1,0 +1,111 @@
+"""GPU parity for token sampling (sample_token, crates/nn-gptoss/src/sampling.rs:136-185).
+
+nnq_sample_token runs penalties, temperature, a two-pass top-k over the whole vocabulary,
+top-p, softmax and the selector walk on the device.  The picked token must equal the
+oracle's restatement of sample_token on the same logits, for every configuration and
+seed tried (the only freedom the reference leaves, the order of exactly equal logits at
+the k-th place, does not arise with these inputs).  nnq_linear_sample (Q6_K LM head +
+sampling) is checked the same way on the logits it produced, and those logits against
+the oracle's GEMV with the linear bars.
+"""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_linear import check_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def dev():
+    import nn_amd
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    nn_amd.init(0)
+    return torch.device("cuda:0")
+
+
+def pick(logits_np, dev, **cfg):
+    import nn_amd
+    t = torch.from_numpy(np.asarray(logits_np, np.float32)).to(dev)
+    return int(nn_amd.sample_token(t, **cfg).item())
+
+
+def test_sample_reference_cases(O, dev):
+    greedy = dict(temperature=1e-7, top_k=1, top_p=None)
+    assert pick([1.0, 5.0, 3.0, 0.5], dev, **greedy) == 1
+    assert pick([3.9, 4.0, 3.8], dev, repetition_penalty=10.0, past_tokens=[1], **greedy) == 0
+    assert pick([1.01, 1.0, 1.0, 1.0, 1.0], dev, temperature=1e-7, top_k=1, top_p=0.9) == 0
+    assert pick([3.0, 1.0], dev, repetition_penalty=2.0, past_tokens=[0, 0], **greedy) == 1
+    assert pick([5.0, 4.2], dev, frequency_penalty=0.5, past_tokens=[0, 0], **greedy) == 1
+    assert pick([1.0, 2.0], dev, repetition_penalty=9.0, past_tokens=[5], **greedy) == 1
+    assert pick([1.0, 3.0, 3.0, 2.0], dev, temperature=1.0, top_k=0, top_p=None) == 2  # argmax_slice: last max
+    assert pick([0.0, 10.0, 0.0], dev, temperature=1.0, top_k=None, top_p=0.01, seed=7777) == 1
+
+
+CONFIGS = [
+    dict(temperature=0.7, top_k=50, top_p=0.9),
+    dict(temperature=1.0, top_k=5, top_p=None),
+    dict(temperature=1.3, top_k=200, top_p=0.5),
+    dict(temperature=0.9, top_k=1, top_p=None),
+    dict(temperature=1.0, top_k=40, top_p=0.95, repetition_penalty=1.3, frequency_penalty=0.4),
+]
+
+
+@pytest.mark.parametrize("n", [151936, 5000, 37])
+@pytest.mark.parametrize("ci", range(len(CONFIGS)))
+def test_sample_vs_oracle(O, dev, n, ci):
+    import nn_amd
+    cfg = dict(CONFIGS[ci])
+    lg = nn_amd.synth_normal(n + ci, 1, (n,), 2.0)
+    lg[n // 3] = -np.inf
+    if n > 100:
+        lg[n // 2] = np.nan
+    rng = np.random.default_rng(n + ci)
+    past = rng.integers(0, n + 10, 40).tolist() + [int(np.argmax(lg))] * 3
+    if "repetition_penalty" in cfg:
+        cfg["past_tokens"] = past
+    t = torch.from_numpy(lg).to(dev)
+    for seed in (0, 1, 4999, 9999, 123456789, 31337):
+        got = int(nn_amd.sample_token(t, seed=seed, **cfg).item())
+        want = O.sample_token(lg, seed=seed, **cfg)
+        assert got == want, (n, cfg, seed)
+
+
+def test_sample_top_k_none_small_vocab(O, dev):
+    import nn_amd
+    n = 3000
+    lg = nn_amd.synth_normal(3, 1, (n,), 1.5)
+    t = torch.from_numpy(lg).to(dev)
+    for seed in (3, 5000, 9998):
+        assert int(nn_amd.sample_token(t, temperature=1.0, top_k=None, top_p=None, seed=seed).item()) == \
+            O.sample_token(lg, temperature=1.0, top_k=None, top_p=None, seed=seed)
+        assert int(nn_amd.sample_token(t, temperature=0.8, top_k=None, top_p=0.7, seed=seed).item()) == \
+            O.sample_token(lg, temperature=0.8, top_k=None, top_p=0.7, seed=seed)
+
+
+def test_sample_errors(O, dev):
+    import nn_amd
+    t = torch.zeros(151936, device=dev)
+    with pytest.raises(nn_amd.Unsupported):
+        nn_amd.sample_token(t, top_k=None)
+    with pytest.raises(nn_amd.TensorError):
+        nn_amd.sample_token(t, temperature=0.0)
+    with pytest.raises(nn_amd.TensorError):
+        nn_amd.sample_token(t, temperature=float("inf"))
+
+
+def test_lm_head_sample_q6k(O, dev):
+    """Config 3's LM head (Q6_K 151936 x 4096, nn-gguf layout) fused with sampling."""
+    import nn_amd
+    n, k = 151936, 4096
+    wb = nn_amd.quantize_q6_k(nn_amd.synth_normal(3, 1, (n, k), 0.02))
+    w = nn_amd.QuantizedWeight.from_quantized(wb, nn_amd.QuantType.Q6_K, (n, k), layout=nn_amd.Layout.NN_GGUF)
+    x = torch.from_numpy(nn_amd.synth_normal(3, 2, (k,), 1.0)).to(dev)
+    for seed, cfg in [(17, dict(temperature=0.7, top_k=50, top_p=0.9)), (4242, dict(temperature=1.0, top_k=1,
+                                                                                   top_p=None))]:
+        logits, tok = nn_amd.linear_sample(x, w, seed=seed, **cfg)
+        lg = logits.cpu().numpy()
+        assert int(tok.item()) == O.sample_token(lg, seed=seed, **cfg)
+    ref = O.q6k_linear(x.cpu().numpy()[None, :], wb, n)
+    check_close(ref, lg[None, :], "lm head logits")

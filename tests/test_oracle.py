@@ -565,3 +565,62 @@ def test_router_logits_matches_f64(O):
     got = O.router_logits(x, w, b)
     assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
     assert np.abs(O.router_logits(x, w) + b - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+# ---- token sampling (crates/nn-gptoss/src/sampling.rs) ---------------------------------
+
+
+def test_sample_token_reference_cases(O):
+    """The reference's own sample_token tests (sampling.rs:566-606) and its step tests
+    restated through the whole pipeline."""
+    greedy = dict(temperature=1e-7, top_k=1, top_p=None)
+    assert O.sample_token([1.0, 5.0, 3.0, 0.5], **greedy) == 1
+    assert O.sample_token([3.9, 4.0, 3.8], repetition_penalty=10.0, past_tokens=[1], **greedy) == 0
+    assert O.sample_token([1.01, 1.0, 1.0, 1.0, 1.0], temperature=1e-7, top_k=1, top_p=0.9) == 0
+    # top_k larger than the vocabulary keeps every finite logit; top_p = 1 keeps all
+    picks = {O.sample_token([1.0, 2.0, 3.0], temperature=1.0, top_k=10, top_p=1.0, seed=s) for s in range(0, 10000, 37)}
+    assert picks == {0, 1, 2}
+    # a very small top_p keeps only the peak (sampling.rs:494-500)
+    assert {O.sample_token([0.0, 10.0, 0.0], temperature=1.0, top_k=None, top_p=0.01, seed=s)
+            for s in range(0, 10000, 101)} == {1}
+    # top_k = 0: no candidates, argmax of the original logits; max_by keeps the LAST maximum
+    assert O.sample_token([1.0, 3.0, 3.0, 2.0], temperature=1.0, top_k=0, top_p=None) == 2
+    assert O.argmax_slice([1.0, 3.0, 3.0, 2.0]) == 2
+
+
+def test_sample_token_penalties_per_occurrence(O):
+    """Repetition penalty divides positive / multiplies negative logits once per
+    occurrence (:277-290); frequency penalty subtracts once per occurrence (:297-306)."""
+    greedy = dict(temperature=1e-7, top_k=1, top_p=None)
+    assert O.sample_token([3.0, 1.0], repetition_penalty=2.0, past_tokens=[0], **greedy) == 0    # 1.5 > 1
+    assert O.sample_token([3.0, 1.0], repetition_penalty=2.0, past_tokens=[0, 0], **greedy) == 1  # 0.75 < 1
+    assert O.sample_token([-1.0, -1.5], repetition_penalty=2.0, past_tokens=[0], **greedy) == 1   # -2 < -1.5
+    assert O.sample_token([0.0, -0.5], repetition_penalty=9.0, past_tokens=[0], **greedy) == 0    # zero unchanged
+    assert O.sample_token([1.0, 2.0], repetition_penalty=9.0, past_tokens=[5], **greedy) == 1     # out of range
+    assert O.sample_token([5.0, 4.2], frequency_penalty=0.5, past_tokens=[0], **greedy) == 0     # 4.5
+    assert O.sample_token([5.0, 4.2], frequency_penalty=0.5, past_tokens=[0, 0], **greedy) == 1  # 4.0
+
+
+def test_sample_token_selection_matches_softmax(O):
+    """Over all 10000 selector values (seed % 10000) the picks follow the softmax of
+    logit / temperature in candidate (index) order: the count of each token equals the
+    number of selectors in its cumulative interval, against an f64 closed form."""
+    logits = np.array([0.3, -1.2, 2.0, 0.9, 1.4, -0.2], np.float32)
+    T = 0.8
+    counts = np.zeros(6, int)
+    for s in range(10000):
+        counts[O.sample_token(logits, temperature=T, top_k=4, top_p=None, seed=s)] += 1
+    keep = np.argsort(-logits)[:4]
+    z = logits[np.sort(keep)].astype(np.float64) / T
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    assert set(np.nonzero(counts)[0]) == set(keep.tolist())
+    assert np.abs(counts[np.sort(keep)] / 10000.0 - p).max() <= 2e-4
+    # with top_p the candidates are walked in descending order and cut at cumulative >= p
+    z6 = logits.astype(np.float64) / T
+    q = np.exp(z6 - z6.max())
+    q /= q.sum()
+    order = np.argsort(-logits)
+    cut = int(np.searchsorted(np.cumsum(q[order]), 0.8) + 1)
+    picks = {O.sample_token(logits, temperature=T, top_k=None, top_p=0.8, seed=s) for s in range(0, 10000, 7)}
+    assert picks == set(order[:cut].tolist())
