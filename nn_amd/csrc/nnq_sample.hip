@@ -1,19 +1,23 @@
 // Token sampling on gfx950: sample_token (crates/nn-gptoss/src/sampling.rs:136-185) over a
 // logits vector that stays on the device, e.g. straight out of the LM-head GEMV.
 //
+// Every logit becomes a 64-bit key: its orderable value (after the penalties and the
+// temperature) above its inverted index, so keys are unique, larger keys are larger
+// values, and equal values order the lower index first.  NaN keys sit below every
+// value and never become candidates.
+//
 //   sample_local_kernel  one workgroup per 2048 logits: repetition / frequency penalties
-//                        (per occurrence in past_tokens, :277-306), temperature (:193-199),
-//                        then the block's logits as 64-bit keys (orderable value, inverted
-//                        index) sorted descending in LDS (bitonic); the block's best
-//                        min(k, 2048) keys go to the candidate buffer
-//   sample_final_kernel  one workgroup: the candidates sorted the same way give the top k
-//                        (apply_top_k, :245-275; equal values keep the lower index first),
-//                        then one thread runs the short sequential tail exactly as the
-//                        reference does: finite candidates in index order, top-p over the
-//                        descending order (:211-238), softmax and the seed's selector walk
-//                        (:340-391), and the argmax_slice fallback (:394-400) when no
-//                        candidate is left.
-// NaN logits sort below -inf and never become candidates.
+//                        (per occurrence of past_tokens, :277-306), temperature
+//                        (:193-199), keys; an exact radix select (8 passes of 8 bits)
+//                        finds the block's kk-th largest key, and the kk keys at or
+//                        above it go to the candidate buffer (unordered)
+//   sample_final_kernel  one workgroup: the same radix select over the candidates gives
+//                        exactly the top k (apply_top_k, :245-275), sorted by a small
+//                        bitonic network; wave 0 then runs the reference's tail with
+//                        the exponentials in parallel and every sum in candidate order:
+//                        finite candidates in index order, or top-p over the descending
+//                        order (:211-238), softmax and the seed's selector walk
+//                        (:340-391), and argmax_slice (:394-400) when no candidate is left.
 #include <algorithm>
 #include <type_traits>
 
@@ -35,81 +39,92 @@ __device__ __forceinline__ uint32_t ord_f32(float v) {
 __device__ __forceinline__ float unord_f32(uint32_t o) {
     return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
-// descending key order = descending value, then ascending index; NaN and padding at the end
 __device__ __forceinline__ uint64_t cand_key(float v, uint32_t idx) {
-    if (v != v) return 0xFFFFFFFFull - idx;  // below every real value (ord(-inf) > 0)
+    if (v != v) return 0xFFFFFFFFull - idx;  // below every value (ord(-inf) > 0), above padding 0
     return ((uint64_t)ord_f32(v) << 32) | (0xFFFFFFFFull - idx);
 }
 __device__ __forceinline__ uint32_t key_idx(uint64_t k) { return 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull); }
 __device__ __forceinline__ float key_val(uint64_t k) { return unord_f32((uint32_t)(k >> 32)); }
+__device__ __forceinline__ bool key_finite(uint64_t k) { return (k >> 32) != 0 && fabsf(key_val(k)) <= 3.402823466e38f; }
 
-// Bitonic sort, descending, of E * nact 64-bit keys (a power of two) held E per thread in
-// registers: thread t < nact owns elements E t .. E t + E - 1 in e[].  Stages whose partner
-// is in the same thread (stride < E) run in registers; the others publish the thread's
-// keys to `buf` (E * nact entries, element r of thread t at r * nact + t, so that a wave's
-// accesses fall in distinct banks), read the partner thread's, and keep the larger or
-// smaller of each pair.  Every thread of the workgroup calls it (barriers).
-template <int E>
-__device__ void bitonic_reg(uint64_t (&e)[E], uint64_t *buf, int nact) {
-    const int t = threadIdx.x;
-    const bool act = t < nact;
-    const int n = E * nact;
-    for (int size = 2; size <= n; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            if (stride >= E) {
-                if (act)
-#pragma unroll
-                    for (int r = 0; r < E; r++) buf[r * nact + t] = e[r];
-                __syncthreads();
-                if (act) {
-                    const int pt = t ^ (stride / E);
-#pragma unroll
-                    for (int r = 0; r < E; r++) {
-                        const int j = E * t + r, p = E * pt + r;
-                        const uint64_t ep = buf[r * nact + pt];
-                        const bool desc = ((j < p ? j : p) & size) == 0, lo = j < p;
-                        const uint64_t mx = e[r] > ep ? e[r] : ep, mn = e[r] > ep ? ep : e[r];
-                        e[r] = (lo == desc) ? mx : mn;
-                    }
-                }
-                __syncthreads();
-            } else if (act) {
-#pragma unroll
-                for (int r = 0; r < E; r++)
-                    if ((r & stride) == 0) {
-                        const int p = r | stride;
-                        const bool desc = ((E * t + r) & size) == 0;
-                        const uint64_t x = e[r], y = e[p];
-                        if ((x < y) == desc) {
-                            e[r] = y;
-                            e[p] = x;
-                        }
-                    }
-            }
-        }
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// keys[0..n) (n a power of two, at most 1024 * 16) sorted descending in place, 1024 threads
-__device__ void sort_desc_lds(uint64_t *keys, int n) {
-    auto run = [&](auto ec) {
-        constexpr int E = decltype(ec)::value;
-        const int nact = n / E;
-        uint64_t e[E];
-        if ((int)threadIdx.x < nact)
-#pragma unroll
-            for (int r = 0; r < E; r++) e[r] = keys[E * threadIdx.x + r];
+// A threshold t with exactly k of the nonzero keys held E per thread at or above it (k <=
+// their number, all distinct; zero keys are padding and take no part): passes over 8-bit
+// digits, most significant first, until the digit bin that holds the kth largest is
+// needed whole (then t is the prefix so far with zeros below) or all 64 bits are fixed
+// (then t is the kth largest key).  Each wave counts into its own histogram (hist holds
+// blockDim / 64 of them), so equal digits only contend within a wave.  Every thread of
+// the workgroup calls it.
+template <int E>
+__device__ uint64_t radix_kth(const uint64_t (&e)[E], int k, int *hist, uint64_t *bcast) {
+    uint64_t prefix = 0, mask = 0;
+    int rem = k;
+    const int lane = threadIdx.x & 63, nw = blockDim.x / 64;
+    int *my = hist + (threadIdx.x / 64) * 256;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        for (int i = threadIdx.x; i < 256 * nw; i += blockDim.x) hist[i] = 0;
         __syncthreads();
-        bitonic_reg<E>(e, keys, nact);
-        if ((int)threadIdx.x < nact)
 #pragma unroll
-            for (int r = 0; r < E; r++) keys[E * threadIdx.x + r] = e[r];
+        for (int r = 0; r < E; r++)
+            if (e[r] != 0 && (e[r] & mask) == prefix) atomicAdd(&my[(e[r] >> shift) & 255], 1);
         __syncthreads();
-    };
-    if (n <= 1024) run(std::integral_constant<int, 1>{});
-    else if (n <= 2048) run(std::integral_constant<int, 2>{});
-    else if (n <= 4096) run(std::integral_constant<int, 4>{});
-    else if (n <= 8192) run(std::integral_constant<int, 8>{});
-    else run(std::integral_constant<int, 16>{});
+        if (threadIdx.x < 64) {
+            // lane l holds digits 255 - 4l .. 252 - 4l (descending order)
+            int c[4], sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = 255 - (4 * lane + j);
+                int cd = 0;
+                for (int w = 0; w < nw; w++) cd += hist[w * 256 + d];
+                c[j] = cd;
+                sum += cd;
+            }
+            int before = sum;  // inclusive scan over lanes, then exclusive
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int v = __shfl_up(before, o, 64);
+                if (lane >= o) before += v;
+            }
+            before -= sum;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (before < rem && before + c[j] >= rem)
+                    bcast[0] = ((uint64_t)(255 - (4 * lane + j)) << 48) | ((uint64_t)c[j] << 24) | (uint64_t)before;
+                before += c[j];
+            }
+        }
+        __syncthreads();
+        const uint64_t b = bcast[0];
+        const int above = (int)(b & 0xFFFFFF), inbin = (int)((b >> 24) & 0xFFFFFF);
+        rem -= above;
+        prefix |= (b >> 48) << shift;
+        mask |= 0xFFull << shift;
+        __syncthreads();  // bcast and hist are rewritten by the next pass
+        if (inbin == rem) break;  // the whole bin is taken (uniform)
+    }
+    return prefix;
+}
+
+// Bitonic sort, descending, of n keys in LDS (n a power of two <= 16384); all threads.
+__device__ void sort_desc_lds(uint64_t *a, int n) {
+    for (int size = 2; size <= n; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
+                const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+                const bool desc = (lo & size) == 0;
+                const uint64_t x = a[lo], y = a[hi];
+                if ((x < y) == desc) {
+                    a[lo] = y;
+                    a[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
 }
 
 struct SampleParams {
@@ -121,8 +136,10 @@ struct SampleParams {
 
 __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, int64_t n, const uint32_t *past,
                                                            int64_t n_past, SampleParams sp, int kk, uint64_t *cand) {
-    __shared__ uint64_t keys[kSampleBlock];
     __shared__ int cnt[kSampleBlock];
+    __shared__ int hist[4 * 256];
+    __shared__ uint64_t bcast[1];
+    __shared__ int nout;
     const int tid = threadIdx.x;
     const int64_t base = (int64_t)blockIdx.x * kSampleBlock;
     const bool pen = (sp.rep_on || sp.freq_on) && n_past > 0;
@@ -133,14 +150,14 @@ __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, 
             const int64_t t = past[i];
             if (t >= base && t < base + kSampleBlock && t < n) atomicAdd(&cnt[t - base], 1);
         }
-        __syncthreads();
     }
-    // thread t: elements 8t .. 8t + 7 of the block (loaded as two coalesced passes)
+    if (tid == 0) nout = 0;
+    __syncthreads();
     constexpr int E = kSampleBlock / 256;
     uint64_t e[E];
 #pragma unroll
     for (int r = 0; r < E; r++) {
-        const int j = E * tid + r;
+        const int j = r * 256 + tid;  // coalesced
         const int64_t i = base + j;
         uint64_t key = 0;  // padding past n: below everything
         if (i < n) {
@@ -157,136 +174,185 @@ __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, 
         }
         e[r] = key;
     }
-    bitonic_reg<E>(e, keys, 256);
+    // the block's real logits may be fewer than kk: keep them all, pad the slots with 0
+    const int real = (int)std::min<int64_t>(kSampleBlock, n - base);
+    const int kb = std::min(kk, real);
+    const uint64_t kth = radix_kth<E>(e, kb, hist, bcast);
+    uint64_t *out = cand + (int64_t)blockIdx.x * kk;
 #pragma unroll
     for (int r = 0; r < E; r++)
-        if (E * tid + r < kk) cand[(int64_t)blockIdx.x * kk + E * tid + r] = e[r];
+        if (e[r] >= kth && e[r] != 0) out[atomicAdd(&nout, 1)] = e[r];
+    for (int j = kb + tid; j < kk; j += 256) out[j] = 0;
 }
 
-// softmax_candidates (sampling.rs:371-391) over c[0..n) into p[0..n), one thread
-__device__ void softmax_seq(const float *v, int n, float *p) {
+__device__ __forceinline__ float lane_f(float v, int i) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+
+// softmax_candidates (sampling.rs:371-391) of val[0..n) into p[0..n), by wave 0:
+// exponentials and quotients in parallel, the maximum (order-free) by reduction, the sum
+// in candidate order, element by element from the lanes.
+__device__ void softmax_wave(const float *val, int n, float *ex, float *p) {
+    const int lane = threadIdx.x;
     float mx = -INFINITY;
-    for (int i = 0; i < n; i++) mx = fmaxf(mx, v[i]);
+    for (int i = lane; i < n; i += 64) mx = fmaxf(mx, val[i]);
+    mx = wave_max(mx);
     if (!(fabsf(mx) <= 3.402823466e38f)) {
-        for (int i = 0; i < n; i++) p[i] = 1.0f / (float)n;
+        for (int i = lane; i < n; i += 64) p[i] = 1.0f / (float)n;
+        wave_sync();
         return;
     }
     float sum = 0.0f;
-    for (int i = 0; i < n; i++) {
-        p[i] = expf(v[i] - mx);
-        sum += p[i];
+    for (int c = 0; c < n; c += 64) {
+        const float e = c + lane < n ? expf(val[c + lane] - mx) : 0.0f;
+        if (c + lane < n) ex[c + lane] = e;
+        const int m = min(64, n - c);
+        for (int i = 0; i < m; i++) sum += lane_f(e, i);
     }
+    wave_sync();
     if (!(fabsf(sum) <= 3.402823466e38f) || sum == 0.0f) {
-        for (int i = 0; i < n; i++) p[i] = 1.0f / (float)n;
-        return;
+        for (int i = lane; i < n; i += 64) p[i] = 1.0f / (float)n;
+    } else {
+        for (int i = lane; i < n; i += 64) p[i] = ex[i] / sum;
     }
-    for (int i = 0; i < n; i++) p[i] = p[i] / sum;
+    wave_sync();
+}
+
+// the first i with (cumulative sum of p[0..i] in order) meeting `stop` (n when none)
+template <class F>
+__device__ int walk_wave(const float *p, int n, F stop) {
+    const int lane = threadIdx.x;
+    float cum = 0.0f;
+    for (int c = 0; c < n; c += 64) {
+        const float v = c + lane < n ? p[c + lane] : 0.0f;
+        const int m = min(64, n - c);
+        for (int i = 0; i < m; i++) {
+            cum += lane_f(v, i);
+            if (stop(cum)) return c + i;
+        }
+    }
+    return n;
 }
 
 __global__ __launch_bounds__(1024) void sample_final_kernel(const float *logits, int64_t n, const uint64_t *cand,
                                                             int ncand, SampleParams sp, float *work,
                                                             uint32_t *token) {
-    __shared__ uint64_t keys[kSampleMaxCand];
-    // the tail's arrays: in the upper half of `keys` (free once the top k, k <= 2048, sit
-    // in keys[0..k)), else in the global scratch
-    const bool in_lds = sp.k <= 2048;
-    float *val = in_lds ? reinterpret_cast<float *>(keys + kSampleMaxCand / 2) : work;
-    float *prob = in_lds ? val + 2048 : work + kSampleMaxCand;
-    uint32_t *idx = in_lds ? reinterpret_cast<uint32_t *>(val + 4096) : reinterpret_cast<uint32_t *>(work + 2 * kSampleMaxCand);
-    int P = 1;
-    while (P < ncand) P <<= 1;
-    for (int j = threadIdx.x; j < P; j += 1024) keys[j] = j < ncand ? cand[j] : 0ull;
-    __syncthreads();
-    sort_desc_lds(keys, P);
-    const int k = (int)sp.k;  // keys[0..k) are the top k (k <= ncand)
-    if (!sp.use_top_p && k > 1) {
-        // Without top-p the reference walks its candidates in index order: re-sort the k
-        // by (finite first, ascending index), carrying each one's position (< 2^14) so
-        // that its value can be found again in `val`.
+    __shared__ uint64_t sel[kSampleMaxCand];
+    __shared__ int hist[16 * 256];
+    __shared__ uint64_t bcast[1];
+    __shared__ int nsel;
+    constexpr int E = kSampleMaxCand / 1024;
+    const int tid = threadIdx.x, k = (int)sp.k;
+    // the tail's arrays: in the upper half of `sel` when k <= 2048, else global scratch
+    const bool in_lds = k <= 2048;
+    const int cap = in_lds ? 2048 : kSampleMaxCand;
+    float *val = in_lds ? reinterpret_cast<float *>(sel + kSampleMaxCand / 2) : work;
+    float *ex = val + cap, *prob = ex + cap;
+    uint32_t *idx = reinterpret_cast<uint32_t *>(prob + cap);
+    int nc = 0;
+    if (k > 0) {
+        uint64_t e[E];
+#pragma unroll
+        for (int r = 0; r < E; r++) {
+            const int j = r * 1024 + tid;
+            e[r] = j < ncand ? cand[j] : 0ull;
+        }
+        if (tid == 0) nsel = 0;
+        const uint64_t kth = radix_kth<E>(e, k, hist, bcast);  // (its barriers order nsel)
         int Q = 1;
         while (Q < k) Q <<= 1;
-        for (int j = threadIdx.x; j < k; j += 1024) val[j] = key_val(keys[j]);
+        for (int j = k + tid; j < Q; j += 1024) sel[j] = 0;
+#pragma unroll
+        for (int r = 0; r < E; r++)
+            if (e[r] >= kth && e[r] != 0) sel[atomicAdd(&nsel, 1)] = e[r];
         __syncthreads();
-        for (int j = threadIdx.x; j < Q; j += 1024) {
-            uint64_t r = 0;
-            if (j < k) {
-                const uint64_t key = keys[j];
-                const bool fin = (key >> 32) != 0 && fabsf(val[j]) <= 3.402823466e38f;
-                r = fin ? (0x8000000000000000ull | ((uint64_t)(0xFFFFFFFFu - key_idx(key)) << 14) | (uint64_t)j) : 0ull;
+        sort_desc_lds(sel, Q);  // sel[0..k): the top k, descending (ties: lower index first)
+        if (!sp.use_top_p && k > 1) {
+            // without top-p the reference walks the candidates in index order: re-sort by
+            // (finite first, ascending index), carrying each one's position (< 2^14)
+            for (int j = tid; j < k; j += 1024) val[j] = key_val(sel[j]);
+            __syncthreads();
+            for (int j = tid; j < Q; j += 1024) {
+                uint64_t r = 0;
+                if (j < k && key_finite(sel[j]))
+                    r = 0x8000000000000000ull | ((uint64_t)(0xFFFFFFFFu - key_idx(sel[j])) << 14) | (uint64_t)j;
+                sel[j] = r;
             }
-            keys[j] = r;
+            __syncthreads();
+            sort_desc_lds(sel, Q);
+            if (tid < 64) {
+                int f = 0;
+                for (int j = tid; j < k; j += 64) {
+                    const uint64_t r = sel[j];
+                    if (r >> 63) {
+                        prob[j] = val[r & 0x3FFFull];
+                        idx[j] = 0xFFFFFFFFu - (uint32_t)((r >> 14) & 0xFFFFFFFFull);
+                        f++;
+                    }
+                }
+                wave_sync();
+                for (int j = tid; j < k; j += 64) val[j] = prob[j];
+                for (int o = 32; o > 0; o >>= 1) f += __shfl_xor(f, o, 64);
+                nc = f;  // the finite ones come first
+            }
+        } else if (tid < 64) {
+            // descending order: +inf keys first, then the finite ones, then -inf and NaN;
+            // the finite ones move to the front in order
+            int f = 0, a = 0;
+            for (int j = tid; j < k; j += 64) {
+                const uint64_t s = sel[j];
+                f += key_finite(s) ? 1 : 0;
+                a += ((s >> 32) == 0xFF800000u) ? 1 : 0;  // ord(+inf)
+            }
+            for (int o = 32; o > 0; o >>= 1) {
+                f += __shfl_xor(f, o, 64);
+                a += __shfl_xor(a, o, 64);
+            }
+            for (int j = tid; j < k; j += 64) {
+                const uint64_t s = sel[j];
+                if (key_finite(s)) {
+                    val[j - a] = key_val(s);
+                    idx[j - a] = key_idx(s);
+                }
+            }
+            nc = f;
         }
-        __syncthreads();
-        sort_desc_lds(keys, Q);
     }
-    if (threadIdx.x != 0) return;
-    // the finite candidates, in the order the reference walks them
-    int nc = 0;
-    if (!sp.use_top_p && k > 1) {
-        for (int j = 0; j < k; j++) {
-            const uint64_t r = keys[j];
-            if (!(r >> 63)) break;  // the non-finite ones sort last
-            const int pos = (int)(r & 0x3FFFull);
-            prob[nc] = val[pos];
-            idx[nc] = 0xFFFFFFFFu - (uint32_t)((r >> 14) & 0xFFFFFFFFull);
-            nc++;
-        }
-        for (int j = 0; j < nc; j++) val[j] = prob[j];
-    } else {
-        for (int j = 0; j < k; j++) {
-            const uint64_t key = keys[j];
-            const float v = key_val(key);
-            if ((key >> 32) != 0 && fabsf(v) <= 3.402823466e38f) {
-                val[nc] = v;
-                idx[nc] = key_idx(key);
-                nc++;
-            }
-        }
-        if (sp.use_top_p && nc > 0) {
-            // apply_top_p_candidates: descending order (ties by index), the smallest
-            // prefix whose cumulative probability reaches top_p
-            softmax_seq(val, nc, prob);
-            float cum = 0.0f;
-            int keep = 0;
-            for (int i = 0; i < nc; i++) {
-                cum += prob[i];
-                keep = i + 1;
-                if (cum >= sp.top_p) break;
-            }
-            nc = keep;
-        }
+    if (tid >= 64) return;
+    wave_sync();
+    if (sp.use_top_p && nc > 0) {
+        // apply_top_p_candidates: the smallest prefix (descending order) whose cumulative
+        // probability reaches top_p
+        softmax_wave(val, nc, ex, prob);
+        const float tp = sp.top_p;
+        const int i = walk_wave(prob, nc, [tp](float cum) { return cum >= tp; });
+        nc = i < nc ? i + 1 : nc;
     }
     if (nc == 0) {
         // argmax_slice of the original logits: the running maximum moves on unless it
         // compares greater (ties and NaN move on)
-        int64_t best = 0;
-        float bv = logits[0];
-        for (int64_t j = 1; j < n; j++) {
-            const float v = logits[j];
-            if (!(bv > v)) {
-                best = j;
-                bv = v;
+        if (tid == 0) {
+            int64_t best = 0;
+            float bv = logits[0];
+            for (int64_t j = 1; j < n; j++) {
+                const float v = logits[j];
+                if (!(bv > v)) {
+                    best = j;
+                    bv = v;
+                }
             }
+            *token = (uint32_t)best;
         }
-        *token = (uint32_t)best;
         return;
     }
     if (nc == 1) {
-        *token = idx[0];
+        if (tid == 0) *token = idx[0];
         return;
     }
-    softmax_seq(val, nc, prob);
+    softmax_wave(val, nc, ex, prob);
     const float selector = (float)(sp.seed % 10000ull) / 10000.0f;
-    float cum = 0.0f;
-    uint32_t out = idx[nc - 1];
-    for (int i = 0; i < nc; i++) {
-        cum += prob[i];
-        if (selector < cum) {
-            out = idx[i];
-            break;
-        }
-    }
-    *token = out;
+    const int i = walk_wave(prob, nc, [selector](float cum) { return selector < cum; });
+    if (tid == 0) *token = i < nc ? idx[i] : idx[nc - 1];
 }
 
 }  // namespace
@@ -294,7 +360,7 @@ __global__ __launch_bounds__(1024) void sample_final_kernel(const float *logits,
 size_t sample_scratch_bytes(int64_t n, int64_t k) {
     const int64_t blocks = (n + kSampleBlock - 1) / kSampleBlock;
     const int64_t kk = std::min<int64_t>(std::max<int64_t>(k, 1), kSampleBlock);
-    return (size_t)blocks * kk * 8 + 256 + (size_t)kSampleMaxCand * 12;
+    return (((size_t)blocks * kk * 8 + 255) & ~(size_t)255) + (size_t)kSampleMaxCand * 16;
 }
 
 bool sample_supported(int64_t n, int64_t k) {

@@ -109,3 +109,20 @@ def test_lm_head_sample_q6k(O, dev):
         assert int(tok.item()) == O.sample_token(lg, seed=seed, **cfg)
     ref = O.q6k_linear(x.cpu().numpy()[None, :], wb, n)
     check_close(ref, lg[None, :], "lm head logits")
+
+
+@pytest.mark.parametrize("top_p", [None, 0.9])
+def test_sample_infinite_logits(O, dev, top_p):
+    """+inf logits take top-k places but are not candidates (the reference keeps finite
+    candidates only); -inf and NaN sort last."""
+    import nn_amd
+    n = 9000
+    lg = nn_amd.synth_normal(21, 1, (n,), 1.0)
+    lg[[5, 77, 4000]] = np.inf
+    lg[[6, 78]] = -np.inf
+    lg[[7, 8000]] = np.nan
+    t = torch.from_numpy(lg).to(dev)
+    for seed in (0, 2500, 9999):
+        for k in (3, 10, 64):
+            got = int(nn_amd.sample_token(t, temperature=1.0, top_k=k, top_p=top_p, seed=seed).item())
+            assert got == O.sample_token(lg, temperature=1.0, top_k=k, top_p=top_p, seed=seed), (k, seed)
