@@ -84,6 +84,7 @@ typedef struct nnq_weight nnq_weight;   /* opaque: device-resident, repacked blo
 typedef struct nnq_moe nnq_moe;         /* opaque: device-resident MXFP4 expert weights + biases */
 typedef struct nnq_mlp nnq_mlp;         /* opaque: device-resident SwiGLU MLP (gate | up, down) */
 typedef struct nnq_router nnq_router;   /* opaque: device-resident f32 router Linear */
+typedef struct nnq_gguf nnq_gguf;       /* opaque: a memory-mapped GGUF file */
 
 /* ---- device ------------------------------------------------------------------- */
 
@@ -266,6 +267,49 @@ int nnq_moe_block_forward(const nnq_moe *moe, const nnq_router *router, const vo
  * [inter, hidden] — bit-exact with Mxfp4Tensor::dequantize
  * (crates/nn-gptoss/src/quantize.rs:167-188). Either output may be NULL. */
 int nnq_moe_dequant_expert(const nnq_moe *moe, int64_t expert, float *gate_up, float *down, void *stream);
+
+/* ---- GGUF ingest ------------------------------------------------------------------ */
+
+/* Open a GGUF v3 file memory-mapped (no tensor bytes are read or copied): header,
+ * metadata and tensor infos are parsed and every tensor's byte range is checked against
+ * the file.  The data section starts at the next multiple of 32 bytes after the tensor
+ * infos (fixed, as the reference does).  Errors: NNQ_ERR_WRONG_FORMAT (magic, version,
+ * unknown metadata or tensor type), NNQ_ERR_INVALID_SHAPE (a reference limit exceeded:
+ * 100000 tensors or metadata pairs, 16 MiB strings, 10^7 array elements, 8 dimensions,
+ * a zero dimension, 8 GiB per tensor), NNQ_ERR_DATA_LENGTH (truncated file, tensor data
+ * out of bounds), NNQ_ERR_INVALID_ARGUMENT (cannot open).  Host only; no device needed.
+ * Replaces GgufFile::open (crates/nn-gguf/src/reader.rs:68-141). */
+int nnq_gguf_open(const char *path, nnq_gguf **out);
+
+int nnq_gguf_close(nnq_gguf *gguf);
+
+int nnq_gguf_info(const nnq_gguf *gguf, uint32_t *version, int64_t *tensor_count, int64_t *metadata_count,
+                  uint64_t *data_offset);
+
+/* Tensor i (file order): name (valid until close), dimensions as stored (dims holds up to
+ * 8), GGUF type id, offset in the data section and byte size (GgufTensorInfo,
+ * crates/nn-gguf/src/tensor_info.rs:20-33).  Any output may be NULL. */
+int nnq_gguf_tensor_info(const nnq_gguf *gguf, int64_t i, const char **name, int32_t *n_dims, uint64_t *dims,
+                         uint32_t *dtype, uint64_t *offset, uint64_t *nbytes);
+
+/* Zero-copy tensor bytes: a pointer into the mapping, valid until close
+ * (GgufFile::tensor_data, reader.rs:287-344).  A repeated name resolves to its last entry. */
+int nnq_gguf_tensor_data(const nnq_gguf *gguf, const char *name, const uint8_t **data, uint64_t *nbytes);
+
+/* Metadata value of `key` (GgufMetadata::get, crates/nn-gguf/src/metadata.rs:98-130): its
+ * GGUF type id and value (unsigned / bool in *u, signed in *i, floats in *f, strings in
+ * *str (valid until close), arrays as element type and count).  Any output may be NULL. */
+int nnq_gguf_metadata(const nnq_gguf *gguf, const char *key, uint32_t *type, uint64_t *u, int64_t *i, double *f,
+                      const char **str, uint32_t *arr_type, uint64_t *arr_count);
+
+/* A device weight straight from a Q8_0 / Q4_K / Q6_K tensor's mapped bytes (repacked on
+ * upload, as nnq_weight_create; no f32 expansion).  The 2-D shape is read as stored,
+ * [out, in], or with ggml_order != 0 as [in, out] (ggml's ne0 first).  layout selects the
+ * block decoder the bytes follow (NNQ_LAYOUT_NN_GGUF: nn-gguf's, which its reader uses).
+ * Replaces the read_tensor_f32 + Linear path of weight loading
+ * (crates/nn-gguf/src/reader.rs:192-281). */
+int nnq_gguf_weight_create(const nnq_gguf *gguf, const char *name, nnq_layout layout, int ggml_order,
+                           nnq_weight **out);
 
 /* ---- host encoders (CPU, no device needed) --------------------------------------- */
 

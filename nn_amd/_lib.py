@@ -57,6 +57,18 @@ SIGNATURES = {
     "nnq_sample_token": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),
     "nnq_linear_sample": (c_int, [c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_void_p,
                                   c_void_p, c_void_p]),
+    "nnq_gguf_open": (c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),
+    "nnq_gguf_close": (c_int, [c_void_p]),
+    "nnq_gguf_info": (c_int, [c_void_p, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(c_i64),
+                              ctypes.POINTER(c_i64), ctypes.POINTER(c_u64)]),
+    "nnq_gguf_tensor_info": (c_int, [c_void_p, c_i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int32),
+                                     ctypes.POINTER(c_u64), ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(c_u64),
+                                     ctypes.POINTER(c_u64)]),
+    "nnq_gguf_tensor_data": (c_int, [c_void_p, ctypes.c_char_p, ctypes.POINTER(c_void_p), ctypes.POINTER(c_u64)]),
+    "nnq_gguf_metadata": (c_int, [c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(c_u64),
+                                  ctypes.POINTER(c_i64), ctypes.POINTER(c_double), ctypes.POINTER(ctypes.c_char_p),
+                                  ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(c_u64)]),
+    "nnq_gguf_weight_create": (c_int, [c_void_p, ctypes.c_char_p, c_int, c_int, ctypes.POINTER(c_void_p)]),
     "nnq_quantize_q4_k": (c_int, [c_void_p, c_sz, c_void_p]),
     "nnq_quantize_mxfp4": (c_int, [c_void_p, c_sz, c_void_p, c_void_p]),
     "nnq_quantize_q8_0": (c_int, [c_void_p, c_sz, c_void_p]),

@@ -26,7 +26,7 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-u
 HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_moe.hip", "nnq_sample.hip"]
 # per-file device flags (none at present)
 EXTRA_FLAGS = {}
-HOST_SOURCES = ["nnq_abi.cpp", "nnq_repack.cpp", "nnq_host.cpp"]
+HOST_SOURCES = ["nnq_abi.cpp", "nnq_repack.cpp", "nnq_host.cpp", "nnq_gguf.cpp"]
 
 
 def _run(cmd):

@@ -174,6 +174,11 @@ void parallel_for(int64_t n, F &&fn) {
 
 }  // namespace
 
+int nnq::set_error(int code, const char *msg) {
+    g_err = msg;
+    return code;
+}
+
 extern "C" {
 
 const char *nnq_last_error(void) { return g_err.c_str(); }

@@ -56,6 +56,9 @@ void q4k_legacy_to_gguf(const uint8_t *legacy, uint8_t *gguf);
 // Q4_K aux plane of tiles [t0, t1) from the device header plane (GGUF-spec headers).
 void q4k_aux_plane(const uint8_t *hdr, const Layout &L, uint8_t *aux, int64_t t0, int64_t t1);
 
+// the calling thread's last-error message (nnq_last_error); returns `code`
+int set_error(int code, const char *msg);
+
 // ---- kernel launch parameters ------------------------------------------------------
 struct GemvArgs {
     const uint8_t *qs;    // quant plane
