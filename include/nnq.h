@@ -3,8 +3,8 @@
  *
  * Drop-in boundary for alabsystems/nn's dequant-fused matmul over GGUF block
  * formats (Q8_0, Q4_K, Q6_K) and the GPT-OSS MXFP4 mixture-of-experts layer.
- * A Rust backend crate binds these symbols with `extern "C"` (the binding is
- * shown in INTEGRATION.md) the way nn-cuda binds libamdhip64
+ * A Rust backend crate binds these symbols with `extern "C"` the way nn-cuda
+ * binds libamdhip64
  * (crates/nn-cuda/src/hip_runtime_ffi_linux.rs:17-47): plain pointers, sizes
  * and i32 status codes, no C++ or torch types.
  *

@@ -444,7 +444,7 @@ size_t orc_dequant_q6_k_legacy(const uint8_t *data, size_t nbytes, size_t num_el
     return nb * 256;
 }
 
-/* Q6_K encoder for the nn-gguf layout.  The reference has none;
+/* Q6_K encoder for the nn-gguf layout.  The reference has none (its tests hand-build blocks);
  * build-defined: per 16-value sub-block scale amax/31, d = f16(max/127),
  * int8 sub-scales, q6 = clamp(round(v / (d*sc)), -32, 31) + 32. */
 void orc_quantize_q6_k_legacy(const float *v, size_t n, uint8_t *out) {

@@ -282,7 +282,7 @@ def test_q4k_legacy_known_values_and_divergence(O):
     blk[16:32] = 0x33
     leg = O.dequant_q4_k_legacy(blk, 256)
     assert np.all(np.abs(leg[:32] - 6.0) < 1e-4) and np.all(np.abs(leg[32:]) < 1e-6)
-    # the same bytes under the GGUF layout: elements 16..31 are 0
+    # the same bytes under the GGUF layout: elements 16..31 are 0 (the two decoders differ)
     gg = O.dequant_q4_k(blk, 256)
     assert np.all(gg[:16] == 6.0) and np.all(gg[16:32] == 0.0)
 
