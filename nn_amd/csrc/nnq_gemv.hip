@@ -790,12 +790,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tile0 = (int)blockIdx.x * R;  // this workgroup's tiles: tile0 .. tile0 + R - 1
-    // per wave: two unit buffers [token, hi/lo][256] f16, each followed by 64 zero
-    // halves that the A operand of the rows without data reads
+    // per wave: one buffer per unit of a pass [token, hi/lo][256] f16, each followed
+    // by 64 zero halves that the A operand of the rows without data reads
     constexpr int kBuf = MT * 512 + 64;
-    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][2][kBuf];
+    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][UPW][kBuf];
     __shared__ float red[WAVES][R * MT][16];
-    if (lane < 16)  // the wave's own pads, read later only by lanes of this wave
+    if (lane < 8 * UPW)  // the wave's own pads, read later only by lanes of this wave
         *reinterpret_cast<u32x4 *>(&xbuf[wv][lane >> 3][MT * 512 + 8 * (lane & 7)]) = u32x4{0u, 0u, 0u, 0u};
 
     // A-operand rows of lane group G: 4G + 2t + part (token t, hi / lo part) over the
@@ -852,22 +852,29 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        // every unit's activation slice is staged first: it needs only the activation
+        // loads (issued before the weights), so it runs while the weights stream in
+        XStat st_all[UPW][MT];
 #pragma unroll
         for (int j = 0; j < UPW; j++) {
             if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
-            uint16_t *buf = xbuf[wv][j & 1];
-            XStat st[MT];
+            uint16_t *buf = xbuf[wv][j];
 #pragma unroll
             for (int t = 0; t < MT; t++) {
                 u32x4 xv = xr[j][t];
                 if constexpr (XM == 2) xv = swiglu4(xv, xu[j][t]);
-                stage_q4k<XB>(xv, buf + 512 * t, buf + 512 * t + 256, st[t]);
+                stage_q4k<XB>(xv, buf + 512 * t, buf + 512 * t + 256, st_all[j][t]);
             }
-            // the wave's own LDS writes are read back by other lanes of the same wave
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const uint16_t *ap = buf + aoff;
+        }
+        // the wave's own LDS writes are read back by other lanes of the same wave
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
+            const XStat *st = st_all[j];
+            const uint16_t *ap = xbuf[wv][j] + aoff;
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K
