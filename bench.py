@@ -307,6 +307,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--only-gemm", action="store_true", help="only the two M=512 prefill GEMMs (for PMC runs)")
+    ap.add_argument("--only-moe", action="store_true", help="only the MXFP4 MoE layer (for PMC runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every box in this run has one MI355X, and the quantized-linear "
@@ -316,6 +318,15 @@ def main():
     nn_amd.init(0)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.only_gemm:
+        for (m, n, k) in [(512, 12288, 4096), (512, 4096, 12288)]:
+            g = bench_gemm(m, n, k, args.steps, args.warmup)
+            log(f"prefill GEMM {m}x{n}x{k}: {g['sec'] * 1e6:.2f} us/call  {g['tflops']:.1f} TFLOP/s")
+        return
+    if args.only_moe:
+        g = bench_moe(args.steps, args.warmup)
+        log(f"MXFP4 MoE: {g['sec'] * 1e6:.2f} us/call  {g['gbs']:.1f} GB/s")
         return
 
     log("bench: Q4_K GEMV 4096x12288 (rotating copies)")
