@@ -678,6 +678,115 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
+// Streaming decode GEMV over many tiles (m <= 2, Q8_0 / Q6_K; the LM head).  Each
+// workgroup loops over tiles blockIdx.x, + gridDim.x, ...  The activation (all of K)
+// is staged once per workgroup into LDS as in gemv_kernel, and every wave loads its
+// units of the next tile into registers before it computes the current one, so the
+// weight stream of one tile overlaps the unit math of the previous one.  The waves
+// of a tile meet in one of two reduction buffers (one barrier per tile).
+// ---------------------------------------------------------------------------------
+template <int FMT, int WAVES, int UPW>
+__global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(GemvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    using Unit = typename UnitOf<FMT>::T;
+    constexpr int GRAN = Fmt<FMT>::kSumGran;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int mt = (int)a.m;
+    const int units = (int)(FMT == FQ80 ? a.nblk / 8 : a.nblk);
+    const int kc = units * 256;  // K padded to whole units (the host checks mt * kc fits)
+    uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
+    float *xsum = reinterpret_cast<float *>(smem + (size_t)mt * kc * 4);
+    float *backs = xsum + (size_t)mt * (kc / GRAN);
+    __shared__ float red[2][2][WAVES][2][16];  // [tile parity][acc1 / acc2][wave][token][row]
+
+    const int64_t ntile = a.ntile, step = gridDim.x;
+    int64_t tile = blockIdx.x;  // the host launches at most ntile workgroups
+    // every load below is issued unconditionally (a clamped unit or tile re-reads valid
+    // bytes), so the in-order wait for one batch never covers a later one
+    auto load = [&](int64_t t, Unit (&u)[UPW]) {
+#pragma unroll
+        for (int i = 0; i < UPW; i++) {
+            const int ul = wv + i * WAVES;
+            load_unit(a, t, ul < units ? ul : units - 1, u[i]);
+        }
+    };
+    XRaw raw;
+    stage_x_load(a, mt, 0, kc, 1.0f / (float)(kc / 8), raw);
+    Unit w0[UPW], w1[UPW];
+    load(tile, w0);
+    stage_x_store<GRAN, FMT == FQ80>(a, kc, raw, xs, xsum, backs);
+    __syncthreads();
+
+    int par = 0;
+    const int g = lane >> 4, n = lane & 15;
+    auto body = [&](Unit (&cur)[UPW], Unit (&nxt)[UPW]) {
+        const int64_t next = tile + step;
+        load(next < ntile ? next : ntile - 1, nxt);
+        float acc1[4][2] = {}, acc2[4][2] = {};
+#pragma unroll
+        for (int i = 0; i < UPW; i++) {
+            const int ul = wv + i * WAVES;
+            if (ul < units) compute_unit(cur[i], xs, xsum, kc, mt, ul * 256, backs + ul * 8, acc1[0], acc2[0]);
+        }
+        if constexpr (FMT == FQ6K) {
+            // lane group g holds token g
+            if (g < 2) {
+                red[par][0][wv][g][n] = acc1[0][0];
+                red[par][1][wv][g][n] = acc2[0][0];
+            }
+        } else {
+            // lane group 0 holds tokens 0 and 1
+            if (g == 0) {
+                red[par][0][wv][0][n] = acc1[0][0];
+                red[par][0][wv][1][n] = acc1[0][1];
+                red[par][1][wv][0][n] = acc2[0][0];
+                red[par][1][wv][1][n] = acc2[0][1];
+            }
+        }
+        __syncthreads();  // the other buffer is rewritten only after the next tile's barrier
+        if (tid < mt * 16) {
+            const int t = tid >> 4, nn = tid & 15;
+            float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < WAVES; w2++) {
+                s1 += red[par][0][w2][t][nn];
+                s2 += red[par][1][w2][t][nn];
+            }
+            // s1 carries the f16-subnormal factor 2^-24 of the integer weight codes
+            const float bias_k = FMT == FQ80 ? 128.0f : 32.0f;
+            float y = s1 * 16777216.0f - bias_k * s2;
+            const int64_t row = tile * 16 + nn;
+            if (row < a.n) {
+                if (a.bias) y += a.bias[row];
+                gemv_status(a, y, tile == 0 && tid == 0);
+                if (a.y_bf16)
+                    reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+                else
+                    reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+            }
+            if (a.argmax_partial && t == 0) {
+                // first-index argmax of this tile's 16 logits (row-major order), NaN -> max key
+                uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
+                for (int o = 8; o > 0; o >>= 1) {
+                    uint64_t other = __shfl_xor(key, o, 16);
+                    key = other > key ? other : key;
+                }
+                if (nn == 0) a.argmax_partial[tile] = key;
+            }
+        }
+        par ^= 1;
+        tile = next;
+    };
+    for (;;) {
+        body(w0, w1);
+        if (tile >= ntile) break;
+        body(w1, w0);
+        if (tile >= ntile) break;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the last (unused) prefetch
+}
+
+// ---------------------------------------------------------------------------------
 // Q4_K decode kernel (m <= 2).  Same division of work as gemv_wave_kernel (one
 // workgroup per 16-row tile, unit u of K to wave u % WAVES, all loads of a pass
 // issued up front), arranged so that almost nothing but the MFMA inputs goes
@@ -1208,8 +1317,40 @@ static int launch_wave_t(const GemvArgs &a, void *stream) {
 
 // decode (m <= 2): 8 waves with just enough units each to cover K in one pass
 // (longer K loops over passes)
+// streaming kernel: workgroups = CUs (every one loops over tiles); dynamic LDS holds
+// the staged activation of all of K
+static int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;  // idempotent: concurrent first calls store the same value
+    }
+    return cus[dev];
+}
+
+template <int FMT, int WAVES, int UPW>
+static int launch_stream_t(const GemvArgs &a, int64_t units, int cus, void *stream) {
+    constexpr int GRAN = Fmt<FMT>::kSumGran;
+    const int64_t kc = units * 256;
+    const size_t lds = (size_t)a.m * kc * 4 + (size_t)a.m * (kc / GRAN) * 4 + (size_t)a.m * (kc / 32) * 4;
+    const int64_t grid = a.ntile < cus ? a.ntile : cus;
+    hipLaunchKernelGGL((gemv_stream_kernel<FMT, WAVES, UPW>), dim3((unsigned)grid), dim3(WAVES * 64), lds,
+                       (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+
 template <int FMT>
 static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
+    // many tiles per CU (the LM head): loop over tiles with the activation staged once
+    // per workgroup and the next tile's weights in flight during the current one's math
+    if (!a.x_swiglu) {
+        const int cus = device_cus();
+        if (a.ntile >= 4 * (int64_t)cus && a.m * units * 256 <= 8192 && units <= 16)
+            return launch_stream_t<FMT, 16, 1>(a, units, cus, stream);
+    }
     constexpr int umax = FMT == FQ4K ? 6 : 4;
     // up to two tiles per CU and K of 9-16 units: 16 waves of one unit hide more
     // latency (Q8_0 4096x4096: 6.2 instead of 6.9 us); with many tiles per CU (the

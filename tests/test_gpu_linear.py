@@ -135,6 +135,30 @@ def test_linear_small(O, dev, fmt, n, k, m):
     check_close(ref, y, f"{fmt} n={n} k={k} m={m}")
 
 
+@pytest.mark.parametrize("fmt", ["q8_0", "q6_k"])
+@pytest.mark.parametrize("n,k,m,xdt", [(16385, 1024, 1, "f32"), (16385, 4096, 2, "f32"), (20000, 2048, 2, "bf16"),
+                                       (40000, 256, 1, "bf16")])
+def test_linear_streaming_many_tiles(O, dev, fmt, n, k, m, xdt):
+    """Decode GEMV over at least four tiles per CU (the streaming form that stages x
+    once per workgroup and prefetches the next tile): ragged last tile, m = 1 and 2,
+    f32 and bf16 x, bias, and the fused argmax over the same launch."""
+    import nn_amd
+    b = quantized_weight_bytes(fmt, n, k, seed=31 + n + k, O=O)
+    w = make_weight(fmt, b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(17 + m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    bias = nn_amd.synth_normal(5, 3, (n,), 0.5)
+    y = nn_amd.quantized_linear(x, w, torch.from_numpy(bias).to(dev)).cpu().numpy()
+    ref = oracle_linear(O, fmt, b, n, k, x.float().cpu().numpy()) + bias[None, :]
+    check_close(ref, y, f"{fmt} streaming n={n} k={k} m={m} x={xdt}")
+    if m == 1:
+        logits, idx = nn_amd.linear_argmax(x[0].float(), w)
+        ref0 = oracle_linear(O, fmt, b, n, k, x[0:1].float().cpu().numpy())[0]
+        check_close(ref0[None], logits.cpu().numpy()[None], f"{fmt} streaming logits")
+        assert int(idx) == O.argmax(ref0)
+
+
 @pytest.mark.parametrize("k", [1536, 2560, 6144, 16384, 20480])
 @pytest.mark.parametrize("m,xdt", [(1, "f32"), (2, "f32"), (1, "bf16"), (2, "bf16")])
 def test_q4k_decode_launch_shapes(O, dev, k, m, xdt):
