@@ -787,6 +787,207 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
+// Q6_K streaming decode GEMV (the LM head): gemv_stream_kernel's tile loop with one
+// unit (256 k) per wave and K <= 16 units, arranged so that a tile costs little more
+// than its weight bytes:
+//  * everything that depends only on x is built once per workgroup, before the loop,
+//    in registers: the A operands of the unit's 8 MFMAs, its 2^-s block factors, and
+//    the A operand of the offset term;
+//  * the offset term 32 * sum_j sc_j * sum(x over sub-block j) is one more MFMA per
+//    unit: A = the 16 sub-block sums of x (f16 hi + lo under a power of two per token
+//    and unit), B = the row's 16 int8 scales as f16 (exact);
+//  * the int8 scales become f16 with byte moves and one packed add (1024 + 128 + s is
+//    an exact f16 built from the byte s ^ 0x80 under exponent 10), and enter the f32
+//    sums through mixed-precision FMAs;
+//  * weight pointers are scalar per wave and tile.
+// Q6_K codes q (6 bits) enter as f16 subnormals q * 2^-24, exact, as in compute_unit.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t i8pair_to_f16x2(uint32_t w, int hi) {
+    // bytes (2 hi, 2 hi + 1) of w -> f16 (s0, s1): 0x64 | (b ^ 0x80) is 1152 + s exactly
+    const uint32_t b = __builtin_amdgcn_perm(0u, w, hi ? 0x0C030C02u : 0x0C010C00u) ^ 0x64806480u;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, b) + h2{(_Float16)-1152.0f, (_Float16)-1152.0f});
+}
+__device__ __forceinline__ float f16_lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu)); }
+__device__ __forceinline__ float f16_hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
+
+template <int MT>
+__global__ __launch_bounds__(1024) void gemv_q6k_stream_kernel(GemvArgs a) {
+    constexpr int WAVES = 16, GRAN = 16;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int units = (int)a.nblk;  // 1 .. 16 (host-checked)
+    const int kc = units * 256;
+    uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
+    float *xsum = reinterpret_cast<float *>(smem + (size_t)MT * kc * 4);
+    float *backs = xsum + (size_t)MT * (kc / GRAN);
+    __shared__ float red[2][2][WAVES][2][16];  // [tile parity][main / offset][wave][token][row]
+    __shared__ __attribute__((aligned(16))) uint16_t zpad[8];
+
+    const int64_t ntile = a.ntile, step = gridDim.x;
+    int64_t tile = blockIdx.x;
+    const bool has = wv < units;  // wave-uniform: this wave owns unit wv
+    const int ul = has ? wv : 0;
+    const int p = lane >> 4, m = lane & 15, n = m, g = p;
+
+    auto qptr = [&](int64_t t) { return a.qs + (size_t)(t * a.nblk + ul) * 3072 + 12 * lane; };
+    auto hptr = [&](int64_t t) { return a.hdr + (size_t)(t * a.nblk + ul) * 288; };
+    struct W {
+        u32x3 q[4];
+        u32x4 s;
+        uint32_t d;
+    };
+    auto load = [&](int64_t t, W &w) {
+        const uint8_t *qb = qptr(t), *hb = hptr(t);
+#pragma unroll
+        for (int c = 0; c < 4; c++) w.q[c] = ldg96(qb + 768 * c);
+        w.s = ldg128(hb + 16 * n);
+        w.d = *reinterpret_cast<const uint16_t *>(hb + 256 + 2 * n);
+    };
+
+    XRaw raw;
+    stage_x_load(a, MT, 0, kc, 1.0f / (float)(kc / 8), raw);
+    W w0, w1;
+    if (has) load(tile, w0);
+    if (tid < 2) reinterpret_cast<u32x4 *>(zpad)[0] = u32x4{0u, 0u, 0u, 0u};
+    stage_x_store<GRAN, false>(a, kc, raw, xs, xsum, backs);
+    __syncthreads();
+
+    // ---- per-wave constants (x only) ----
+    // A operand of MFMA (c, h): lane (p, m) -> token m >> 2, half (m >> 1) & 1, part m & 1;
+    // non-zero only where the lane's k-slice p lies in that 16-k half (p >> 1 == half)
+    u32x4 av[4][2];
+    {
+        const int t = m >> 2, part = m & 1, half = (m >> 1) & 1;
+        const bool own = t < MT && (p >> 1) == half;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint16_t *src = own ? xs + ((size_t)t * 2 + part) * kc + ul * 256 + 64 * c + 32 * h + 8 * p : zpad;
+                av[c][h] = *reinterpret_cast<const u32x4 *>(src);
+            }
+    }
+    // 2^-s of the unit's 32-element blocks for this lane group's token
+    float xb[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) xb[i] = g < MT ? backs[g * (kc / 32) + ul * 8 + i] : 0.0f;
+    // offset-term A operand: row m = 4t + part (part < 2) holds the unit's 16 sub-block
+    // sums of token t (k-slices p = 0, 1), as f16 hi / lo of sum * 2^so(t)
+    u32x4 a2 = {0u, 0u, 0u, 0u};
+    float back2 = 0.0f;  // 2^-so of this lane group's token
+    {
+        // so per token: max |sum| over the unit's 16 sums -> [2^14, 2^15)
+        float so_t[MT];
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(xsum[t * (kc / GRAN) + ul * 16 + j]));
+            float s, b;
+            f16_prescale(mx, s, b);
+            so_t[t] = s;
+            if (g == t) back2 = b;
+        }
+        const int t = m >> 2, part = m & 3;
+        if (t < MT && part < 2 && p < 2) {
+            const float s = so_t[t];
+            uint32_t hv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                uint32_t hh, ll;
+                split_f16(xsum[t * (kc / GRAN) + ul * 16 + 8 * p + i] * s, hh, ll);
+                hv[i] = part ? ll : hh;
+            }
+            a2 = u32x4{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16)};
+        }
+    }
+
+    int par = 0;
+    auto body = [&](W &cur, W &nxt) {
+        const int64_t next = tile + step;
+        if (has) load(next < ntile ? next : ntile - 1, nxt);
+        float acc1 = 0.0f, acc2 = 0.0f;
+        if (has) {
+            // the row's 16 scales as f16 pairs: sc[i] = (scale 2i, scale 2i + 1)
+            uint32_t sc[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sc[2 * i] = i8pair_to_f16x2(cur.s[i], 0);
+                sc[2 * i + 1] = i8pair_to_f16x2(cur.s[i], 1);
+            }
+            float t1 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t A = cur.q[c][0], B = cur.q[c][1], C = cur.q[c][2];
+                const u32x4 ba = {((A)&0x000F000Fu) | ((C << 4) & 0x00300030u),
+                                  ((A >> 4) & 0x000F000Fu) | ((C << 2) & 0x00300030u),
+                                  ((A >> 8) & 0x000F000Fu) | ((C)&0x00300030u),
+                                  ((A >> 12) & 0x000F000Fu) | ((C >> 2) & 0x00300030u)};
+                const u32x4 bb = {((B)&0x000F000Fu) | ((C >> 4) & 0x00300030u),
+                                  ((B >> 4) & 0x000F000Fu) | ((C >> 6) & 0x00300030u),
+                                  ((B >> 8) & 0x000F000Fu) | ((C >> 8) & 0x00300030u),
+                                  ((B >> 12) & 0x000F000Fu) | ((C >> 10) & 0x00300030u)};
+                const floatx4 ca = mfma16x16x32_f16(av[c][0], ba, floatx4{0.f, 0.f, 0.f, 0.f});
+                const floatx4 cb = mfma16x16x32_f16(av[c][1], bb, floatx4{0.f, 0.f, 0.f, 0.f});
+                // sub-blocks 4c .. 4c + 3: scales sc[2c] (lo, hi), sc[2c + 1] (lo, hi)
+                const float ta = f16_lo(sc[2 * c]) * (ca[0] + ca[1]) + f16_hi(sc[2 * c]) * (ca[2] + ca[3]);
+                const float tb = f16_lo(sc[2 * c + 1]) * (cb[0] + cb[1]) + f16_hi(sc[2 * c + 1]) * (cb[2] + cb[3]);
+                t1 += xb[2 * c] * ta + xb[2 * c + 1] * tb;
+            }
+            // offset term: B2 lane (p, n) = scales 8 (p & 1) .. + 7 of row n (A2 is zero for p >= 2)
+            const u32x4 b2 = (p & 1) ? u32x4{sc[4], sc[5], sc[6], sc[7]} : u32x4{sc[0], sc[1], sc[2], sc[3]};
+            const floatx4 c2 = mfma16x16x32_f16(a2, b2, floatx4{0.f, 0.f, 0.f, 0.f});
+            const float d = f16_to_f32(cur.d);
+            acc1 = d * t1;
+            acc2 = d * ((c2[0] + c2[1]) * back2);
+        }
+        if (g < MT) {
+            red[par][0][wv][g][n] = acc1;
+            red[par][1][wv][g][n] = acc2;
+        }
+        __syncthreads();  // the other buffer is rewritten only after the next tile's barrier
+        if (tid < MT * 16) {
+            const int t = tid >> 4, nn = tid & 15;
+            float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < WAVES; w2++) {
+                s1 += red[par][0][w2][t][nn];
+                s2 += red[par][1][w2][t][nn];
+            }
+            float y = s1 * 16777216.0f - 32.0f * s2;
+            const int64_t row = tile * 16 + nn;
+            if (row < a.n) {
+                if (a.bias) y += a.bias[row];
+                gemv_status(a, y, tile == 0 && tid == 0);
+                if (a.y_bf16)
+                    reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+                else
+                    reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+            }
+            if (a.argmax_partial && t == 0) {
+                uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
+                for (int o = 8; o > 0; o >>= 1) {
+                    uint64_t other = __shfl_xor(key, o, 16);
+                    key = other > key ? other : key;
+                }
+                if (nn == 0) a.argmax_partial[tile] = key;
+            }
+        }
+        par ^= 1;
+        tile = next;
+    };
+    for (;;) {
+        body(w0, w1);
+        if (tile >= ntile) break;
+        body(w1, w0);
+        if (tile >= ntile) break;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the last (unused) prefetch
+}
+
+// ---------------------------------------------------------------------------------
 // Q4_K decode kernel (m <= 2).  Same division of work as gemv_wave_kernel (one
 // workgroup per 16-row tile, unit u of K to wave u % WAVES, all loads of a pass
 // issued up front), arranged so that almost nothing but the MFMA inputs goes
@@ -1348,8 +1549,21 @@ static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
     // per workgroup and the next tile's weights in flight during the current one's math
     if (!a.x_swiglu) {
         const int cus = device_cus();
-        if (a.ntile >= 4 * (int64_t)cus && a.m * units * 256 <= 8192 && units <= 16)
+        if (a.ntile >= 4 * (int64_t)cus && a.m * units * 256 <= 8192 && units <= 16) {
+            if constexpr (FMT == FQ6K) {
+                const int64_t kc = units * 256;
+                const size_t lds = (size_t)a.m * kc * 4 + (size_t)a.m * (kc / 16) * 4 + (size_t)a.m * (kc / 32) * 4;
+                const int64_t grid = a.ntile < cus ? a.ntile : cus;
+                if (a.m == 1)
+                    hipLaunchKernelGGL((gemv_q6k_stream_kernel<1>), dim3((unsigned)grid), dim3(1024), lds,
+                                       (hipStream_t)stream, a);
+                else
+                    hipLaunchKernelGGL((gemv_q6k_stream_kernel<2>), dim3((unsigned)grid), dim3(1024), lds,
+                                       (hipStream_t)stream, a);
+                return (int)hipGetLastError();
+            }
             return launch_stream_t<FMT, 16, 1>(a, units, cus, stream);
+        }
     }
     constexpr int umax = FMT == FQ4K ? 6 : 4;
     // up to two tiles per CU and K of 9-16 units: 16 waves of one unit hide more
