@@ -1263,6 +1263,150 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
 }
 
 // ---------------------------------------------------------------------------------
+// Q4_K streaming decode GEMV (m <= 2, K <= 16 units, many tiles: the fused gate | up
+// of an MLP).  gemv_q4k_decode_kernel's unit math inside gemv_stream_kernel's tile
+// loop: wave w owns unit w of every tile, stages its activation slice once, keeps the
+// 8 A operands and the slice statistics in registers, and loads its unit of the next
+// tile before it computes the current one.
+// ---------------------------------------------------------------------------------
+template <int MT, bool XB>
+__global__ __launch_bounds__(1024) void gemv_q4k_stream_kernel(GemvArgs a) {
+    constexpr int WAVES = 16, kBuf = MT * 512 + 64;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][kBuf];
+    __shared__ float red[2][WAVES][MT][16];  // [tile parity][wave][token][row]
+    if (lane < 8)  // the wave's zero pad, read only by lanes of this wave
+        *reinterpret_cast<u32x4 *>(&xbuf[wv][MT * 512 + 8 * lane]) = u32x4{0u, 0u, 0u, 0u};
+
+    const int units = (int)a.nblk, k = (int)a.k;  // units <= 16 (host-checked)
+    const bool has = wv < units;                  // wave-uniform
+    const int ul = has ? wv : 0;
+    const int G = lane >> 4, n = lane & 15, i = n & 3;
+    const bool own = G == (n >> 2) && (i >> 1) < MT;
+    const int aoff = own ? ((i >> 1) * 2 + (i & 1)) * 256 + 64 * G : MT * 512;
+    const int64_t ntile = a.ntile, step = gridDim.x;
+    int64_t tile = blockIdx.x;
+
+    struct W {
+        u32x4 q0, q1, h;
+    };
+    auto load = [&](int64_t t, W &w) {
+        const uint8_t *qb = a.qs + ((size_t)t * units + ul) * 2048 + 16 * lane;
+        w.q0 = ldg128(qb);
+        w.q1 = ldg128(qb + 1024);
+        w.h = ldg128(a.hdr + ((size_t)t * units + ul) * 256 + 16 * n);
+    };
+    // activation slice of unit ul (issued before the weights)
+    constexpr int xe = XB ? 2 : 4;
+    u32x4 xr[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const uint8_t *p = reinterpret_cast<const uint8_t *>(a.x) + ((size_t)t * k + ul * 256 + 4 * lane) * xe;
+        if (XB) {
+            const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+            xr[t] = u32x4{w2[0], w2[1], 0u, 0u};
+        } else {
+            xr[t] = *reinterpret_cast<const u32x4 *>(p);
+        }
+    }
+    W w0, w1;
+    if (has) load(tile, w0);
+    XStat st[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) stage_q4k<XB>(xr[t], xbuf[wv] + 512 * t, xbuf[wv] + 512 * t + 256, st[t]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    u32x4 av[4][2];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; q4++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) av[q4][h] = *reinterpret_cast<const u32x4 *>(xbuf[wv] + aoff + 32 * h + 8 * q4);
+    const uint32_t hsel = 0u - (uint32_t)(G >> 1);  // all ones for sub-blocks 4..7
+
+    int par = 0;
+    auto body = [&](W &cur, W &nxt) {
+        const int64_t next = tile + step;
+        if (has) load(next < ntile ? next : ntile - 1, nxt);
+        float acc1[MT], acc2[MT];
+#pragma unroll
+        for (int t = 0; t < MT; t++) acc1[t] = acc2[t] = 0.0f;
+        if (has) {
+            // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K packing,
+            // get_scale_min_k4, crates/nn-core/src/layers/quantized/linear.rs:166-176)
+            const u32x4 &h = cur.h;
+            const float d = f16_to_f32(h[0] & 0xFFFFu), dmin = f16_to_f32(h[0] >> 16);
+            const uint32_t S1 = h[1], S2 = h[2], S3 = h[3];
+            const uint32_t scw =
+                ((S1 & 0x3F3F3F3Fu) & ~hsel) | (((S3 & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) & hsel);
+            const uint32_t mnw =
+                ((S2 & 0x3F3F3F3Fu) & ~hsel) | ((((S3 >> 4) & 0x0F0F0F0Fu) | ((S2 >> 2) & 0x30303030u)) & hsel);
+            const uint32_t scp = scw >> (16 * (G & 1)), mnp = mnw >> (16 * (G & 1));
+            const float sc_lo = (float)(scp & 0xFFu), sc_hi = 0.0625f * (float)((scp >> 8) & 0xFFu);
+            const float mn_lo = (float)(mnp & 0xFFu), mn_hi = (float)((mnp >> 8) & 0xFFu);
+            floatx4 clo = {0.f, 0.f, 0.f, 0.f}, chi = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                const u32x4 q = q4 < 2 ? cur.q0 : cur.q1;
+                const uint32_t w0 = q[2 * (q4 & 1)], w1 = q[2 * (q4 & 1) + 1];
+                const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
+                const u32x4 blo = {w0 & 0x000F000Fu, w0s & 0x000F000Fu, w1 & 0x000F000Fu, w1s & 0x000F000Fu};
+                const u32x4 bhi = {w0 & 0x00F000F0u, w0s & 0x00F000F0u, w1 & 0x00F000F0u, w1s & 0x00F000F0u};
+                clo = mfma16x16x32_f16(av[q4][0], blo, clo);
+                chi = mfma16x16x32_f16(av[q4][1], bhi, chi);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const float T = (sc_lo * st[t].b_lo) * (clo[2 * t] + clo[2 * t + 1]) +
+                                (sc_hi * st[t].b_hi) * (chi[2 * t] + chi[2 * t + 1]);
+                acc1[t] = d * T;
+                acc2[t] = dmin * (mn_lo * st[t].xs_lo + mn_hi * st[t].xs_hi);
+            }
+        }
+        // y = 2^24 * (code sums) - (min terms), summed over the lane groups, then the waves
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const float v = sum_rows(acc1[t] * 16777216.0f - acc2[t]);
+            if (lane < 16) red[par][wv][t][lane] = v;
+        }
+        __syncthreads();  // the other buffer is rewritten only after the next tile's barrier
+        if (tid < MT * 16) {
+            const int t = tid >> 4, nn = tid & 15;
+            float y = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < WAVES; w2++) y += red[par][w2][t][nn];
+            const int64_t row = tile * 16 + nn;
+            if (row < a.n) {
+                if (a.bias) y += a.bias[row];
+                gemv_status(a, y, tile == 0 && tid == 0);
+                if (a.y_bf16)
+                    reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+                else
+                    reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+            }
+            if (a.argmax_partial && t == 0) {
+                uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
+                for (int o = 8; o > 0; o >>= 1) {
+                    uint64_t other = __shfl_xor(key, o, 16);
+                    key = other > key ? other : key;
+                }
+                if (nn == 0) a.argmax_partial[tile] = key;
+            }
+        }
+        par ^= 1;
+        tile = next;
+    };
+    for (;;) {
+        body(w0, w1);
+        if (tile >= ntile) break;
+        body(w1, w0);
+        if (tile >= ntile) break;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the last (unused) prefetch
+}
+
+// ---------------------------------------------------------------------------------
 // Bit-exact dequantization from the device layout (the parity gate for decode).
 // One wave per (tile, unit); lane l = 16p + n decodes its bytes for row n.
 // ---------------------------------------------------------------------------------
@@ -1604,8 +1748,29 @@ static int launch_q4k_decode_t(const GemvArgs &a, void *stream) {
 // Q4_K decode shapes, from sweeps on MI355X: K of up to 16 units takes 8 waves of
 // up to 2 units, longer K 16 waves of up to 4 units (then passes); one tile per
 // workgroup (two tiles per workgroup, sharing the staged activation, measured slower).
+static int device_cus();
+
 static int launch_q4k_decode(const GemvArgs &a, void *stream) {
     const int64_t units = a.nblk;
+    // many tiles per CU and K <= 16 units: one workgroup per CU loops over tiles
+    if (!a.x_swiglu && units <= 16) {
+        const int cus = device_cus();
+        if (a.ntile >= 4 * (int64_t)cus) {
+            const dim3 grid((unsigned)(a.ntile < cus ? a.ntile : cus));
+            if (a.m == 1) {
+                if (a.x_bf16)
+                    hipLaunchKernelGGL((gemv_q4k_stream_kernel<1, true>), grid, dim3(1024), 0, (hipStream_t)stream, a);
+                else
+                    hipLaunchKernelGGL((gemv_q4k_stream_kernel<1, false>), grid, dim3(1024), 0, (hipStream_t)stream, a);
+            } else {
+                if (a.x_bf16)
+                    hipLaunchKernelGGL((gemv_q4k_stream_kernel<2, true>), grid, dim3(1024), 0, (hipStream_t)stream, a);
+                else
+                    hipLaunchKernelGGL((gemv_q4k_stream_kernel<2, false>), grid, dim3(1024), 0, (hipStream_t)stream, a);
+            }
+            return (int)hipGetLastError();
+        }
+    }
     if (units <= 4) return launch_q4k_decode_t<4, 1, 1>(a, stream);
     if (units <= 8) return launch_q4k_decode_t<8, 1, 1>(a, stream);
     if (units <= 16) return launch_q4k_decode_t<8, 2, 1>(a, stream);

@@ -135,7 +135,7 @@ def test_linear_small(O, dev, fmt, n, k, m):
     check_close(ref, y, f"{fmt} n={n} k={k} m={m}")
 
 
-@pytest.mark.parametrize("fmt", ["q8_0", "q6_k"])
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k"])
 @pytest.mark.parametrize("n,k,m,xdt", [(16385, 1024, 1, "f32"), (16385, 4096, 2, "f32"), (20000, 2048, 2, "bf16"),
                                        (40000, 256, 1, "bf16")])
 def test_linear_streaming_many_tiles(O, dev, fmt, n, k, m, xdt):
