@@ -60,29 +60,35 @@ __device__ __forceinline__ void wave_sync() {
 // (then t is the kth largest key).  Each wave counts into its own histogram (hist holds
 // blockDim / 64 of them), so equal digits only contend within a wave.  Every thread of
 // the workgroup calls it.
-template <int E>
+template <int E, int NW>
 __device__ uint64_t radix_kth(const uint64_t (&e)[E], int k, int *hist, uint64_t *bcast) {
     uint64_t prefix = 0, mask = 0;
     int rem = k;
-    const int lane = threadIdx.x & 63, nw = blockDim.x / 64;
+    const int lane = threadIdx.x & 63;
     int *my = hist + (threadIdx.x / 64) * 256;
+    int *col = hist + NW * 256;  // [256] digit counts summed over the waves
     for (int shift = 56; shift >= 0; shift -= 8) {
-        for (int i = threadIdx.x; i < 256 * nw; i += blockDim.x) hist[i] = 0;
+        for (int i = threadIdx.x; i < 256 * NW; i += NW * 64) hist[i] = 0;
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < E; r++)
             if (e[r] != 0 && (e[r] & mask) == prefix) atomicAdd(&my[(e[r] >> shift) & 255], 1);
+        __syncthreads();
+        // column sums: one digit per thread, the NW loads independent of each other
+        for (int d = threadIdx.x; d < 256; d += NW * 64) {
+            int cd = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) cd += hist[w * 256 + d];
+            col[d] = cd;
+        }
         __syncthreads();
         if (threadIdx.x < 64) {
             // lane l holds digits 255 - 4l .. 252 - 4l (descending order)
             int c[4], sum = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int d = 255 - (4 * lane + j);
-                int cd = 0;
-                for (int w = 0; w < nw; w++) cd += hist[w * 256 + d];
-                c[j] = cd;
-                sum += cd;
+                c[j] = col[255 - (4 * lane + j)];
+                sum += c[j];
             }
             int before = sum;  // inclusive scan over lanes, then exclusive
 #pragma unroll
@@ -110,21 +116,48 @@ __device__ uint64_t radix_kth(const uint64_t (&e)[E], int k, int *hist, uint64_t
     return prefix;
 }
 
-// Bitonic sort, descending, of n keys in LDS (n a power of two <= 16384); all threads.
+// Bitonic sort, descending, of n keys in LDS (n a power of two <= 16384); all threads
+// call it.  Up to 64 keys wave 0 sorts them in registers (one per lane, partners by lane
+// exchange), up to 128 in LDS with wave-level synchronisation; one barrier at the end
+// publishes the result to the other waves.
 __device__ void sort_desc_lds(uint64_t *a, int n) {
-    for (int size = 2; size <= n; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
-                const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
-                const bool desc = (lo & size) == 0;
-                const uint64_t x = a[lo], y = a[hi];
-                if ((x < y) == desc) {
-                    a[lo] = y;
-                    a[hi] = x;
+    if (n <= 64) {
+        // one key per lane of wave 0, the network on registers (lane exchanges)
+        if (threadIdx.x < 64) {
+            const int lane = threadIdx.x;
+            uint64_t v = lane < n ? a[lane] : 0ull;
+            for (int size = 2; size <= n; size <<= 1)
+                for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                    const uint64_t o = __shfl_xor(v, stride, 64);
+                    const bool desc = (lane & size) == 0, lower = (lane & stride) == 0;
+                    v = (lower == desc) ? (o > v ? o : v) : (o < v ? o : v);
                 }
-            }
-            __syncthreads();
+            if (lane < n) a[lane] = v;
         }
+        __syncthreads();
+        return;
+    }
+    const bool small = n <= 128;  // uniform
+    if (!small || threadIdx.x < 64) {
+        const int nth = small ? 64 : (int)blockDim.x;
+        for (int size = 2; size <= n; size <<= 1)
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                for (int i = threadIdx.x; i < n / 2; i += nth) {
+                    const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+                    const bool desc = (lo & size) == 0;
+                    const uint64_t x = a[lo], y = a[hi];
+                    if ((x < y) == desc) {
+                        a[lo] = y;
+                        a[hi] = x;
+                    }
+                }
+                if (small)
+                    wave_sync();
+                else
+                    __syncthreads();
+            }
+    }
+    if (small) __syncthreads();
 }
 
 struct SampleParams {
@@ -137,7 +170,7 @@ struct SampleParams {
 __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, int64_t n, const uint32_t *past,
                                                            int64_t n_past, SampleParams sp, int kk, uint64_t *cand) {
     __shared__ int cnt[kSampleBlock];
-    __shared__ int hist[4 * 256];
+    __shared__ int hist[5 * 256];
     __shared__ uint64_t bcast[1];
     __shared__ int nout;
     const int tid = threadIdx.x;
@@ -177,7 +210,7 @@ __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, 
     // the block's real logits may be fewer than kk: keep them all, pad the slots with 0
     const int real = (int)std::min<int64_t>(kSampleBlock, n - base);
     const int kb = std::min(kk, real);
-    const uint64_t kth = radix_kth<E>(e, kb, hist, bcast);
+    const uint64_t kth = radix_kth<E, 4>(e, kb, hist, bcast);
     uint64_t *out = cand + (int64_t)blockIdx.x * kk;
 #pragma unroll
     for (int r = 0; r < E; r++)
@@ -185,13 +218,24 @@ __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, 
     for (int j = kb + tid; j < kk; j += 256) out[j] = 0;
 }
 
-__device__ __forceinline__ float lane_f(float v, int i) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+// The f32 sum ((0 + p[0]) + p[1]) + ... + p[n - 1] in element order, the same value in
+// every lane: 16-byte broadcast reads (p is 16-byte aligned and readable up to the next
+// multiple of 4), the additions one after another.
+__device__ __forceinline__ float ordered_sum(const float *p, int n) {
+    float sum = 0.0f;
+    for (int i = 0; i < n; i += 4) {
+        const floatx4 v = *reinterpret_cast<const floatx4 *>(p + i);
+        sum += v[0];
+        if (i + 1 < n) sum += v[1];
+        if (i + 2 < n) sum += v[2];
+        if (i + 3 < n) sum += v[3];
+    }
+    return sum;
 }
 
 // softmax_candidates (sampling.rs:371-391) of val[0..n) into p[0..n), by wave 0:
 // exponentials and quotients in parallel, the maximum (order-free) by reduction, the sum
-// in candidate order, element by element from the lanes.
+// in candidate order.
 __device__ void softmax_wave(const float *val, int n, float *ex, float *p) {
     const int lane = threadIdx.x;
     float mx = -INFINITY;
@@ -202,14 +246,9 @@ __device__ void softmax_wave(const float *val, int n, float *ex, float *p) {
         wave_sync();
         return;
     }
-    float sum = 0.0f;
-    for (int c = 0; c < n; c += 64) {
-        const float e = c + lane < n ? expf(val[c + lane] - mx) : 0.0f;
-        if (c + lane < n) ex[c + lane] = e;
-        const int m = min(64, n - c);
-        for (int i = 0; i < m; i++) sum += lane_f(e, i);
-    }
+    for (int i = lane; i < n; i += 64) ex[i] = expf(val[i] - mx);
     wave_sync();
+    const float sum = ordered_sum(ex, n);
     if (!(fabsf(sum) <= 3.402823466e38f) || sum == 0.0f) {
         for (int i = lane; i < n; i += 64) p[i] = 1.0f / (float)n;
     } else {
@@ -218,30 +257,32 @@ __device__ void softmax_wave(const float *val, int n, float *ex, float *p) {
     wave_sync();
 }
 
-// the first i with (cumulative sum of p[0..i] in order) meeting `stop` (n when none)
+// the first i with (cumulative sum of p[0..i] in order) meeting `stop` (n when none);
+// every lane walks the same broadcast values
 template <class F>
 __device__ int walk_wave(const float *p, int n, F stop) {
-    const int lane = threadIdx.x;
     float cum = 0.0f;
-    for (int c = 0; c < n; c += 64) {
-        const float v = c + lane < n ? p[c + lane] : 0.0f;
-        const int m = min(64, n - c);
-        for (int i = 0; i < m; i++) {
-            cum += lane_f(v, i);
-            if (stop(cum)) return c + i;
+    for (int i = 0; i < n; i += 4) {
+        const floatx4 v = *reinterpret_cast<const floatx4 *>(p + i);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (i + j >= n) return n;
+            cum += v[j];
+            if (stop(cum)) return i + j;
         }
     }
     return n;
 }
 
-__global__ __launch_bounds__(1024) void sample_final_kernel(const float *logits, int64_t n, const uint64_t *cand,
+template <int NTH>
+__global__ __launch_bounds__(NTH) void sample_final_kernel(const float *logits, int64_t n, const uint64_t *cand,
                                                             int ncand, SampleParams sp, float *work,
                                                             uint32_t *token) {
     __shared__ uint64_t sel[kSampleMaxCand];
-    __shared__ int hist[16 * 256];
+    __shared__ int hist[(NTH / 64 + 1) * 256];
     __shared__ uint64_t bcast[1];
     __shared__ int nsel;
-    constexpr int E = kSampleMaxCand / 1024;
+    constexpr int E = 16;  // keys per thread: NTH * 16 >= the candidates (host-checked)
     const int tid = threadIdx.x, k = (int)sp.k;
     // the tail's arrays: in the upper half of `sel` when k <= 2048, else global scratch
     const bool in_lds = k <= 2048;
@@ -254,14 +295,14 @@ __global__ __launch_bounds__(1024) void sample_final_kernel(const float *logits,
         uint64_t e[E];
 #pragma unroll
         for (int r = 0; r < E; r++) {
-            const int j = r * 1024 + tid;
+            const int j = r * NTH + tid;
             e[r] = j < ncand ? cand[j] : 0ull;
         }
         if (tid == 0) nsel = 0;
-        const uint64_t kth = radix_kth<E>(e, k, hist, bcast);  // (its barriers order nsel)
+        const uint64_t kth = radix_kth<E, NTH / 64>(e, k, hist, bcast);  // (its barriers order nsel)
         int Q = 1;
         while (Q < k) Q <<= 1;
-        for (int j = k + tid; j < Q; j += 1024) sel[j] = 0;
+        for (int j = k + tid; j < Q; j += NTH) sel[j] = 0;
 #pragma unroll
         for (int r = 0; r < E; r++)
             if (e[r] >= kth && e[r] != 0) sel[atomicAdd(&nsel, 1)] = e[r];
@@ -270,9 +311,9 @@ __global__ __launch_bounds__(1024) void sample_final_kernel(const float *logits,
         if (!sp.use_top_p && k > 1) {
             // without top-p the reference walks the candidates in index order: re-sort by
             // (finite first, ascending index), carrying each one's position (< 2^14)
-            for (int j = tid; j < k; j += 1024) val[j] = key_val(sel[j]);
+            for (int j = tid; j < k; j += NTH) val[j] = key_val(sel[j]);
             __syncthreads();
-            for (int j = tid; j < Q; j += 1024) {
+            for (int j = tid; j < Q; j += NTH) {
                 uint64_t r = 0;
                 if (j < k && key_finite(sel[j]))
                     r = 0x8000000000000000ull | ((uint64_t)(0xFFFFFFFFu - key_idx(sel[j])) << 14) | (uint64_t)j;
@@ -389,8 +430,15 @@ int launch_sample(const float *logits, int64_t n, const uint32_t *past, int64_t 
                                             (((size_t)blocks * kk * 8 + 255) & ~(size_t)255));
     hipLaunchKernelGGL(sample_local_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, logits, n, past,
                        n_past, sp, kk, cand);
-    hipLaunchKernelGGL(sample_final_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, n, cand,
-                       (int)(blocks * kk), sp, work, token);
+    // up to 4096 candidates (top-k up to 54 over a 151936 vocabulary) four waves hold
+    // them, and the select's barriers are cheaper than with sixteen
+    const int ncand = (int)(blocks * kk);
+    if (ncand <= 256 * 16)
+        hipLaunchKernelGGL((sample_final_kernel<256>), dim3(1), dim3(256), 0, (hipStream_t)stream, logits, n, cand,
+                           ncand, sp, work, token);
+    else
+        hipLaunchKernelGGL((sample_final_kernel<1024>), dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, n, cand,
+                           ncand, sp, work, token);
     return (int)hipGetLastError();
 }
 
