@@ -24,9 +24,10 @@ struct nnq_weight {
 };
 
 struct nnq_mlp {
-    nnq_weight *gu = nullptr;    // [2 * inter, hidden]: gate rows, then up rows
+    nnq_weight *gu = nullptr;    // [2 * inter, hidden]: gate rows, then up rows (or interleaved8)
     nnq_weight *down = nullptr;  // [hidden, inter]
     int64_t hidden = 0, inter = 0;
+    bool interleaved8 = false;   // rows 16j .. 16j + 7 = gate rows 8j .., 16j + 8 .. = up rows 8j ..
 };
 
 struct nnq_router {
@@ -350,8 +351,10 @@ static size_t linear_scratch_bytes(const nnq_weight *w, int64_t m, nnq_dtype x_d
 
 static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m, const float *bias,
                            void *y, nnq_dtype y_dtype, void *stream, int x_swiglu = 0, int32_t *status = nullptr,
-                           int status_mode = 0, void *ext_scratch = nullptr) {
+                           int status_mode = 0, void *ext_scratch = nullptr, int swiglu_out = 0) {
     if (m == 0) return NNQ_OK;
+    if (swiglu_out && (w->L.fmt != NNQ_FMT_Q4_K || m > 2 || x_swiglu || bias || w->L.n % 16))
+        return fail(NNQ_ERR_INVALID_ARGUMENT, "SwiGLU epilogue needs a Q4_K decode GEMV over whole tiles");
     const Layout &L = w->L;
     const int64_t k = L.k;
     const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, ye = y_dtype == NNQ_BF16 ? 2 : 4;
@@ -378,6 +381,7 @@ static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype
         a.x = (const uint8_t *)x + (size_t)m0 * xrow * xe;
         a.x_bf16 = x_dtype == NNQ_BF16;
         a.x_swiglu = x_swiglu;
+        a.swiglu_out = swiglu_out;
         a.bias = bias;
         a.y = (uint8_t *)y + (size_t)m0 * L.n * ye;
         a.y_bf16 = y_dtype == NNQ_BF16;
@@ -549,10 +553,22 @@ int nnq_mlp_create(nnq_format gu_fmt, nnq_layout gu_layout, const uint8_t *gate,
     if (hidden <= 0 || inter <= 0)
         return fail(NNQ_ERR_INVALID_ARGUMENT, "MLP shape hidden=%lld inter=%lld", (long long)hidden, (long long)inter);
     // gate_proj and up_proj are W[inter, hidden]: stacked they are one W[2 * inter, hidden]
-    // (block rows are independent), so a single GEMV computes both
+    // (block rows are independent), so a single GEMV computes both.  Q4_K with inter a
+    // multiple of 8 stacks them 8 rows at a time (8 gate rows, the same 8 up rows, ...), so
+    // every 16-row tile holds matching gate and up rows and the decode GEMV can write
+    // silu(gate) * up directly.
     std::vector<uint8_t> cat(2 * gu_nbytes);
-    std::memcpy(cat.data(), gate, gu_nbytes);
-    std::memcpy(cat.data() + gu_nbytes, up, gu_nbytes);
+    const bool il8 = gu_fmt == NNQ_FMT_Q4_K && inter % 8 == 0 && gu_nbytes % (size_t)inter == 0;
+    if (il8) {
+        const size_t rb = gu_nbytes / (size_t)inter;  // bytes of one row (whole blocks)
+        for (int64_t g8 = 0; g8 < inter / 8; g8++) {
+            std::memcpy(cat.data() + (size_t)(16 * g8) * rb, gate + (size_t)(8 * g8) * rb, 8 * rb);
+            std::memcpy(cat.data() + (size_t)(16 * g8 + 8) * rb, up + (size_t)(8 * g8) * rb, 8 * rb);
+        }
+    } else {
+        std::memcpy(cat.data(), gate, gu_nbytes);
+        std::memcpy(cat.data() + gu_nbytes, up, gu_nbytes);
+    }
     nnq_weight *gu = nullptr, *dn = nullptr;
     int rc = nnq_weight_create(gu_fmt, gu_layout, cat.data(), cat.size(), 2 * inter, hidden, &gu);
     if (rc) return rc;
@@ -566,6 +582,7 @@ int nnq_mlp_create(nnq_format gu_fmt, nnq_layout gu_layout, const uint8_t *gate,
     p->down = dn;
     p->hidden = hidden;
     p->inter = inter;
+    p->interleaved8 = il8;
     *out = p;
     return NNQ_OK;
 }
@@ -586,9 +603,13 @@ int nnq_mlp_forward(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t 
     if (m == 0) return NNQ_OK;
     const int64_t I = p->inter;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    const bool fused = m <= 2;  // the down GEMV takes gate | up and applies SwiGLU while staging
-    // one scratch: gate | up [m, 2I] f32, h [m, I] f32, then the GEMM scratch of either linear
-    const size_t gu_bytes = al((size_t)m * 2 * I * 4), h_bytes = fused ? 0 : al((size_t)m * I * 4);
+    // m <= 2: interleaved Q4_K gate | up -> the GEMV writes h = silu(gate) * up and the
+    // down GEMV reads h; otherwise the down GEMV takes gate | up and applies SwiGLU while
+    // staging.  m > 2: linear, swiglu_kernel, linear.
+    const bool fused = m <= 2, hout = fused && p->interleaved8;
+    // one scratch: gate | up [m, 2I] f32 (h [m, I] when hout), h [m, I] f32, then the GEMM
+    // scratch of either linear
+    const size_t gu_bytes = al((size_t)m * (hout ? 1 : 2) * I * 4), h_bytes = fused ? 0 : al((size_t)m * I * 4);
     const size_t lin_bytes =
         std::max(linear_scratch_bytes(p->gu, m, x_dtype), fused ? 0 : linear_scratch_bytes(p->down, m, NNQ_F32));
     Scratch s;
@@ -596,11 +617,13 @@ int nnq_mlp_forward(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t 
     uint8_t *base = reinterpret_cast<uint8_t *>(s.p);
     float *gu = reinterpret_cast<float *>(base);
     void *lin = lin_bytes ? base + gu_bytes + h_bytes : nullptr;
-    rc = dispatch_linear(p->gu, x, x_dtype, m, nullptr, gu, NNQ_F32, stream, 0, status_dev, fused ? 1 : 0, lin);
+    rc = dispatch_linear(p->gu, x, x_dtype, m, nullptr, gu, NNQ_F32, stream, 0, status_dev, fused ? 1 : 0, lin,
+                         hout ? 1 : 0);
     if (rc) return rc;
+    if (hout) return dispatch_linear(p->down, gu, NNQ_F32, m, nullptr, y, y_dtype, stream, 0, status_dev, 2);
     if (fused) return dispatch_linear(p->down, gu, NNQ_F32, m, nullptr, y, y_dtype, stream, 1, status_dev, 2);
     float *h = reinterpret_cast<float *>(base + gu_bytes);
-    int e = launch_swiglu(gu, m, I, h, status_dev, stream);
+    int e = launch_swiglu(gu, m, I, h, status_dev, stream, p->interleaved8 ? 1 : 0);
     if (e) return hip_fail((hipError_t)e, "swiglu launch");
     rc = dispatch_linear(p->down, h, NNQ_F32, m, nullptr, y, y_dtype, stream, 0, nullptr, 0, lin);
     if (rc) return rc;

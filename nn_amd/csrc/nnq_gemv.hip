@@ -42,6 +42,25 @@ __device__ __forceinline__ void gemv_status(const GemvArgs &a, float y, bool fir
     if (a.status_mode == 2 && !(fabsf(y) <= 3.402823466e38f)) *a.status = NNQ_ERR_NON_FINITE;
 }
 
+// SwiGLU epilogue of a gate | up GEMV whose 16-row tiles hold 8 gate rows and then the
+// 8 matching up rows: the 16 lanes of a tile (nn = row in tile) exchange halves, and
+// lane nn < 8 stores silu(gate) * up (f32, as Qwen3MLP::forward, crates/nn-qwen3/src/
+// layers.rs:40-47) at column 8 * tile + nn of y [m, n / 2].  Every lane of the 16 calls it.
+__device__ __forceinline__ void store_swiglu_pair(const GemvArgs &a, float y, int t, int64_t tile, int nn,
+                                                  bool first) {
+    const float other = __shfl_xor(y, 8, 16);
+    if (a.status_mode == 1 && first) *a.status = NNQ_OK;
+    if (nn < 8) {
+        const float h = y / (1.0f + expf(-y)) * other;
+        if (a.status_mode == 2 && !(fabsf(h) <= 3.402823466e38f)) *a.status = NNQ_ERR_NON_FINITE;
+        const int64_t col = tile * 8 + nn, cols = a.n / 2;
+        if (a.y_bf16)
+            reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * cols + col] = (uint16_t)f32_to_bf16_bits(h);
+        else
+            reinterpret_cast<float *>(a.y)[(int64_t)t * cols + col] = h;
+    }
+}
+
 enum { FQ4K = 12, FQ80 = 8, FQ6K = 14 };
 
 template <int FMT>
@@ -1242,7 +1261,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
 #pragma unroll
         for (int w2 = 0; w2 < WAVES; w2++) y += red[w2][rt][nn];
         const int64_t row = tile * 16 + nn;
-        if (row < a.n) {
+        if (a.swiglu_out) {
+            // rows nn < 8 are gate rows, nn + 8 their up rows (full tiles: n = 2 * inter, inter % 8 == 0)
+            store_swiglu_pair(a, y, t, tile, nn, blockIdx.x == 0 && tid == 0);
+        } else if (row < a.n) {
             if (a.bias) y += a.bias[row];
             gemv_status(a, y, blockIdx.x == 0 && tid == 0);
             if (a.y_bf16)
@@ -1377,7 +1399,9 @@ __global__ __launch_bounds__(1024) void gemv_q4k_stream_kernel(GemvArgs a) {
 #pragma unroll
             for (int w2 = 0; w2 < WAVES; w2++) y += red[par][w2][t][nn];
             const int64_t row = tile * 16 + nn;
-            if (row < a.n) {
+            if (a.swiglu_out) {
+                store_swiglu_pair(a, y, t, tile, nn, tile == 0 && tid == 0);
+            } else if (row < a.n) {
                 if (a.bias) y += a.bias[row];
                 gemv_status(a, y, tile == 0 && tid == 0);
                 if (a.y_bf16)
@@ -1522,7 +1546,17 @@ __global__ void argmax_final_kernel(const unsigned long long *partial, int64_t c
                                     int32_t *status) {
     __shared__ unsigned long long red[16];
     unsigned long long key = 0;
-    for (int64_t i = threadIdx.x; i < count; i += blockDim.x) key = partial[i] > key ? partial[i] : key;
+    // eight independent loads in flight per thread and round (one round up to 8192 keys)
+    for (int64_t base = threadIdx.x; base < count; base += 8 * (int64_t)blockDim.x) {
+        unsigned long long v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int64_t i = base + (int64_t)u * blockDim.x;
+            v[u] = i < count ? partial[i] : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) key = v[u] > key ? v[u] : key;
+    }
     for (int o = 32; o > 0; o >>= 1) {
         unsigned long long other = __shfl_xor(key, o, 64);
         key = other > key ? other : key;
@@ -1566,13 +1600,15 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int
 // 0 clears the status that the output check sets afterwards.
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void swiglu_kernel(const float *gu, int64_t m, int64_t inter, float *h,
-                                                     int32_t *status) {
+                                                     int32_t *status, int interleaved8) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (status && i == 0) *status = NNQ_OK;
     if (i >= m * inter) return;
     const int64_t t = i / inter, c = i % inter;
-    const float g = gu[t * 2 * inter + c];
-    h[i] = g / (1.0f + expf(-g)) * gu[t * 2 * inter + inter + c];
+    // gate column and its up column: halves [gate | up], or 8 gate then 8 up per 16
+    const int64_t gc = interleaved8 ? (c / 8) * 16 + c % 8 : c, uc = interleaved8 ? gc + 8 : inter + c;
+    const float g = gu[t * 2 * inter + gc];
+    h[i] = g / (1.0f + expf(-g)) * gu[t * 2 * inter + uc];
 }
 
 // check_output_finite (crates/nn-core/src/layers/nan_check.rs:113-140) on the device:
@@ -1586,10 +1622,11 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(const void *y, int y_bf1
     if (__any(bad) && (threadIdx.x & 63) == 0) *status = NNQ_ERR_NON_FINITE;
 }
 
-int launch_swiglu(const float *gu, int64_t m, int64_t inter, float *h, int32_t *status, void *stream) {
+int launch_swiglu(const float *gu, int64_t m, int64_t inter, float *h, int32_t *status, void *stream,
+                  int interleaved8) {
     const int64_t n = m * inter;
     hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, gu, m,
-                       inter, h, status);
+                       inter, h, status, interleaved8);
     return (int)hipGetLastError();
 }
 

@@ -74,6 +74,8 @@ struct GemvArgs {
     float *logits_out;    // optional copy (argmax fusion)
     unsigned long long *argmax_partial;  // optional per-tile (orderable value, index) keys
     int x_swiglu;         // x is f32 [m, 2k] (gate | up); the GEMV input is silu(gate) * up (m <= 2)
+    int swiglu_out;       // Q4_K, m <= 2: rows come as 8 gate rows then the 8 matching up rows per
+                          //   16-row tile; y [m, n / 2] gets silu(gate) * up (no bias, no argmax)
     int32_t *status;      // optional: status_mode 1 stores NNQ_OK (one thread), 2 stores
     int status_mode;      //   NNQ_ERR_NON_FINITE when an output is NaN or infinite
 };
@@ -85,9 +87,11 @@ int launch_argmax_reduce(const float *v, int64_t n, uint32_t *idx, int32_t *stat
                          size_t scratch_bytes, void *stream);
 int launch_argmax_final(const unsigned long long *partial, int64_t count, uint32_t *idx, int32_t *status,
                         void *stream);
-// MLP glue: h = silu(gate) * up from gu [m, 2 * inter] (clears *status when given), and
-// the non-finite output check (sets *status to NNQ_ERR_NON_FINITE)
-int launch_swiglu(const float *gu, int64_t m, int64_t inter, float *h, int32_t *status, void *stream);
+// MLP glue: h = silu(gate) * up from gu [m, 2 * inter] (gate | up halves, or with
+// interleaved8 the 8-gate-rows / 8-up-rows order of each 16 columns; clears *status when
+// given), and the non-finite output check (sets *status to NNQ_ERR_NON_FINITE)
+int launch_swiglu(const float *gu, int64_t m, int64_t inter, float *h, int32_t *status, void *stream,
+                  int interleaved8 = 0);
 int launch_nonfinite_check(const void *y, int y_bf16, int64_t count, int32_t *status, void *stream);
 
 // Token sampling over device logits[n] (k = min(top_k, n), 0: none): scratch bytes, whether
