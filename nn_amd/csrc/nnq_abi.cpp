@@ -441,9 +441,11 @@ int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const floa
     a.ntile = L.ntile;
     a.nblk = L.nblk;
     a.argmax_partial = (unsigned long long *)s.p;
+    int64_t nkeys = L.ntile;  // the launch lowers it when it writes one key per workgroup
+    a.argmax_count = &nkeys;
     int e = launch_gemv(L.fmt, a, stream);
     if (e) return hip_fail((hipError_t)e, "gemv launch");
-    e = launch_argmax_final(a.argmax_partial, L.ntile, idx, status_dev, stream);
+    e = launch_argmax_final(a.argmax_partial, nkeys, idx, status_dev, stream);
     if (e) return hip_fail((hipError_t)e, "argmax launch");
     return NNQ_OK;
 }

@@ -737,6 +737,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(GemvArgs a) {
     __syncthreads();
 
     int par = 0;
+    uint64_t run_key = 0;  // thread 0: the largest argmax key of this workgroup's tiles
     const int g = lane >> 4, n = lane & 15;
     auto body = [&](Unit (&cur)[UPW], Unit (&nxt)[UPW]) {
         const int64_t next = tile + step;
@@ -790,7 +791,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(GemvArgs a) {
                     uint64_t other = __shfl_xor(key, o, 16);
                     key = other > key ? other : key;
                 }
-                if (nn == 0) a.argmax_partial[tile] = key;
+                if (nn == 0) run_key = key > run_key ? key : run_key;
             }
         }
         par ^= 1;
@@ -802,6 +803,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(GemvArgs a) {
         body(w1, w0);
         if (tile >= ntile) break;
     }
+    // one argmax key per workgroup (the host reduces gridDim.x keys)
+    if (a.argmax_partial && tid == 0) a.argmax_partial[blockIdx.x] = run_key;
     __builtin_amdgcn_s_waitcnt(0);  // the last (unused) prefetch
 }
 
@@ -924,6 +927,7 @@ __global__ __launch_bounds__(1024) void gemv_q6k_stream_kernel(GemvArgs a) {
     }
 
     int par = 0;
+    uint64_t run_key = 0;  // thread 0: the largest argmax key of this workgroup's tiles
     auto body = [&](W &cur, W &nxt) {
         const int64_t next = tile + step;
         if (has) load(next < ntile ? next : ntile - 1, nxt);
@@ -991,7 +995,7 @@ __global__ __launch_bounds__(1024) void gemv_q6k_stream_kernel(GemvArgs a) {
                     uint64_t other = __shfl_xor(key, o, 16);
                     key = other > key ? other : key;
                 }
-                if (nn == 0) a.argmax_partial[tile] = key;
+                if (nn == 0) run_key = key > run_key ? key : run_key;
             }
         }
         par ^= 1;
@@ -1003,6 +1007,8 @@ __global__ __launch_bounds__(1024) void gemv_q6k_stream_kernel(GemvArgs a) {
         body(w1, w0);
         if (tile >= ntile) break;
     }
+    // one argmax key per workgroup (the host reduces gridDim.x keys)
+    if (a.argmax_partial && tid == 0) a.argmax_partial[blockIdx.x] = run_key;
     __builtin_amdgcn_s_waitcnt(0);  // the last (unused) prefetch
 }
 
@@ -1348,6 +1354,7 @@ __global__ __launch_bounds__(1024) void gemv_q4k_stream_kernel(GemvArgs a) {
     const uint32_t hsel = 0u - (uint32_t)(G >> 1);  // all ones for sub-blocks 4..7
 
     int par = 0;
+    uint64_t run_key = 0;  // thread 0: the largest argmax key of this workgroup's tiles
     auto body = [&](W &cur, W &nxt) {
         const int64_t next = tile + step;
         if (has) load(next < ntile ? next : ntile - 1, nxt);
@@ -1415,7 +1422,7 @@ __global__ __launch_bounds__(1024) void gemv_q4k_stream_kernel(GemvArgs a) {
                     uint64_t other = __shfl_xor(key, o, 16);
                     key = other > key ? other : key;
                 }
-                if (nn == 0) a.argmax_partial[tile] = key;
+                if (nn == 0) run_key = key > run_key ? key : run_key;
             }
         }
         par ^= 1;
@@ -1427,6 +1434,8 @@ __global__ __launch_bounds__(1024) void gemv_q4k_stream_kernel(GemvArgs a) {
         body(w1, w0);
         if (tile >= ntile) break;
     }
+    // one argmax key per workgroup (the host reduces gridDim.x keys)
+    if (a.argmax_partial && tid == 0) a.argmax_partial[blockIdx.x] = run_key;
     __builtin_amdgcn_s_waitcnt(0);  // the last (unused) prefetch
 }
 
@@ -1719,6 +1728,7 @@ static int launch_stream_t(const GemvArgs &a, int64_t units, int cus, void *stre
     const int64_t kc = units * 256;
     const size_t lds = (size_t)a.m * kc * 4 + (size_t)a.m * (kc / GRAN) * 4 + (size_t)a.m * (kc / 32) * 4;
     const int64_t grid = a.ntile < cus ? a.ntile : cus;
+    if (a.argmax_count) *a.argmax_count = grid;
     hipLaunchKernelGGL((gemv_stream_kernel<FMT, WAVES, UPW>), dim3((unsigned)grid), dim3(WAVES * 64), lds,
                        (hipStream_t)stream, a);
     return (int)hipGetLastError();
@@ -1735,6 +1745,7 @@ static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
                 const int64_t kc = units * 256;
                 const size_t lds = (size_t)a.m * kc * 4 + (size_t)a.m * (kc / 16) * 4 + (size_t)a.m * (kc / 32) * 4;
                 const int64_t grid = a.ntile < cus ? a.ntile : cus;
+                if (a.argmax_count) *a.argmax_count = grid;
                 if (a.m == 1)
                     hipLaunchKernelGGL((gemv_q6k_stream_kernel<1>), dim3((unsigned)grid), dim3(1024), lds,
                                        (hipStream_t)stream, a);
@@ -1794,6 +1805,7 @@ static int launch_q4k_decode(const GemvArgs &a, void *stream) {
         const int cus = device_cus();
         if (a.ntile >= 4 * (int64_t)cus) {
             const dim3 grid((unsigned)(a.ntile < cus ? a.ntile : cus));
+            if (a.argmax_count) *a.argmax_count = grid.x;
             if (a.m == 1) {
                 if (a.x_bf16)
                     hipLaunchKernelGGL((gemv_q4k_stream_kernel<1, true>), grid, dim3(1024), 0, (hipStream_t)stream, a);

@@ -73,6 +73,8 @@ struct GemvArgs {
     int kc;               // K elements staged in LDS per chunk (multiple of 256)
     float *logits_out;    // optional copy (argmax fusion)
     unsigned long long *argmax_partial;  // optional per-tile (orderable value, index) keys
+    int64_t *argmax_count;  // with argmax_partial: the launch stores how many keys it writes
+                            //   (one per tile, or one per workgroup of a streaming kernel)
     int x_swiglu;         // x is f32 [m, 2k] (gate | up); the GEMV input is silu(gate) * up (m <= 2)
     int swiglu_out;       // Q4_K, m <= 2: rows come as 8 gate rows then the 8 matching up rows per
                           //   16-row tile; y [m, n / 2] gets silu(gate) * up (no bias, no argmax)
