@@ -142,7 +142,7 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 __global__ __launch_bounds__(256) void moe_route_kernel(const float *logits, int nsplit, const float *bias, int64_t T,
                                                         int E, int k, uint32_t *ti, float *tw, uint32_t *ti_out,
                                                         float *tw_out) {
-    __shared__ float ex[4][256];
+    __shared__ __attribute__((aligned(16))) float ex[4][256];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int64_t t = (int64_t)blockIdx.x * 4 + wv;
     if (t >= T) return;  // wave-uniform; no barrier below
@@ -185,8 +185,15 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *logits, int
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // the index-order sum, the same in every lane: 16-byte broadcast reads (ex rows
+        // are 16-byte aligned and 256 long), additions one after another
         float sum = -0.0f;
-        for (int c = 0; c < E; c++) sum = sum + ex[wv][c];
+        for (int c = 0; c < E; c += 4) {
+            const floatx4 q = *reinterpret_cast<const floatx4 *>(&ex[wv][c]);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (c + j < E) sum = sum + q[j];
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++) p[j] = p[j] / sum;
     }
@@ -273,31 +280,53 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, i
             if (lane == 0) wcnt[wv][e] = __popcll(m);
         }
         __syncthreads();
+        // per expert (one per thread): wcnt[w][e] becomes the count of earlier tokens,
+        // base[e] plus the waves before w (the 16 loads independent of each other)
+        for (int e = tid; e < E; e += 1024) {
+            int32_t c[16];
+#pragma unroll
+            for (int w = 0; w < 16; w++) c[w] = wcnt[w][e];
+            int32_t run = base[e];
+#pragma unroll
+            for (int w = 0; w < 16; w++) {
+                wcnt[w][e] = run;
+                run += c[w];
+            }
+            base[e] = run;
+        }
+        __syncthreads();
         if (t < T)
 #pragma unroll
-            for (int s = 0; s < k; s++) {
-                const uint32_t e = ex[s];
-                int32_t r = base[e] + rk[s];
-                for (int w = 0; w < wv; w++) r += wcnt[w][e];
-                pos[t * k + s] = r;  // rank within the expert; the offset is added below
-            }
-        __syncthreads();
-        for (int e = tid; e < E; e += 1024) {
-            int32_t c = 0;
-            for (int w = 0; w < 16; w++) c += wcnt[w][e];
-            base[e] += c;
-        }
-        __syncthreads();
+            for (int s = 0; s < k; s++)
+                pos[t * k + s] = wcnt[wv][ex[s]] + rk[s];  // rank within the expert; offset below
+        __syncthreads();  // wcnt is rewritten by the next chunk
     }
-    if (tid == 0) {
-        int32_t acc = 0;
-        for (int e = 0; e < E; e++) {
-            const int32_t c = base[e];
-            base[e] = acc;
-            off[e] = acc;
-            acc += c;
+    if (tid < 64) {
+        // exclusive scan of the expert counts: lane l holds experts 4l .. 4l + 3 (E <= 256)
+        int32_t c[4], sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = 4 * tid + j;
+            c[j] = e < E ? base[e] : 0;
+            sum += c[j];
         }
-        off[E] = acc;
+        int32_t before = sum;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t v = __shfl_up(before, o, 64);
+            if (tid >= o) before += v;
+        }
+        if (tid == 63) off[E] = before;  // the total
+        before -= sum;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = 4 * tid + j;
+            if (e < E) {
+                base[e] = before;
+                off[e] = before;
+            }
+            before += c[j];
+        }
     }
     __syncthreads();
     for (int64_t i = tid; i < T * k; i += 1024) {
