@@ -290,3 +290,32 @@ def test_argmax_semantics(dev):
     v[5] = float("nan")
     with pytest.raises(nn_amd.NonFiniteData):
         nn_amd.argmax(v)
+
+
+def test_lm_head_argmax_graph_replay(O, dev):
+    """The streaming LM head (one argmax key per workgroup, then argmax_final_kernel)
+    captured into a HIP graph: every replay, and eager calls with another input between
+    the replays, give the oracle's index."""
+    import nn_amd
+    n, k = 32768, 1024
+    b = quantized_weight_bytes("q6_k", n, k, seed=41, O=O)
+    w = make_weight("q6_k", b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(41, 2, (k,), 1.0)).to(dev)
+    ref = O.argmax(oracle_linear(O, "q6_k", b, n, k, x.cpu().numpy())[0])
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            logits, idx = nn_amd.linear_argmax(x, w, check=False)  # no host read under capture
+    torch.cuda.current_stream().wait_stream(s)
+    x2 = torch.from_numpy(nn_amd.synth_normal(42, 2, (k,), 1.0)).to(dev)
+    ref2 = O.argmax(oracle_linear(O, "q6_k", b, n, k, x2.cpu().numpy())[0])
+    assert ref2 != ref
+    for i in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(idx) == ref, f"replay {i}"
+        _, i2 = nn_amd.linear_argmax(x2, w)  # eager, between the replays
+        torch.cuda.synchronize()
+        assert int(i2) == ref2, f"eager after replay {i}"
