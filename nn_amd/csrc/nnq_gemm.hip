@@ -16,7 +16,7 @@
 // Activation staging (gemm_prep_kernel, once per call): each row of x is scaled by a
 // power of two so that max|x| lands in [2^14, 2^15) and converted to f16 (bf16 input
 // converts exactly; f32 input is split into hi + lo planes, K-stacked in the MFMA),
-// and its 32-element sums are stored as f16 hi + lo of sum * 2^-8.
+// and its 32-element sums are stored negated, as f16 hi + lo of -sum * 2^-8.
 //
 // Tiling.  A workgroup computes a BM x BN output tile with WGM x WGN waves (wave tile
 // WM x WN of 16x16 MFMA tiles).  K advances one super-block (256 k) per stage: the
@@ -172,8 +172,9 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *x, int x_bf1
         if ((g & 3) == 0) {
             uint32_t th, tl;
             split_f16(tot * 0.00390625f, th, tl);  // 2^-8 keeps 32 * 2^15 inside f16
-            sc.xs[row * nsub + g / 4] = (uint16_t)th;
-            sc.xs[m * nsub + row * nsub + g / 4] = (uint16_t)tl;
+            // stored negated (sign bits flipped, exact): the min term is subtracted
+            sc.xs[row * nsub + g / 4] = (uint16_t)(th ^ 0x8000u);
+            sc.xs[m * nsub + row * nsub + g / 4] = (uint16_t)(tl ^ 0x8000u);
         }
     };
     if (NG > 0) {
@@ -387,9 +388,9 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_q4k_kernel(GemmArgs a, Gem
             const int64_t row = m0 + wm * C::WM + mt * 16 + l16;
             ah[mt] = al[mt] = u32x4{0u, 0u, 0u, 0u};
             if (kin && row < M) {
-                // negated: the min term is subtracted
-                ah[mt] = *reinterpret_cast<const u32x4 *>(sc.xs + row * nsub + jg0 + 8 * p) ^ 0x80008000u;
-                al[mt] = *reinterpret_cast<const u32x4 *>(sc.xs + M * nsub + row * nsub + jg0 + 8 * p) ^ 0x80008000u;
+                // the sums are staged negated: the min term is subtracted
+                ah[mt] = *reinterpret_cast<const u32x4 *>(sc.xs + row * nsub + jg0 + 8 * p);
+                al[mt] = *reinterpret_cast<const u32x4 *>(sc.xs + M * nsub + row * nsub + jg0 + 8 * p);
             }
         }
 #pragma unroll

@@ -295,12 +295,11 @@ __global__ __launch_bounds__(256) void gemm_q4k_rk_kernel(GemmArgs a, GemmScratc
             if (p == 2) {
                 // min term of the super-block: one MFMA per tile whose 32 k are the four
                 // (x hi / lo) x (w hi / lo) cross products of its 8 sub-blocks: lane group G
-                // takes x part G & 1 (negated: the min term is subtracted) and w part G >> 1
+                // takes x part G & 1 (staged negated: the min term is subtracted) and w part G >> 1
                 u32x4 xa[MT], wb[NT];
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++)
-                    xa[mt] = *reinterpret_cast<const u32x4 *>(area + C::XS_OFF + (size_t)(arow[mt] * 2 + (G & 1)) * 16) ^
-                             0x80008000u;
+                    xa[mt] = *reinterpret_cast<const u32x4 *>(area + C::XS_OFF + (size_t)(arow[mt] * 2 + (G & 1)) * 16);
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
                     wb[nt] = *reinterpret_cast<const u32x4 *>(
