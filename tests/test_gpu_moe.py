@@ -93,6 +93,32 @@ def test_moe_small_vs_oracle(O, dev, E, H, I, T, k, xdt):
     check_close(ref, y.cpu().numpy(), f"moe E={E} H={H} I={I} T={T} k={k} x={xdt}")
 
 
+# Uneven loads: a large logit on expert 0 sends every token there (more than 64 rows:
+# several passes of the expert kernel over its token rows, the last one partial), and a
+# single decode token (one row per expert used).
+@pytest.mark.parametrize("E,H,I,T,k,xdt,skew", [(8, 256, 320, 200, 2, "bf16", True), (4, 96, 96, 130, 1, "f32", True),
+                                               (8, 256, 320, 1, 4, "f32", False), (32, 96, 64, 1, 4, "bf16", False)])
+def test_moe_uneven_loads_vs_oracle(O, dev, E, H, I, T, k, xdt, skew):
+    import nn_amd
+    L = make_layer(E, H, I, seed=E * 11 + T)
+    moe = upload(L, E, H, I)
+    x = torch.from_numpy(nn_amd.synth_normal(13, 5, (T, H), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    lg = nn_amd.synth_normal(13, 6, (T, E), 1.0)
+    if skew:
+        lg[:, 0] += 12.0
+    logits = torch.from_numpy(lg).to(dev)
+    y, ti, tw = moe.forward(x, logits, top_k=k, return_routing=True)
+    ref, rti, rtw = O.moe_forward(x.float().cpu().numpy(), lg, k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    counts = np.bincount(rti.ravel(), minlength=E)
+    if skew:
+        assert counts[0] == T and T > 64, "every token routed to expert 0, more than one 64-row pass"
+    assert np.array_equal(ti.cpu().numpy().astype(np.uint32), rti), "routing differs"
+    assert np.allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    check_close(ref, y.cpu().numpy(), f"moe uneven E={E} H={H} I={I} T={T} k={k} x={xdt} skew={skew}")
+
+
 def test_moe_expert_dequant_bit_exact(O, dev):
     E, H, I = 3, 96, 64
     L = make_layer(E, H, I, seed=5)
