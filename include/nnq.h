@@ -156,7 +156,8 @@ int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const floa
  * The Option fields become flags: top_k < 0 is None, use_top_p = 0 is None. */
 typedef struct nnq_sampling {
     float temperature;        /* > 0 and finite */
-    int32_t top_k;            /* < 0: None (keep all finite logits); 0: no candidate (argmax fallback) */
+    int32_t top_k;            /* < 0: None (every logit > -inf, +inf included, is a candidate);
+                                 0: no candidate (argmax fallback); >= n: the finite logits */
     int32_t use_top_p;        /* 0: top_p is None */
     float top_p;
     float repetition_penalty; /* 1.0: none */

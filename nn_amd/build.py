@@ -27,6 +27,9 @@ HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_moe.hip
 # per-file device flags (none at present)
 EXTRA_FLAGS = {}
 HOST_SOURCES = ["nnq_abi.cpp", "nnq_repack.cpp", "nnq_host.cpp", "nnq_gguf.cpp"]
+# measurement probes for bench.py (streaming-read floor, empty launch), a library of their own
+PROBE_SOURCES = ["nnq_probe.hip"]
+PROBE_LIB = os.path.join(HERE, "libnnq_probe.so")
 
 
 def _run(cmd):
@@ -55,12 +58,14 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     os.makedirs(BUILD, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(_compile, HIP_SOURCES + HOST_SOURCES))
-    tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread"])
-    os.replace(tmp, LIB)
-    if verbose:
-        print(f"built {LIB}")
+        objs = list(ex.map(_compile, HIP_SOURCES + HOST_SOURCES + PROBE_SOURCES))
+    nlib = len(HIP_SOURCES) + len(HOST_SOURCES)
+    for out, parts in ((LIB, objs[:nlib]), (PROBE_LIB, objs[nlib:])):
+        tmp = out + ".tmp"
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *parts, "-lpthread"])
+        os.replace(tmp, out)
+        if verbose:
+            print(f"built {out}")
     return LIB
 
 

@@ -313,7 +313,8 @@ static int check_linear(const nnq_weight *w, const void *x, nnq_dtype xd, int64_
     if (m > 0 && (!x || !y)) return fail(NNQ_ERR_INVALID_ARGUMENT, "x or y is null");
     if (xd != NNQ_F32 && xd != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d (f32 or bf16)", (int)xd);
     if (yd != NNQ_F32 && yd != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "output dtype %d (f32 or bf16)", (int)yd);
-    if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(NNQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if ((uintptr_t)x & 15) return fail(NNQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if ((uintptr_t)y & 3) return fail(NNQ_ERR_INVALID_ARGUMENT, "y must be 4-byte aligned");
     return NNQ_OK;
 }
 
@@ -751,7 +752,7 @@ static int run_sample(const float *logits, int64_t n, const uint32_t *past, int6
     // sample_token's conditions for applying the penalties (sampling.rs:155-162)
     const int rep_on = std::fabs(cfg->repetition_penalty - 1.0f) > 1.1920929e-7f;
     const int freq_on = std::fabs(cfg->frequency_penalty) > 1.1920929e-7f;
-    int e = launch_sample(logits, n, past, n_past, cfg->temperature, k, cfg->use_top_p != 0, cfg->top_p,
+    int e = launch_sample(logits, n, past, n_past, cfg->temperature, k, cfg->top_k < 0, cfg->use_top_p != 0, cfg->top_p,
                           cfg->repetition_penalty, rep_on, cfg->frequency_penalty, freq_on, cfg->seed, token, s.p,
                           stream);
     if (e) return hip_fail((hipError_t)e, "sample launch");

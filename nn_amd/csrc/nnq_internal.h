@@ -100,9 +100,10 @@ int launch_nonfinite_check(const void *y, int y_bf16, int64_t count, int32_t *st
 // the shape fits the two-pass top-k (ceil(n / 2048) * min(k, 2048) <= 16384), and the launch
 size_t sample_scratch_bytes(int64_t n, int64_t k);
 bool sample_supported(int64_t n, int64_t k);
+// keep_inf: top_k is None, so +inf logits are candidates too (k = n)
 int launch_sample(const float *logits, int64_t n, const uint32_t *past, int64_t n_past, float temperature, int64_t k,
-                  int use_top_p, float top_p, float rep, int rep_on, float freq, int freq_on, uint64_t seed,
-                  uint32_t *token, void *scratch, void *stream);
+                  int keep_inf, int use_top_p, float top_p, float rep, int rep_on, float freq, int freq_on,
+                  uint64_t seed, uint32_t *token, void *scratch, void *stream);
 
 // GEMM (prefill) for Q4_K: x bf16/f32 [m, k] -> y [m, n].  `scratch` holds the
 // staged activation and split-K partials (gemm_scratch_bytes(args) bytes, 256-byte

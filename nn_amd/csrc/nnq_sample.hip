@@ -46,6 +46,13 @@ __device__ __forceinline__ uint64_t cand_key(float v, uint32_t idx) {
 __device__ __forceinline__ uint32_t key_idx(uint64_t k) { return 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull); }
 __device__ __forceinline__ float key_val(uint64_t k) { return unord_f32((uint32_t)(k >> 32)); }
 __device__ __forceinline__ bool key_finite(uint64_t k) { return (k >> 32) != 0 && fabsf(key_val(k)) <= 3.402823466e38f; }
+// ord(+inf): the largest orderable value
+constexpr uint32_t kOrdPosInf = 0xFF800000u;
+// a candidate of the tail: finite, or also +inf when top_k is None (sampling.rs:160-164
+// keeps every v > -inf there; apply_top_k keeps finite values only)
+__device__ __forceinline__ bool key_cand(uint64_t k, bool keep_inf) {
+    return key_finite(k) || (keep_inf && (uint32_t)(k >> 32) == kOrdPosInf);
+}
 
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -163,7 +170,8 @@ __device__ void sort_desc_lds(uint64_t *a, int n) {
 struct SampleParams {
     float temperature, top_p, rep, freq;
     int rep_on, freq_on, use_top_p;
-    int64_t k;  // candidates kept by top-k (already min(top_k, n); 0: none)
+    int keep_inf;  // top_k None: +inf logits are candidates too
+    int64_t k;     // candidates kept by top-k (already min(top_k, n); 0: none)
     uint64_t seed;
 };
 
@@ -310,12 +318,12 @@ __global__ __launch_bounds__(NTH) void sample_final_kernel(const float *logits, 
         sort_desc_lds(sel, Q);  // sel[0..k): the top k, descending (ties: lower index first)
         if (!sp.use_top_p && k > 1) {
             // without top-p the reference walks the candidates in index order: re-sort by
-            // (finite first, ascending index), carrying each one's position (< 2^14)
+            // (candidates first, ascending index), carrying each one's position (< 2^14)
             for (int j = tid; j < k; j += NTH) val[j] = key_val(sel[j]);
             __syncthreads();
             for (int j = tid; j < Q; j += NTH) {
                 uint64_t r = 0;
-                if (j < k && key_finite(sel[j]))
+                if (j < k && key_cand(sel[j], sp.keep_inf != 0))
                     r = 0x8000000000000000ull | ((uint64_t)(0xFFFFFFFFu - key_idx(sel[j])) << 14) | (uint64_t)j;
                 sel[j] = r;
             }
@@ -334,16 +342,17 @@ __global__ __launch_bounds__(NTH) void sample_final_kernel(const float *logits, 
                 wave_sync();
                 for (int j = tid; j < k; j += 64) val[j] = prob[j];
                 for (int o = 32; o > 0; o >>= 1) f += __shfl_xor(f, o, 64);
-                nc = f;  // the finite ones come first
+                nc = f;  // the candidates come first
             }
         } else if (tid < 64) {
             // descending order: +inf keys first, then the finite ones, then -inf and NaN;
-            // the finite ones move to the front in order
+            // the candidates move to the front in order (the +inf keys are candidates, and
+            // stay in front, only when top_k is None)
             int f = 0, a = 0;
             for (int j = tid; j < k; j += 64) {
                 const uint64_t s = sel[j];
-                f += key_finite(s) ? 1 : 0;
-                a += ((s >> 32) == 0xFF800000u) ? 1 : 0;  // ord(+inf)
+                f += key_cand(s, sp.keep_inf != 0) ? 1 : 0;
+                a += (!sp.keep_inf && (uint32_t)(s >> 32) == kOrdPosInf) ? 1 : 0;
             }
             for (int o = 32; o > 0; o >>= 1) {
                 f += __shfl_xor(f, o, 64);
@@ -351,7 +360,7 @@ __global__ __launch_bounds__(NTH) void sample_final_kernel(const float *logits, 
             }
             for (int j = tid; j < k; j += 64) {
                 const uint64_t s = sel[j];
-                if (key_finite(s)) {
+                if (key_cand(s, sp.keep_inf != 0)) {
                     val[j - a] = key_val(s);
                     idx[j - a] = key_idx(s);
                 }
@@ -411,9 +420,10 @@ bool sample_supported(int64_t n, int64_t k) {
 }
 
 int launch_sample(const float *logits, int64_t n, const uint32_t *past, int64_t n_past, float temperature, int64_t k,
-                  int use_top_p, float top_p, float rep, int rep_on, float freq, int freq_on, uint64_t seed,
-                  uint32_t *token, void *scratch, void *stream) {
+                  int keep_inf, int use_top_p, float top_p, float rep, int rep_on, float freq, int freq_on,
+                  uint64_t seed, uint32_t *token, void *scratch, void *stream) {
     SampleParams sp;
+    sp.keep_inf = keep_inf;
     sp.temperature = temperature;
     sp.top_p = top_p;
     sp.rep = rep;

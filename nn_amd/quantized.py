@@ -161,6 +161,22 @@ def _ptr(t: Optional[torch.Tensor]):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
 
 
+def _device_input(t: torch.Tensor, what: str, device: Optional[int] = None) -> torch.Tensor:
+    """Reject a tensor the kernels cannot read: the C ABI takes device pointers and
+    cannot tell a host address from a device one, so a CPU tensor (or one on another
+    device than the weights') is refused here, before any launch."""
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise Unsupported(f"{what} must be a device tensor")
+    if device is not None and t.device.index != device:
+        raise Unsupported(f"{what} is on cuda:{t.device.index}, the weights on cuda:{device}")
+    return t
+
+
+def _side_input(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    """A secondary operand (bias, router logits) as contiguous f32 on the device of `like`."""
+    return t.to(device=like.device, dtype=torch.float32).contiguous()
+
+
 def _as_u8(data) -> np.ndarray:
     if isinstance(data, (bytes, bytearray, memoryview)):
         return np.frombuffer(bytes(data), dtype=np.uint8)
@@ -237,15 +253,14 @@ class QuantizedWeight:
         return out
 
 
-def _validate_input(input: torch.Tensor, in_features: int):
+def _validate_input(input: torch.Tensor, in_features: int, device: Optional[int] = None):
     """validate_input (quantized_matmul.rs:121-145)."""
     if input.dim() < 2:
         raise RankMismatch(f"expected rank >= 2, got {input.dim()}")
     k = input.shape[-1]
     if k != in_features:
         raise ShapeMismatch(f"quantized matmul shape mismatch: input last dim {k} != weight in_features {in_features}")
-    if not input.is_cuda:
-        raise Unsupported("input must be a device tensor")
+    _device_input(input, "input", device)
     if input.dtype not in (torch.float32, torch.bfloat16):
         input = input.float()
     return input.contiguous()
@@ -261,11 +276,11 @@ def quantized_linear(input: torch.Tensor, weight: QuantizedWeight, bias: Optiona
     if not isinstance(weight, QuantizedWeight):
         raise NotQuantized("quantized_linear: weight is not quantized")
     n, k = weight.shape
-    x = _validate_input(input, k)
+    x = _validate_input(input, k, weight.device)
     if bias is not None:
         if bias.dim() != 1 or bias.shape[0] != n:
             raise BiasMismatch(f"bias shape mismatch: expected [{n}], got {list(bias.shape)}")
-        bias = bias.to(device=x.device, dtype=torch.float32).contiguous()
+        bias = _side_input(bias, x)
     out_dtype = out_dtype or torch.float32
     y = torch.empty(tuple(x.shape[:-1]) + (n,), dtype=out_dtype, device=x.device)
     m = x.numel() // k
@@ -298,7 +313,7 @@ def argmax(logits: torch.Tensor) -> torch.Tensor:
         raise Unsupported("argmax: 1-D input expected")
     if logits.numel() == 0:
         raise InvalidShape("argmax over a zero-length dimension")
-    v = logits.float().contiguous()
+    v = _device_input(logits, "logits").float().contiguous()
     idx = torch.empty(1, dtype=torch.int32, device=v.device)
     st = torch.zeros(1, dtype=torch.int32, device=v.device)
     _check(_lib.load().nnq_argmax_f32(_ptr(v), v.numel(), _ptr(idx), _ptr(st), _stream(v)))
@@ -311,13 +326,13 @@ def linear_argmax(x: torch.Tensor, weight: QuantizedWeight, bias: Optional[torch
                   check: bool = True):
     """LM head: logits = x @ W^T (+bias) and their first-index argmax, fused."""
     n, k = weight.shape
-    xv = x.reshape(-1).float().contiguous()
+    xv = _device_input(x, "x", weight.device).reshape(-1).float().contiguous()
     if xv.numel() != k:
         raise ShapeMismatch(f"input has {xv.numel()} elements, weight in_features {k}")
     if bias is not None:
         if bias.dim() != 1 or bias.shape[0] != n:
             raise BiasMismatch(f"bias shape mismatch: expected [{n}], got {list(bias.shape)}")
-        bias = bias.float().contiguous()
+        bias = _side_input(bias, xv)
     logits = torch.empty(n, dtype=torch.float32, device=xv.device)
     idx = torch.empty(1, dtype=torch.int32, device=xv.device)
     st = torch.zeros(1, dtype=torch.int32, device=xv.device)
@@ -354,7 +369,7 @@ def sample_token(logits: torch.Tensor, temperature: float = 0.7, top_k: Optional
                  past_tokens=None, seed: int = 0) -> torch.Tensor:
     """sample_token (sampling.rs:136-185) over a 1-D device f32 logits tensor; returns the
     token as a device int64 scalar tensor (no host synchronisation)."""
-    v = logits.reshape(-1).float().contiguous()
+    v = _device_input(logits, "logits").reshape(-1).float().contiguous()
     if v.numel() == 0:
         raise InvalidShape("logits must be non-empty")
     past, n_past = _past(past_tokens, v.device)
@@ -370,13 +385,13 @@ def linear_sample(x: torch.Tensor, weight: QuantizedWeight, bias: Optional[torch
                   repetition_penalty: float = 1.0, frequency_penalty: float = 0.0, past_tokens=None, seed: int = 0):
     """LM head + sampling: logits = x @ W^T (+bias), then sample_token on the device."""
     n, k = weight.shape
-    xv = x.reshape(-1).float().contiguous()
+    xv = _device_input(x, "x", weight.device).reshape(-1).float().contiguous()
     if xv.numel() != k:
         raise ShapeMismatch(f"input has {xv.numel()} elements, weight in_features {k}")
     if bias is not None:
         if bias.dim() != 1 or bias.shape[0] != n:
             raise BiasMismatch(f"bias shape mismatch: expected [{n}], got {list(bias.shape)}")
-        bias = bias.float().contiguous()
+        bias = _side_input(bias, xv)
     logits = torch.empty(n, dtype=torch.float32, device=xv.device)
     past, n_past = _past(past_tokens, xv.device)
     tok = torch.empty(1, dtype=torch.int32, device=xv.device)
@@ -428,7 +443,7 @@ class QuantizedMLP:
 
     def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None, check: bool = True) -> torch.Tensor:
         """down(silu(gate(x)) * up(x)) over the last dimension of x (Qwen3MLP::forward)."""
-        _validate_input(x, self.hidden)
+        _validate_input(x, self.hidden, self.device)
         xx = x if x.dtype in (torch.float32, torch.bfloat16) else x.float()
         xx = xx.reshape(-1, self.hidden).contiguous()
         m = xx.shape[0]
@@ -501,6 +516,7 @@ class QuantizedMoE:
                 setattr(self, name, None)
 
     def _input(self, x):
+        _device_input(x, "x", self.device)
         if x.dim() != 2 or x.shape[1] != self.hidden:
             raise ShapeMismatch(f"x must be [tokens, {self.hidden}]")
         return x.contiguous() if x.dtype in (torch.float32, torch.bfloat16) else x.float().contiguous()
@@ -548,7 +564,7 @@ class QuantizedMoE:
             raise ShapeMismatch(f"router logits must be [{T}, {self.num_experts}]")
         if top_k <= 0 or top_k > self.num_experts:
             raise InvalidShape(f"topk k={top_k} out of range for dim 1 (size {self.num_experts})")
-        lg = router_logits.float().contiguous()
+        lg = _side_input(router_logits, xx)
         y = torch.empty((T, self.hidden), dtype=torch.float32, device=xx.device)
         ti = torch.empty((T, top_k), dtype=torch.int32, device=xx.device) if return_routing else None
         tw = torch.empty((T, top_k), dtype=torch.float32, device=xx.device) if return_routing else None

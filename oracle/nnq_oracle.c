@@ -845,8 +845,10 @@ int orc_any_nonfinite(const float *v, size_t n) {
 /* Top-k ties: the reference sorts with sort_unstable_by, whose order among  */
 /* equal logits is unspecified; here equal values keep the lower index       */
 /* first (parity unpinned for exact ties at the k-th place).  NaN logits are */
-/* ordered below -inf for the selection and never become candidates (the     */
-/* reference keeps only finite candidates; its NaN sort order is unspecified).*/
+/* ordered below -inf for the selection and never become candidates.  With   */
+/* top_k Some(k) the candidates are the finite logits among the k largest    */
+/* (apply_top_k, :245-275); with top_k None every logit v > -inf is one,     */
+/* +inf included (:158-165), which makes softmax_candidates uniform.         */
 /* ------------------------------------------------------------------------ */
 
 typedef struct { uint32_t idx; float v; } orc_cand;
@@ -929,13 +931,18 @@ int orc_sample_token(const float *logits, size_t n, const uint32_t *past, size_t
     /* apply_temperature (:193-199) */
     for (size_t i = 0; i < n; i++)
         if (isfinite(s[i])) s[i] /= temperature;
-    /* apply_top_k (:245-275): the k largest, then candidates in index order, finite only */
     orc_cand *c = (orc_cand *)malloc(n * sizeof(orc_cand));
     size_t nc = 0;
-    if (top_k < 0 || (size_t)top_k >= n) {
+    if (top_k < 0) {
+        /* top_k None (:160-164): every v > -inf in index order; NaN compares false */
+        for (size_t i = 0; i < n; i++)
+            if (s[i] > -INFINITY) c[nc++] = (orc_cand){(uint32_t)i, s[i]};
+    } else if ((size_t)top_k >= n) {
+        /* apply_top_k with k >= len (:250-256): the finite logits in index order */
         for (size_t i = 0; i < n; i++)
             if (isfinite(s[i])) c[nc++] = (orc_cand){(uint32_t)i, s[i]};
     } else if (top_k > 0) {
+        /* apply_top_k (:258-275): the k largest, then the finite ones in index order */
         orc_cand *all = (orc_cand *)malloc(n * sizeof(orc_cand));
         for (size_t i = 0; i < n; i++) all[i] = (orc_cand){(uint32_t)i, s[i]};
         qsort(all, n, sizeof(orc_cand), cand_desc);

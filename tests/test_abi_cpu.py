@@ -115,3 +115,35 @@ def test_no_device_is_reported(lib):
     c = ctypes.c_int(-1)
     assert lib.nnq_device_count(ctypes.byref(c)) == 0 and c.value == 0
     assert lib.nnq_init(0) == _lib.ERR_NO_DEVICE
+
+
+def _fake_weight(n=16, k=256):
+    """A QuantizedWeight with a null handle: enough for the host-side checks, which
+    must reject the call before anything reaches the C ABI."""
+    import nn_amd
+    return nn_amd.QuantizedWeight(ctypes.c_void_p(), nn_amd.QuantType.Q4_K, nn_amd.Layout.GGUF, (n, k), 0)
+
+
+def test_host_tensors_are_refused_before_any_launch():
+    """The C ABI takes device pointers only and cannot tell a host address from a device
+    one, so every wrapper refuses a CPU input with Unsupported on the host."""
+    import torch
+
+    import nn_amd
+    w = _fake_weight()
+    x = torch.zeros(1, 256)
+    with pytest.raises(nn_amd.Unsupported):
+        nn_amd.quantized_linear(x, w)
+    with pytest.raises(nn_amd.Unsupported):
+        nn_amd.linear_argmax(x, w)
+    with pytest.raises(nn_amd.Unsupported):
+        nn_amd.linear_sample(x, w)
+    with pytest.raises(nn_amd.Unsupported):
+        nn_amd.argmax(torch.zeros(8))
+    with pytest.raises(nn_amd.Unsupported):
+        nn_amd.sample_token(torch.zeros(8))
+    moe = object.__new__(nn_amd.QuantizedMoE)
+    moe._h = moe._router = None
+    moe.num_experts, moe.hidden, moe.inter, moe.device = 4, 64, 64, 0
+    with pytest.raises(nn_amd.Unsupported):
+        moe.forward(torch.zeros(2, 64), torch.zeros(2, 4))

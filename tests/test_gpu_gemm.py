@@ -93,10 +93,11 @@ def test_gemm_bias_bf16_out_and_nan_row(O, dev):
     assert np.isnan(yn[5]).all() and np.isfinite(np.delete(yn, 5, axis=0)).all()
 
 
-@pytest.mark.parametrize("m,n,k", [(128, 4096, 4096), (512, 12288, 4096), (512, 4096, 12288), (16, 4096, 12288),
-                                   (64, 12288, 4096)])
+@pytest.mark.parametrize("m", [16, 64, 128, 512])
+@pytest.mark.parametrize("n,k", [(12288, 4096), (4096, 12288)])
 def test_gemm_baseline_shapes(O, dev, m, n, k):
-    """Config 4: Qwen3-8B MLP prefill shapes, bf16 activations, bf16 and f32 outputs."""
+    """Config 4: both Qwen3-8B MLP matrices at M = 16, 64, 128 (the GEMV-to-GEMM
+    crossover) and 512, bf16 activations, f32 and bf16 outputs."""
     import nn_amd
     wb = q4k_bytes(n, k, seed=4000 + k)
     w = make_weight("q4_k", wb, n, k)
@@ -110,7 +111,7 @@ def test_gemm_baseline_shapes(O, dev, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(130, 256, 4096), (256, 384, 2048), (128, 192, 256), (300, 640, 1280),
-                                   (384, 1024, 4096)])
+                                   (384, 1024, 4096), (128, 4096, 4096)])
 def test_gemm_ring_edges(O, dev, m, n, k):
     """The LDS-ring kernel's edges (bf16 activations, m >= 128): ragged last row tile,
     128- and 192-wide column tiles, a single super-block, K split 1, 2 and 4 ways, with

@@ -135,6 +135,25 @@ def test_linear_small(O, dev, fmt, n, k, m):
     check_close(ref, y, f"{fmt} n={n} k={k} m={m}")
 
 
+@pytest.mark.parametrize("k", [320, 2880, 4128])
+@pytest.mark.parametrize("m", [1, 2, 3, 8, 12])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_linear_q8_0_padded_blocks(O, dev, k, m, xdt):
+    """Q8_0 rows whose block count is not a multiple of 8 (10, 90 and 129 blocks): the
+    device layout pads each row to whole 8-block groups, which must add nothing.  2880
+    is GPT-OSS's hidden size; m = 12 runs an 8-token and a 4-token pass."""
+    import nn_amd
+    n = 80
+    b = quantized_weight_bytes("q8_0", n, k, seed=k + m, O=O)
+    w = make_weight("q8_0", b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(k + m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    y = nn_amd.quantized_linear(x, w).cpu().numpy()
+    ref = oracle_linear(O, "q8_0", b, n, k, x.float().cpu().numpy())
+    check_close(ref, y, f"q8_0 padded k={k} m={m} x={xdt}")
+
+
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k"])
 @pytest.mark.parametrize("n,k,m,xdt", [(16385, 1024, 1, "f32"), (16385, 4096, 2, "f32"), (20000, 2048, 2, "bf16"),
                                        (40000, 256, 1, "bf16")])
@@ -319,3 +338,25 @@ def test_lm_head_argmax_graph_replay(O, dev):
         _, i2 = nn_amd.linear_argmax(x2, w)  # eager, between the replays
         torch.cuda.synchronize()
         assert int(i2) == ref2, f"eager after replay {i}"
+
+
+def test_host_bias_moves_to_the_device(O, dev):
+    """A bias given as a CPU tensor is copied to the input's device (never handed to a
+    kernel as a host address): every entry point with a bias gives the same result as
+    with the bias already on the device."""
+    import nn_amd
+    n, k = 300, 1024
+    b = quantized_weight_bytes("q6_k", n, k, seed=91, O=O)
+    w = make_weight("q6_k", b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(91, 2, (1, k), 1.0)).to(dev)
+    bias_h = torch.from_numpy(nn_amd.synth_normal(91, 3, (n,), 0.5))
+    bias_d = bias_h.to(dev)
+    assert torch.equal(nn_amd.quantized_linear(x, w, bias_h), nn_amd.quantized_linear(x, w, bias_d))
+    lh, ih = nn_amd.linear_argmax(x, w, bias_h)
+    ld, idd = nn_amd.linear_argmax(x, w, bias_d)
+    assert torch.equal(lh, ld) and int(ih) == int(idd)
+    lh, th = nn_amd.linear_sample(x, w, bias_h, seed=5)
+    ld, td = nn_amd.linear_sample(x, w, bias_d, seed=5)
+    assert torch.equal(lh, ld) and int(th) == int(td)
+    ref = oracle_linear(O, "q6_k", b, n, k, x.cpu().numpy()) + bias_h.numpy()
+    check_close(ref, ld.cpu().numpy()[None, :], "q6_k linear + host bias")

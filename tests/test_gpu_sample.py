@@ -113,8 +113,8 @@ def test_lm_head_sample_q6k(O, dev):
 
 @pytest.mark.parametrize("top_p", [None, 0.9])
 def test_sample_infinite_logits(O, dev, top_p):
-    """+inf logits take top-k places but are not candidates (the reference keeps finite
-    candidates only); -inf and NaN sort last."""
+    """With top_k Some(k), +inf logits take top-k places but are not candidates
+    (apply_top_k keeps finite values, sampling.rs:245-275); -inf and NaN sort last."""
     import nn_amd
     n = 9000
     lg = nn_amd.synth_normal(21, 1, (n,), 1.0)
@@ -126,3 +126,31 @@ def test_sample_infinite_logits(O, dev, top_p):
         for k in (3, 10, 64):
             got = int(nn_amd.sample_token(t, temperature=1.0, top_k=k, top_p=top_p, seed=seed).item())
             assert got == O.sample_token(lg, temperature=1.0, top_k=k, top_p=top_p, seed=seed), (k, seed)
+
+
+@pytest.mark.parametrize("top_p", [None, 0.6, 0.999])
+@pytest.mark.parametrize("n", [5, 9000, 16384])
+def test_sample_top_k_none_pos_inf(O, dev, n, top_p):
+    """top_k None: every logit v > -inf is a candidate, +inf included (sampling.rs:158-165),
+    so a +inf logit makes the softmax uniform over all candidates (:371-391); the walk
+    runs in index order, or in descending order after the top-p cut."""
+    import nn_amd
+    if n == 5:
+        lg = np.array([0.0, np.inf, 1.0, 2.0, -np.inf], np.float32)
+    else:
+        lg = nn_amd.synth_normal(n + 7, 1, (n,), 1.5)
+        lg[[3, n // 2, n - 1]] = np.inf
+        lg[[4, 100]] = -np.inf
+        lg[[5, n - 2]] = np.nan
+    t = torch.from_numpy(lg).to(dev)
+    for seed in (0, 1, 2600, 5100, 7499, 9999):
+        got = int(nn_amd.sample_token(t, temperature=0.8, top_k=None, top_p=top_p, seed=seed).item())
+        assert got == O.sample_token(lg, temperature=0.8, top_k=None, top_p=top_p, seed=seed), (n, top_p, seed)
+    # without +inf, None keeps the finite logits: the ordinary softmax
+    if n > 5:
+        lg2 = lg.copy()
+        lg2[~np.isfinite(lg2)] = -1.0
+        t2 = torch.from_numpy(lg2).to(dev)
+        for seed in (11, 4321):
+            got = int(nn_amd.sample_token(t2, temperature=0.8, top_k=None, top_p=top_p, seed=seed).item())
+            assert got == O.sample_token(lg2, temperature=0.8, top_k=None, top_p=top_p, seed=seed), (n, top_p, seed)

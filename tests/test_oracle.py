@@ -624,3 +624,41 @@ def test_sample_token_selection_matches_softmax(O):
     cut = int(np.searchsorted(np.cumsum(q[order]), 0.8) + 1)
     picks = {O.sample_token(logits, temperature=T, top_k=None, top_p=0.8, seed=s) for s in range(0, 10000, 7)}
     assert picks == set(order[:cut].tolist())
+
+
+def test_sample_token_top_k_none_keeps_pos_inf(O):
+    """top_k None makes every logit v > -inf a candidate, +inf included
+    (sampling.rs:158-165); a +inf candidate makes softmax_candidates uniform
+    (:371-391).  top_k Some(k >= n) keeps the finite logits only (apply_top_k,
+    :250-256).  Checked over all 10000 selectors against the closed form: uniform
+    probabilities 1/c walked in candidate order, cumulative sums in f32."""
+    lg = np.array([0.0, np.inf, 1.0, 2.0, -np.inf], np.float32)
+
+    def uniform_pick(cands, s):
+        sel = np.float32(s % 10000) / np.float32(10000.0)
+        cum = np.float32(0.0)
+        for c in cands:
+            cum = np.float32(cum + np.float32(1.0) / np.float32(len(cands)))
+            if sel < cum:
+                return c
+        return cands[-1]
+
+    for s in range(10000):
+        # None, no top-p: candidates 0, 1 (+inf), 2, 3 in index order, uniform
+        assert O.sample_token(lg, temperature=1.0, top_k=None, top_p=None, seed=s) == uniform_pick([0, 1, 2, 3], s)
+    # the values the reference gives for two selectors (0.26 and 0.51)
+    assert O.sample_token(lg, temperature=1.0, top_k=None, top_p=None, seed=2600) == 1
+    assert O.sample_token(lg, temperature=1.0, top_k=None, top_p=None, seed=5100) == 2
+    for s in range(0, 10000, 3):
+        # None with top-p 0.6: descending order 1 (+inf), 3, 2, 0 at 1/4 each; the cut keeps
+        # three (cumulative 0.75 >= 0.6), sampled uniformly in that order
+        assert O.sample_token(lg, temperature=1.0, top_k=None, top_p=0.6, seed=s) == uniform_pick([1, 3, 2], s)
+    # Some(k >= n): finite only, so the softmax of [0, 1, 2] over indices 0, 2, 3
+    z = np.array([0.0, 1.0, 2.0])
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    counts = np.zeros(5, int)
+    for s in range(10000):
+        counts[O.sample_token(lg, temperature=1.0, top_k=10, top_p=None, seed=s)] += 1
+    assert counts[1] == 0 and counts[4] == 0
+    assert np.abs(counts[[0, 2, 3]] / 10000.0 - p).max() <= 2e-4
