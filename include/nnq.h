@@ -184,6 +184,19 @@ int nnq_linear_sample(const nnq_weight *w, const float *x, int64_t k, const floa
                       float *logits, const uint32_t *past_tokens, int64_t n_past, const nnq_sampling *cfg,
                       uint32_t *token, void *stream);
 
+/* nnq_linear_sample without allocation.  It has no counterpart in the reference: it is
+ * for callers that cannot call hipMalloc (code under HIP graph capture, serving loops,
+ * harnesses that forbid allocation).  Arguments, results and errors as
+ * nnq_linear_sample; the sampling scratch comes from a fixed device array of 384 KiB
+ * that each GPU holds until the process ends (nnq_init looks up its address), so no
+ * call allocates.  That bounds the top-k: ceil(n / 2048) * min(k, 2048) <= 16384, as for
+ * nnq_linear_sample; beyond it NNQ_ERR_UNSUPPORTED.  Every call on one GPU uses that
+ * GPU's one array: calls that overlap on one GPU (other streams, or graphs replayed
+ * concurrently) race and must be serialized by the caller. */
+int nnq_linear_sample_noalloc(const nnq_weight *w, const float *x, int64_t k, const float *bias, int64_t bias_len,
+                              float *logits, const uint32_t *past_tokens, int64_t n_past, const nnq_sampling *cfg,
+                              uint32_t *token, void *stream);
+
 /* ---- Qwen3 SwiGLU MLP ----------------------------------------------------------- */
 
 /* Upload one layer's MLP: gate_proj and up_proj W[inter, hidden] (block bytes of one

@@ -57,6 +57,8 @@ SIGNATURES = {
     "nnq_sample_token": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),
     "nnq_linear_sample": (c_int, [c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_void_p,
                                   c_void_p, c_void_p]),
+    "nnq_linear_sample_noalloc": (c_int, [c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64,
+                                          c_void_p, c_void_p, c_void_p]),
     "nnq_gguf_open": (c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),
     "nnq_gguf_close": (c_int, [c_void_p]),
     "nnq_gguf_info": (c_int, [c_void_p, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(c_i64),

@@ -201,6 +201,10 @@ int nnq_init(int device) {
     HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
     if (!std::strstr(prop.gcnArchName, "gfx950"))
         return fail(NNQ_ERR_UNSUPPORTED, "kernels are built for gfx950, device is %s", prop.gcnArchName);
+    // the device address of the fixed scratch of nnq_linear_sample_noalloc, looked up
+    // here so that the entry point's calls do no set-up work
+    void *p = nullptr;
+    HIP_TRY((hipError_t)sample_static_scratch(&p), "hipGetSymbolAddress(scratch)");
     return NNQ_OK;
 }
 
@@ -741,14 +745,28 @@ int nnq_moe_block_forward(const nnq_moe *m, const nnq_router *r, const void *x, 
 
 // ---- token sampling ------------------------------------------------------------------
 
-static int run_sample(const float *logits, int64_t n, const uint32_t *past, int64_t n_past, const nnq_sampling *cfg,
-                      uint32_t *token, void *stream) {
-    const int64_t k = cfg->top_k < 0 ? n : std::min<int64_t>(cfg->top_k, n);
-    if (!sample_supported(n, k))
+// the top-k a sampling call keeps (min(top_k, n); n for None), and whether the device
+// path holds it
+static int sample_k(const nnq_sampling *cfg, int64_t n, int64_t *k) {
+    *k = cfg->top_k < 0 ? n : std::min<int64_t>(cfg->top_k, n);
+    if (!sample_supported(n, *k))
         return fail(NNQ_ERR_UNSUPPORTED, "top_k %lld over %lld logits exceeds the device top-k capacity",
-                    (long long)k, (long long)n);
+                    (long long)*k, (long long)n);
+    return NNQ_OK;
+}
+
+// ext_scratch: scratch the caller provides (sample_scratch_bytes(n, k) bytes), or null to
+// take the stream's workspace
+static int run_sample(const float *logits, int64_t n, const uint32_t *past, int64_t n_past, const nnq_sampling *cfg,
+                      uint32_t *token, void *stream, void *ext_scratch = nullptr) {
+    int64_t k = 0;
+    int rc = sample_k(cfg, n, &k);
+    if (rc) return rc;
     Scratch s;
-    HIP_TRY(s.alloc(sample_scratch_bytes(n, k), (hipStream_t)stream), "scratch alloc");
+    if (ext_scratch)
+        s.p = ext_scratch;
+    else
+        HIP_TRY(s.alloc(sample_scratch_bytes(n, k), (hipStream_t)stream), "scratch alloc");
     // sample_token's conditions for applying the penalties (sampling.rs:155-162)
     const int rep_on = std::fabs(cfg->repetition_penalty - 1.0f) > 1.1920929e-7f;
     const int freq_on = std::fabs(cfg->frequency_penalty) > 1.1920929e-7f;
@@ -785,6 +803,29 @@ int nnq_linear_sample(const nnq_weight *w, const float *x, int64_t k, const floa
     rc = dispatch_linear(w, x, NNQ_F32, 1, bias, logits, NNQ_F32, stream);
     if (rc) return rc;
     return run_sample(logits, w->L.n, past_tokens, n_past, cfg, token, stream);
+}
+
+int nnq_linear_sample_noalloc(const nnq_weight *w, const float *x, int64_t k, const float *bias, int64_t bias_len,
+                              float *logits, const uint32_t *past_tokens, int64_t n_past, const nnq_sampling *cfg,
+                              uint32_t *token, void *stream) {
+    int rc = check_linear(w, x, NNQ_F32, 1, k, bias, bias_len, logits, NNQ_F32);
+    if (rc) return rc;
+    rc = check_sampling(cfg, past_tokens, n_past, token);
+    if (rc) return rc;
+    int64_t kk = 0;
+    rc = sample_k(cfg, w->L.n, &kk);
+    if (rc) return rc;
+    const size_t need = sample_scratch_bytes(w->L.n, kk);
+    if (need > kSampleStaticScratchBytes)
+        return fail(NNQ_ERR_UNSUPPORTED, "top_k %lld over %lld logits needs %zu bytes of scratch; the fixed scratch holds %zu",
+                    (long long)kk, (long long)w->L.n, need, kSampleStaticScratchBytes);
+    void *scr = nullptr;
+    HIP_TRY((hipError_t)sample_static_scratch(&scr), "fixed scratch address");
+    // the single-token GEMV takes no scratch; the sampling kernels write every scratch
+    // byte they read, so nothing needs clearing
+    rc = dispatch_linear(w, x, NNQ_F32, 1, bias, logits, NNQ_F32, stream);
+    if (rc) return rc;
+    return run_sample(logits, w->L.n, past_tokens, n_past, cfg, token, stream, scr);
 }
 
 }  // extern "C"

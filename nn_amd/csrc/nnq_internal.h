@@ -100,6 +100,10 @@ int launch_nonfinite_check(const void *y, int y_bf16, int64_t count, int32_t *st
 // the shape fits the two-pass top-k (ceil(n / 2048) * min(k, 2048) <= 16384), and the launch
 size_t sample_scratch_bytes(int64_t n, int64_t k);
 bool sample_supported(int64_t n, int64_t k);
+// The fixed per-device scratch of nnq_linear_sample_noalloc: its size, and its device
+// address on the current device (looked up once per device; returns a hipError_t).
+constexpr size_t kSampleStaticScratchBytes = 384 * 1024;
+int sample_static_scratch(void **out);
 // keep_inf: top_k is None, so +inf logits are candidates too (k = n)
 int launch_sample(const float *logits, int64_t n, const uint32_t *past, int64_t n_past, float temperature, int64_t k,
                   int keep_inf, int use_top_p, float top_p, float rep, int rep_on, float freq, int freq_on,

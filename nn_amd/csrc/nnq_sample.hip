@@ -19,6 +19,7 @@
 //                        order (:211-238), softmax and the seed's selector walk
 //                        (:340-391), and argmax_slice (:394-400) when no candidate is left.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "nnq_device.h"
@@ -417,6 +418,38 @@ bool sample_supported(int64_t n, int64_t k) {
     const int64_t blocks = (n + kSampleBlock - 1) / kSampleBlock;
     const int64_t kk = std::min<int64_t>(std::max<int64_t>(k, 1), kSampleBlock);
     return blocks * kk <= kSampleMaxCand && n <= 0xFFFFFFFFll;
+}
+
+// ---- fixed device scratch for the allocation-free entry point -----------------------
+//
+// One array per GPU (each device that loads the library holds its own copy until the
+// process ends).  Host code never uses its name as an address: the name is a host-side
+// stand-in, so its device address is looked up once per device with
+// hipGetSymbolAddress, with that device current, and that address is what kernels and
+// copies receive.
+
+static __device__ __align__(256) uint8_t scratch[kSampleStaticScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_static_mu;
+void *g_static_ptr[kMaxDevices] = {};
+}  // namespace
+
+int sample_static_scratch(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(g_static_mu);
+    if (!g_static_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        g_static_ptr[dev] = p;
+    }
+    *out = g_static_ptr[dev];
+    return (int)hipSuccess;
 }
 
 int launch_sample(const float *logits, int64_t n, const uint32_t *past, int64_t n_past, float temperature, int64_t k,
