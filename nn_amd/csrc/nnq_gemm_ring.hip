@@ -1,4 +1,4 @@
-// Prefill GEMM for Q4_K weights on gfx950, LDS-ring kernel (bf16 activations, M >= 128):
+// Prefill GEMM for Q4_K weights on gfx950, LDS-ring kernel (bf16 activations, M > 8):
 // Y[m, n] = X[m, k] . W[n, k]^T (+ bias), the arithmetic of QLinear::forward with a batch
 // of tokens (crates/nn-core/src/layers/quantized/linear.rs:366-400).
 //
@@ -6,13 +6,13 @@
 // nibbles of the group's 32 bytes per row) and 2p + 1 (the high nibbles).  A ring of NBUF
 // LDS buffers holds consecutive stages, copied NBUF - 1 stages ahead by every thread with
 // global_load_lds (16 bytes per lane, no register round trip):
-//   A: 128 rows x 8 chunks of 8 f16; chunk c of row r sits at slot c ^ ((r >> 1) & 7), so
+//   A: BM rows (32, 64 or 128) x 8 chunks of 8 f16; chunk c of row r sits at slot c ^ ((r >> 1) & 7), so
 //      the 16-byte fragment reads of 16 consecutive rows fall in distinct banks;
 //   B: the raw tile16 bytes of group p: tile x plane x 16 rows x 16 bytes;
 // and the super-block headers ride along with the first stage of each super-block.
 //
-// Four waves side by side, each a 128 x BN/4 wave tile (WGN = 4; WGN = 2 gives 2 x 2
-// waves of 64 x BN/2); every wave dequantizes the raw bytes of its own columns in
+// Four waves side by side, each a BM x BN/4 wave tile (WGN = 4; WGN = 2 gives 2 x 2
+// waves of BM/2 x BN/2); every wave dequantizes the raw bytes of its own columns in
 // registers (no dequantized copy through LDS):
 // consumer lane 16G + r takes bytes 8G .. 8G + 7 of row r's group (plane G >> 1), whose
 // low nibbles are k = 64p + 8G + i of sub-block 2p and high nibbles k = 64p + 32 + 8G + i
@@ -60,20 +60,20 @@ __device__ __forceinline__ void wait_vmcnt() {
 #define NNQ_GPTR(p) ((const __attribute__((address_space(1))) void *)(p))
 #define NNQ_LPTR(p) ((__attribute__((address_space(3))) void *)(p))
 
-template <int BN, int NBUF, int WGN>
+template <int BN, int NBUF, int WGN, int BM_>
 struct RK {
     // WGN wave columns x (4 / WGN) wave rows, wave tile WM x (BN / WGN)
-    static constexpr int BM = 128, NTH = 256, NTILE = BN / 16, NT = NTILE / WGN, MT = 2 * WGN;
-    static constexpr int WM = BM * WGN / 4;
+    static constexpr int BM = BM_, NTH = 256, NTILE = BN / 16, NT = NTILE / WGN;
+    static constexpr int WM = BM * WGN / 4, MT = WM / 16;
     static constexpr int A_CH = BM * 8, B_CH = NTILE * 32, CH = A_CH + B_CH;
     static constexpr int LPT = (CH + NTH - 1) / NTH;  // copy instructions per thread and stage
     static constexpr int BUF = LPT * NTH * 16;
     // per super-block (two areas, by parity): headers (NTILE x 16 rows x 16 B), the
-    // staged sub-block sums of x (BM rows x hi / lo x 16 B), the weight's min-term
-    // operands (NTILE x hi / lo x 16 rows x 16 B)
+    // staged sub-block sums of x (BM rows x hi / lo x 16 B, in an area of one granule
+    // per thread), the weight's min-term operands (NTILE x hi / lo x 16 rows x 16 B)
     static constexpr int AUX_CH = NTILE * 32, AUXI = (AUX_CH + NTH - 1) / NTH;
     static constexpr int SB_EXTRA = 2 + AUXI;  // copy instructions per thread and super-block
-    static constexpr int HDR_OFF = 0, XS_OFF = NTH * 16, AUX_OFF = XS_OFF + BM * 2 * 16;
+    static constexpr int HDR_OFF = 0, XS_OFF = NTH * 16, AUX_OFF = XS_OFF + NTH * 16;
     static constexpr int SBA = AUX_OFF + AUXI * NTH * 16;
     // epilogue factors: 2^-s_row of the BM rows, s_n of the BN columns (f32)
     static constexpr int EPI_CH = (BM + BN) / 4;
@@ -81,9 +81,9 @@ struct RK {
     static_assert(EPI_CH <= NTH, "one epilogue-factor copy per thread");
     static_assert((size_t)BM * (BN * 4 + 16) <= (size_t)NBUF * BUF + 2 * SBA, "the f32 output tile fits below the factors");
     static_assert(NTILE % WGN == 0, "column tiles split evenly over the wave columns");
-    static_assert(MT * 16 == WM, "wave rows");
+    static_assert(MT * 16 == WM && MT >= 1, "wave rows");
     static_assert(A_CH % NTH == 0, "a copy instruction is all A or all B");
-    static_assert(NTILE * 16 <= NTH && BM * 2 == NTH, "one header and one sums copy per thread");
+    static_assert(NTILE * 16 <= NTH && BM * 2 <= NTH, "one header and one sums copy per thread");
     static_assert(LDS <= 160 * 1024, "LDS budget of a gfx950 workgroup");
     static_assert((NBUF - 1) * (LPT + SB_EXTRA) < 64, "vmcnt range");
 };
@@ -99,9 +99,9 @@ constexpr int rk_wait(int p) {
     return n;
 }
 
-template <int BN, int NBUF, int WGN>
+template <int BN, int NBUF, int WGN, int BM_>
 __global__ __launch_bounds__(256) void gemm_q4k_rk_kernel(GemmArgs a, GemmScratch sc) {
-    using C = RK<BN, NBUF, WGN>;
+    using C = RK<BN, NBUF, WGN, BM_>;
     constexpr int MT = C::MT, NT = C::NT, LPT = C::LPT, NTH = C::NTH, BM = C::BM;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     unsigned char *ring = smem;
@@ -403,18 +403,18 @@ __global__ __launch_bounds__(256) void gemm_finalize_kernel(const float *ys, int
         *reinterpret_cast<floatx4 *>(reinterpret_cast<float *>(y) + i) = v;
 }
 
-template <int BN, int NBUF, int WGN>
+template <int BN, int NBUF, int WGN, int BM>
 int launch_rk(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    using C = RK<BN, NBUF, WGN>;
+    using C = RK<BN, NBUF, WGN, BM>;
     static bool attr_set = false;  // idempotent attribute write; races only repeat it
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_rk_kernel<BN, NBUF, WGN>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_rk_kernel<BN, NBUF, WGN, BM>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
     }
     const int nct = (int)((a.ntile * 16 + BN - 1) / BN), nrt = (int)((a.m + C::BM - 1) / C::BM);
-    hipLaunchKernelGGL((gemm_q4k_rk_kernel<BN, NBUF, WGN>), dim3((unsigned)(nct * nrt * sc.ksplit)), dim3(C::NTH), C::LDS,
+    hipLaunchKernelGGL((gemm_q4k_rk_kernel<BN, NBUF, WGN, BM>), dim3((unsigned)(nct * nrt * sc.ksplit)), dim3(C::NTH), C::LDS,
                        st, a, sc);
     int e = (int)hipGetLastError();
     if (e || sc.ksplit == 1) return e;
@@ -426,43 +426,55 @@ int launch_rk(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
 
 }  // namespace
 
-// Shapes the ring kernel takes (bf16 activations, M >= 128, N % 128 == 0): 128 x BN
-// tiles, BN the widest of 192, 128 dividing N whose tiles alone give at least 256
-// workgroups (one per CU), else the narrowest with K split 2 or 4 ways (a divisor of
-// the super-block count leaving at least 4 super-blocks per workgroup) as far as it
-// takes to reach 256 workgroups.
+// Shapes the ring kernel takes (bf16 activations, N % 128 == 0, a 16-byte aligned output):
+// BM x BN tiles, BM the smallest of 32, 64, 128 holding M (128 beyond), BN 192 or 128
+// (dividing N), K split 1, 2, 4, 8 or 16 ways (a divisor of the super-block count leaving
+// at least 4 super-blocks per workgroup, 2 with BM < 128).  Of these, the plan with the
+// least estimated time: rounds of workgroups (one resident per CU: the rings of the small
+// row tiles are deepened until LDS holds one) times stages per workgroup, a 128-wide
+// stage at 0.8 of a 192-wide one, plus one stage for the split-K finalize.  (Assuming two
+// resident workgroups with shallower rings measured 5-25% slower at M = 16 to 64.)
 // Returns the K split, or 0 when the shape does not fit.
-int gemm_ring_plan(const GemmArgs &a, int *bn) {
+int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm) {
     // (the output tile is written in 16-byte chunks)
-    if (!a.x_bf16 || a.m < 128 || a.nblk < 1 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
-    const int64_t ncols = a.ntile * 16, nrt = (a.m + 127) / 128;
-    // the widest tile that alone gives every CU a workgroup; else the narrowest tile
-    // and a K split (64-wide tiles without a split measured 25% slower than 128-wide
-    // tiles with one at 512 x 4096 x 12288)
-    int b = 0;
+    if (!a.x_bf16 || a.m < 1 || a.nblk < 1 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
+    const int rows = a.m <= 32 ? 32 : (a.m <= 64 ? 64 : 128);
+    const int64_t ncols = a.ntile * 16, nrt = (a.m + rows - 1) / rows;
+    const int min_sb = rows == 128 ? 4 : 2, per_cu = 1;
+    double best_cost = 0.0;
+    int best_bn = 0, best_ks = 0;
     for (int cand : {192, 128}) {
         if (ncols % cand) continue;
-        b = cand;
-        if (nrt * (ncols / cand) >= 256) break;
+        for (int ks = 1; ks <= 16; ks *= 2) {
+            if (a.nblk % ks || (ks > 1 && a.nblk / ks < min_sb)) continue;
+            const int64_t wgs = nrt * (ncols / cand) * ks;
+            const int64_t rounds = (wgs + 256 * per_cu - 1) / (256 * per_cu);
+            const double cost = (double)rounds * (double)(a.nblk / ks) * (cand == 192 ? 1.0 : 0.8) + (ks > 1 ? 1.0 : 0.0);
+            if (best_bn == 0 || cost < best_cost) {
+                best_cost = cost;
+                best_bn = cand;
+                best_ks = ks;
+            }
+        }
     }
-    if (b == 0) return 0;
-    if (bn) *bn = b;
-    const int64_t wgs = nrt * (ncols / b);
-    int best = 1;
-    for (int ks = 2; ks <= 4 && wgs * best < 256; ks *= 2)
-        if (a.nblk % ks == 0 && a.nblk / ks >= 4) best = ks;
-    return best;
+    if (best_bn == 0) return 0;
+    if (bn) *bn = best_bn;
+    if (bm) *bm = rows;
+    return best_ks;
 }
 
 int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream) {
-    int bn = 0;
-    const int ksplit = gemm_ring_plan(a, &bn);
+    int bn = 0, bm = 0;
+    const int ksplit = gemm_ring_plan(a, &bn, &bm);
     if (ksplit == 0 || sc.ksplit != ksplit || (ksplit > 1 && !sc.ysplit)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
-    // waves side by side (128 rows x BN / 4 columns each): measured 4-5% faster on MI355X
-    // than 2 x 2 (64 x BN / 2), which halves the A reads from LDS but doubles the
+    // waves side by side (BM rows x BN / 4 columns each): measured 4-5% faster on MI355X
+    // than 2 x 2 (BM / 2 x BN / 2), which halves the A reads from LDS but doubles the
     // dequantization of every column
-    return bn == 192 ? launch_rk<192, 4, 4>(a, sc, st) : launch_rk<128, 4, 4>(a, sc, st);
+    // the smaller row tiles leave LDS for a deeper ring (more stages in flight)
+    if (bm == 32) return bn == 192 ? launch_rk<192, 8, 4, 32>(a, sc, st) : launch_rk<128, 8, 4, 32>(a, sc, st);
+    if (bm == 64) return bn == 192 ? launch_rk<192, 6, 4, 64>(a, sc, st) : launch_rk<128, 6, 4, 64>(a, sc, st);
+    return bn == 192 ? launch_rk<192, 4, 4, 128>(a, sc, st) : launch_rk<128, 4, 4, 128>(a, sc, st);
 }
 
 }  // namespace nnq

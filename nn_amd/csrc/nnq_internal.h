@@ -136,8 +136,8 @@ struct GemmScratch {
     float *ysplit;     // [ksplit][m][n] f32 partial results when ksplit > 1
 };
 // ring kernel (nnq_gemm_ring.hip): its K split for a shape (0: the shape does not fit
-// the kernel; bn, when given, receives the tile width), and its launch
-int gemm_ring_plan(const GemmArgs &a, int *bn);
+// the kernel; bn and bm, when given, receive the tile width and height), and its launch
+int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm = nullptr);
 int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream);
 
 // MoE (GPT-OSS MXFP4).  Expert weights [E][K][N] with 32-element blocks along N

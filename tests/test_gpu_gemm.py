@@ -111,10 +111,12 @@ def test_gemm_baseline_shapes(O, dev, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(130, 256, 4096), (256, 384, 2048), (128, 192, 256), (300, 640, 1280),
-                                   (384, 1024, 4096), (128, 4096, 4096)])
+                                   (384, 1024, 4096), (128, 4096, 4096), (9, 128, 256), (17, 4096, 12288),
+                                   (40, 384, 4096), (64, 192, 2048), (33, 768, 8192), (100, 1152, 1024)])
 def test_gemm_ring_edges(O, dev, m, n, k):
-    """The LDS-ring kernel's edges (bf16 activations, m >= 128): ragged last row tile,
-    128- and 192-wide column tiles, a single super-block, K split 1, 2 and 4 ways, with
+    """The LDS-ring kernel's edges (bf16 activations): 32-, 64- and 128-row tiles with a
+    ragged last row tile, 128- and 192-wide column tiles, a single super-block, K split
+    1 to 16 ways, with
     random block bytes (arbitrary finite d / dmin / scales), d = 0 super-blocks, bias,
     f32 and bf16 outputs; the split-K sum is deterministic (two calls agree bit for bit)."""
     import nn_amd
