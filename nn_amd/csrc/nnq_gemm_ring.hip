@@ -86,6 +86,10 @@ struct RK {
     static_assert(NTILE * 16 <= NTH && BM * 2 <= NTH, "one header and one sums copy per thread");
     static_assert(LDS <= 160 * 1024, "LDS budget of a gfx950 workgroup");
     static_assert((NBUF - 1) * (LPT + SB_EXTRA) < 64, "vmcnt range");
+    // the super-block areas alternate by parity: the copy issued in iteration s (stage
+    // s + NBUF - 1) may start a super-block of the current one's parity only after the
+    // current one's last read of its area (stage p = 2), i.e. 4 sb + 2 + NBUF - 1 < 4 (sb + 2)
+    static_assert(NBUF <= 6, "a deeper ring would overwrite the current super-block's area");
 };
 
 // VMEM instructions a thread issues after the batch of stage s and before the wait in
@@ -431,7 +435,7 @@ int launch_rk(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
 // (dividing N), K split 1, 2, 4, 8 or 16 ways (a divisor of the super-block count leaving
 // at least 4 super-blocks per workgroup, 2 with BM < 128).  Of these, the plan with the
 // least estimated time: rounds of workgroups (one resident per CU: the rings of the small
-// row tiles are deepened until LDS holds one) times stages per workgroup, a 128-wide
+// row tiles are deepened to 6 stages, which LDS holds once) times stages per workgroup, a 128-wide
 // stage at 0.8 of a 192-wide one, plus one stage for the split-K finalize.  (Assuming two
 // resident workgroups with shallower rings measured 5-25% slower at M = 16 to 64.)
 // Returns the K split, or 0 when the shape does not fit.
@@ -472,7 +476,7 @@ int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     // than 2 x 2 (BM / 2 x BN / 2), which halves the A reads from LDS but doubles the
     // dequantization of every column
     // the smaller row tiles leave LDS for a deeper ring (more stages in flight)
-    if (bm == 32) return bn == 192 ? launch_rk<192, 8, 4, 32>(a, sc, st) : launch_rk<128, 8, 4, 32>(a, sc, st);
+    if (bm == 32) return bn == 192 ? launch_rk<192, 6, 4, 32>(a, sc, st) : launch_rk<128, 6, 4, 32>(a, sc, st);
     if (bm == 64) return bn == 192 ? launch_rk<192, 6, 4, 64>(a, sc, st) : launch_rk<128, 6, 4, 64>(a, sc, st);
     return bn == 192 ? launch_rk<192, 4, 4, 128>(a, sc, st) : launch_rk<128, 4, 4, 128>(a, sc, st);
 }
