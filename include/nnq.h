@@ -67,11 +67,15 @@ typedef enum nnq_format {
  *  NNQ_LAYOUT_NN_GGUF nn-gguf's own decoders: Q4_K (crates/nn-gguf/src/dequant.rs:335-398),
  *                     Q6_K (crates/nn-gguf/src/dequant.rs:415-459, the only Q6_K decoder), Q8_0 (:178-196).
  *  NNQ_LAYOUT_GPTOSS  GPT-OSS Mxfp4Tensor (crates/nn-gptoss/src/quantize.rs:122-188): packed bytes with
- *                     the HIGH nibble = even element, E8M0 scales in a separate array, byte 0 -> 2^-126. */
+ *                     the HIGH nibble = even element, E8M0 scales in a separate array, byte 0 -> 2^-126.
+ *  NNQ_LAYOUT_OCP     nn-core Mxfp4Block (crates/nn-core/src/layers/quantized/mxfp4.rs:70-84,177-244):
+ *                     17-byte blocks [shared_exp][16 packed] along the flattened order, the LOW nibble =
+ *                     even element, scale 2^(shared_exp - 127) with byte 0 -> 2^-127. */
 typedef enum nnq_layout {
     NNQ_LAYOUT_GGUF = 0,
     NNQ_LAYOUT_NN_GGUF = 1,
-    NNQ_LAYOUT_GPTOSS = 2
+    NNQ_LAYOUT_GPTOSS = 2,
+    NNQ_LAYOUT_OCP = 3
 } nnq_layout;
 
 typedef enum nnq_dtype {
@@ -237,6 +241,16 @@ int nnq_moe_create(int64_t num_experts, int64_t hidden, int64_t inter, const uin
                    const uint8_t *gu_scales, const float *gu_bias, const uint8_t *dn_packed,
                    const uint8_t *dn_scales, const float *dn_bias, nnq_moe **out);
 
+/* The same upload from nn-core OCP MXFP4 tensors (NNQ_LAYOUT_OCP): gu_blocks holds the
+ * quantize_tensor blocks of the flat [E, hidden, 2*inter] tensor (E*hidden*2*inter/32
+ * blocks of 17 bytes), dn_blocks those of [E, inter, hidden]; biases as nnq_moe_create.
+ * Both layouts decode to the same values on the device: every E8M0 byte e scales by
+ * 2^(e - 127), GPT-OSS's byte 0 being stored as 1.  Replaces the expert tensors of an MoE
+ * whose weights come from mxfp4_quantize_tensor
+ * (crates/nn-core/src/layers/quantized/mxfp4.rs:293-315). */
+int nnq_moe_create_ocp(int64_t num_experts, int64_t hidden, int64_t inter, const uint8_t *gu_blocks,
+                       const float *gu_bias, const uint8_t *dn_blocks, const float *dn_bias, nnq_moe **out);
+
 int nnq_moe_destroy(nnq_moe *moe);
 
 /* y[t, hidden] (f32) = MoE(x[t, hidden]) with router logits [t, E] (f32):
@@ -281,6 +295,12 @@ int nnq_moe_block_forward(const nnq_moe *moe, const nnq_router *router, const vo
  * [inter, hidden] — bit-exact with Mxfp4Tensor::dequantize
  * (crates/nn-gptoss/src/quantize.rs:167-188). Either output may be NULL. */
 int nnq_moe_dequant_expert(const nnq_moe *moe, int64_t expert, float *gate_up, float *down, void *stream);
+
+/* Decode the first n values of an nn-core OCP MXFP4 tensor (device blocks of 17 bytes,
+ * ceil(n / 32) of them) to f32 at device `out` — bit-exact with dequantize_tensor
+ * (crates/nn-core/src/layers/quantized/mxfp4.rs:226-244,320-333) for every shared_exp
+ * 0..254 (255 scales by +inf: infinities, and NaN for zero codes). */
+int nnq_dequant_mxfp4_ocp(const uint8_t *blocks, int64_t n, float *out, void *stream);
 
 /* ---- GGUF ingest ------------------------------------------------------------------ */
 
@@ -335,6 +355,11 @@ int nnq_quantize_q4_k(const float *v, size_t n, uint8_t *out);
 /* Mxfp4Tensor::quantize (crates/nn-gptoss/src/quantize.rs:122-163): `packed`
  * holds ceil(n/32)*16 bytes, `scales` ceil(n/32) bytes. */
 int nnq_quantize_mxfp4(const float *v, size_t n, uint8_t *packed, uint8_t *scales);
+
+/* nn-core OCP MXFP4 quantize_tensor (crates/nn-core/src/layers/quantized/mxfp4.rs:142-220,
+ * 293-315): `blocks` holds ceil(n/32)*17 bytes; NNQ_ERR_NON_FINITE on NaN/inf
+ * (ValueOutOfRange). */
+int nnq_quantize_mxfp4_ocp(const float *v, size_t n, uint8_t *blocks);
 
 /* Q8_0 and nn-gguf-layout Q6_K encoders.  The reference ships no encoder for
  * either (its tests hand-build blocks, quantized_matmul_tests.rs:37-46); these

@@ -57,6 +57,10 @@ SIGNATURES = {
     "nnq_sample_token": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),
     "nnq_linear_sample": (c_int, [c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_void_p,
                                   c_void_p, c_void_p]),
+    "nnq_moe_create_ocp": (c_int, [c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                   ctypes.POINTER(c_void_p)]),
+    "nnq_dequant_mxfp4_ocp": (c_int, [c_void_p, c_i64, c_void_p, c_void_p]),
+    "nnq_quantize_mxfp4_ocp": (c_int, [c_void_p, c_sz, c_void_p]),
     "nnq_linear_sample_noalloc": (c_int, [c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64,
                                           c_void_p, c_void_p, c_void_p]),
     "nnq_gguf_open": (c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),

@@ -457,9 +457,13 @@ int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const floa
 
 // ---- MoE ---------------------------------------------------------------------------
 
-int nnq_moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, const uint8_t *gu_scales,
-                   const float *gu_bias, const uint8_t *dn_packed, const uint8_t *dn_scales, const float *dn_bias,
-                   nnq_moe **out) {
+}  // extern "C"
+
+// Upload of one layer's experts from GPT-OSS-ordered packed bytes and scale bytes
+// (gptoss_scales: GPT-OSS E8M0 semantics, byte 0 = 2^-126; else nn-core OCP, 2^-127).
+static int moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, const uint8_t *gu_scales,
+                      const float *gu_bias, const uint8_t *dn_packed, const uint8_t *dn_scales, const float *dn_bias,
+                      bool gptoss_scales, nnq_moe **out) {
     if (!out) return fail(NNQ_ERR_INVALID_ARGUMENT, "out is null");
     *out = nullptr;
     if (E <= 0 || H <= 0 || I <= 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "bad MoE shape");
@@ -483,12 +487,12 @@ int nnq_moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, co
     hipError_t e = hipSuccess;
     rq.resize(gu_el / 2);
     rs.resize(gu_el / 32);
-    moe_repack(gu_packed, gu_scales, E, H, 2 * I, rq.data(), rs.data());
+    moe_repack(gu_packed, gu_scales, E, H, 2 * I, rq.data(), rs.data(), gptoss_scales);
     if ((e = upload(rq.data(), rq.size(), &p[0])) == hipSuccess) e = upload(rs.data(), rs.size(), &p[1]);
     if (e == hipSuccess) {
         rq.resize(dn_el / 2);
         rs.resize(dn_el / 32);
-        moe_repack(dn_packed, dn_scales, E, I, H, rq.data(), rs.data());
+        moe_repack(dn_packed, dn_scales, E, I, H, rq.data(), rs.data(), gptoss_scales);
         if ((e = upload(rq.data(), rq.size(), &p[2])) == hipSuccess) e = upload(rs.data(), rs.size(), &p[3]);
     }
     if (e == hipSuccess) e = upload(gu_bias, (size_t)E * 2 * I * 4, &p[4]);
@@ -508,6 +512,39 @@ int nnq_moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, co
     m->d.gu_b = (const float *)p[4];
     m->d.dn_b = (const float *)p[5];
     *out = m;
+    return NNQ_OK;
+}
+
+extern "C" {
+
+int nnq_moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, const uint8_t *gu_scales,
+                   const float *gu_bias, const uint8_t *dn_packed, const uint8_t *dn_scales, const float *dn_bias,
+                   nnq_moe **out) {
+    return moe_create(E, H, I, gu_packed, gu_scales, gu_bias, dn_packed, dn_scales, dn_bias, true, out);
+}
+
+int nnq_moe_create_ocp(int64_t E, int64_t H, int64_t I, const uint8_t *gu_blocks, const float *gu_bias,
+                       const uint8_t *dn_blocks, const float *dn_bias, nnq_moe **out) {
+    if (!out) return fail(NNQ_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (E <= 0 || H <= 0 || I <= 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "bad MoE shape");
+    if (!gu_blocks || !dn_blocks) return fail(NNQ_ERR_INVALID_ARGUMENT, "null weight pointer");
+    if (H % 32 || I % 32)
+        return fail(NNQ_ERR_INVALID_SHAPE, "MoE hidden (%lld) and intermediate (%lld) sizes must be multiples of 32",
+                    (long long)H, (long long)I);
+    const size_t gnb = (size_t)E * H * 2 * I / 32, dnb = (size_t)E * I * H / 32;
+    std::vector<uint8_t> gp(gnb * 16), gs(gnb), dp(dnb * 16), ds(dnb);
+    ocp_split(gu_blocks, gnb, gp.data(), gs.data());
+    ocp_split(dn_blocks, dnb, dp.data(), ds.data());
+    return moe_create(E, H, I, gp.data(), gs.data(), gu_bias, dp.data(), ds.data(), dn_bias, false, out);
+}
+
+int nnq_dequant_mxfp4_ocp(const uint8_t *blocks, int64_t n, float *out, void *stream) {
+    if (n < 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "n = %lld", (long long)n);
+    if (n == 0) return NNQ_OK;
+    if (!blocks || !out) return fail(NNQ_ERR_INVALID_ARGUMENT, "null pointer");
+    int e = launch_ocp_dequant(blocks, n, out, stream);
+    if (e) return hip_fail((hipError_t)e, "mxfp4 dequant launch");
     return NNQ_OK;
 }
 

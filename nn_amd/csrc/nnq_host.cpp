@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "../../include/nnq.h"
+#include "nnq_internal.h"
 
 namespace {
 
@@ -262,6 +263,55 @@ int nnq_quantize_mxfp4(const float *v, size_t n, uint8_t *packed, uint8_t *scale
                 size_t ih = s0 + 2 * p, il = ih + 1;
                 uint8_t ch = fp4_code(ih < n ? v[ih] : 0.0f, sc), cl = fp4_code(il < n ? v[il] : 0.0f, sc);
                 packed[b * 16 + p] = (uint8_t)((ch << 4) | cl);
+            }
+        }
+    });
+    return NNQ_OK;
+}
+
+// nn-core OCP MXFP4 quantize_tensor (crates/nn-core/src/layers/quantized/mxfp4.rs:194-220,
+// 293-315): 17-byte blocks [shared_exp][16 packed, element 2i in the low nibble of byte
+// i], shared_exp = clamp(ceil(log2(max|v| / 6)) + 127, 0, 254) (0 for an all-zero block),
+// codes the nearest e2m1 magnitude of |v| / 2^(e - 127) (strict <: ties keep the lower).
+int nnq_quantize_mxfp4_ocp(const float *v, size_t n, uint8_t *blocks) {
+    if ((!v && n) || (!blocks && n)) return NNQ_ERR_INVALID_ARGUMENT;
+    for (size_t i = 0; i < n; i++)
+        if (!std::isfinite(v[i])) return nnq::set_error(NNQ_ERR_NON_FINITE, "mxfp4 quantize_block: non-finite input value");
+    static const float kMag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    const size_t nb = (n + 31) / 32;
+    parallel_blocks(nb, [&](size_t lo, size_t hi) {
+        for (size_t b = lo; b < hi; b++) {
+            float x[32];
+            float mx = 0.0f;
+            for (int i = 0; i < 32; i++) {
+                x[i] = b * 32 + i < n ? v[b * 32 + i] : 0.0f;
+                const float a = std::fabs(x[i]);
+                if (a > mx) mx = a;
+            }
+            uint8_t e = 0;
+            if (mx != 0.0f) {
+                const int eb = (int)std::ceil(std::log2(mx / 6.0f)) + 127;
+                e = (uint8_t)std::min(254, std::max(0, eb));
+            }
+            const float scale = (float)std::ldexp(1.0, (int)e - 127);
+            uint8_t *blk = blocks + b * 17;
+            blk[0] = e;
+            for (int p = 0; p < 16; p++) blk[1 + p] = 0;
+            for (int i = 0; i < 32; i++) {
+                uint8_t code = 0;
+                if (x[i] != 0.0f && scale != 0.0f) {
+                    const float q = std::fabs(x[i]) / scale;
+                    float best = 3.40282347e38f;
+                    for (uint8_t j = 0; j < 8; j++) {
+                        const float d = std::fabs(q - kMag[j]);
+                        if (d < best) {
+                            best = d;
+                            code = j;
+                        }
+                    }
+                    if (x[i] < 0.0f) code |= 0x8;
+                }
+                blk[1 + i / 2] |= (i % 2 == 0) ? code : (uint8_t)(code << 4);
             }
         }
     });

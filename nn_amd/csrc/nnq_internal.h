@@ -162,6 +162,8 @@ int launch_moe(const MoeDev &m, const void *x, int x_bf16, int64_t T, const floa
                const float *bias, int top_k, float limit, float *y, uint32_t *topk_idx, float *topk_w,
                int32_t *status, void *scratch, void *stream);
 int launch_moe_dequant(const MoeDev &m, int64_t e, float *gate_up, float *down, void *stream);
+// nn-core OCP MXFP4 tensor decode: n values from 17-byte blocks (device pointers)
+int launch_ocp_dequant(const uint8_t *blocks, int64_t n, float *out, void *stream);
 // router Linear x[T, H] @ W[E, H]^T (+ bias), H a multiple of 16, over *nsplit K parts: with one
 // part `partial` receives the logits (bias added), else nsplit slabs [T][E] of partial sums
 // (router_partial_bytes; the bias is left to the consumer).  Clears *status when given.
@@ -170,8 +172,13 @@ int launch_router_logits(const void *x, int x_bf16, int64_t T, int64_t H, const 
                          float *partial, int *nsplit, int32_t *status, void *stream);
 int launch_router_finalize(const float *partial, int ks, int64_t T, int E, const float *bias, float *logits,
                            void *stream);
-// host repack of one weight (codes and scales of E experts, K rows, N columns)
+// host repack of one weight (codes and scales of E experts, K rows, N columns); the device
+// scale byte e means 2^(e - 127), so with gptoss_scales the GPT-OSS byte 0 (2^-126) is
+// stored as 1
 void moe_repack(const uint8_t *packed, const uint8_t *scales, int64_t E, int64_t K, int64_t N, uint8_t *dst_codes,
-                uint8_t *dst_scales);
+                uint8_t *dst_scales, bool gptoss_scales);
+// nn-core OCP MXFP4 blocks (17 bytes: shared_exp, 16 packed with element 2i in the low
+// nibble) -> GPT-OSS-ordered packed bytes (element 2i in the high nibble) and scale bytes
+void ocp_split(const uint8_t *blocks, size_t nblocks, uint8_t *packed, uint8_t *scales);
 
 }  // namespace nnq

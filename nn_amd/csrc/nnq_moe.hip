@@ -87,8 +87,9 @@ __device__ __forceinline__ uint32_t fp4_pair(uint32_t codes, uint32_t scale_bits
 }
 
 // Row i = 0..7 of this lane's 8 rows: code byte i, scale byte i moved to bits 23-30.
-// E8M0 byte 0 means 2^-126 in Mxfp4Tensor::decode (crates/nn-gptoss/src/quantize.rs:84-90)
-// but 2^-127 here; such blocks hold values below 1e-37.
+// Device scale bytes mean 2^(e - 127) for every e: GPT-OSS's byte 0 (2^-126,
+// crates/nn-gptoss/src/quantize.rs:84-90) is stored as byte 1 at upload, and the nn-core
+// OCP byte 0 (2^-127, crates/nn-core/src/layers/quantized/mxfp4.rs:177-186) stays 0.
 __device__ __forceinline__ void fp4_rows(u32x2 codes, u32x2 sc, uint32_t r[8]) {
     r[0] = fp4_pair<0>(codes[0], sc[0] << 23);
     r[1] = fp4_pair<1>(codes[0], sc[0] << 15);
@@ -760,8 +761,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeScratch sc, int64_t
 __constant__ float kFp4Lut[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
                                   -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
 
-// FP4_LUT[code] * 2^(E - 127) (E = 1 for scale byte 0) as f32 bits, built with integer
-// arithmetic so that subnormal results are exact whatever the f32 denormal mode.
+// FP4_LUT[code] * 2^(E - 127) as f32 bits (the device scale byte E: GPT-OSS's byte 0 is
+// stored as 1, see fp4_rows), built with integer arithmetic so that subnormal results
+// are exact whatever the f32 denormal mode.  E = 255 scales by +inf (x * inf, 0 * inf =
+// NaN), as both reference decoders do.
 __device__ __forceinline__ float fp4_decode(uint32_t code, uint32_t sbyte) {
     const uint32_t mag = code & 7u, sign = (code & 8u) << 28;
     if (mag == 0 || sbyte == 255) {  // zeros, and the inf scale (x * inf, 0 * inf = NaN)
@@ -771,7 +774,7 @@ __device__ __forceinline__ float fp4_decode(uint32_t code, uint32_t sbyte) {
     // magnitude = m * 2^x with m in {1, 3}: 0.5 = 1*2^-1, 1, 1.5 = 3*2^-1, 2, 3 = 3*2^0, 4, 6 = 3*2^1
     const int m3 = (mag == 3 || mag == 5 || mag == 7);
     const int x = m3 ? (int)(mag >> 1) - 2 : (int)(mag >> 1) - 1;
-    const int E = sbyte == 0 ? 1 : (int)sbyte;
+    const int E = (int)sbyte;
     const int q = x + m3 + E - 127;  // unbiased exponent of the value (m = 3 -> 1.5 * 2^(x + 1))
     uint32_t bits;
     if (q > 127)
@@ -779,8 +782,22 @@ __device__ __forceinline__ float fp4_decode(uint32_t code, uint32_t sbyte) {
     else if (q >= -126)
         bits = ((uint32_t)(q + 127) << 23) | (m3 ? 0x400000u : 0u);
     else
-        bits = (m3 ? 3u : 1u) << (x + E + 22);  // m * 2^(x + E - 127) as a multiple of 2^-149
+        bits = (m3 ? 3u : 1u) << (x + E + 22);  // m * 2^(x + E - 127) as a multiple of 2^-149 (x >= -1)
     return __uint_as_float(bits | sign);
+}
+
+// nn-core OCP MXFP4 tensor decode (dequantize_tensor, crates/nn-core/src/layers/quantized/
+// mxfp4.rs:226-244, 320-333): 17-byte blocks [shared_exp][16 packed], element 2i in the
+// low nibble of byte i, value magnitude * 2^(shared_exp - 127); one thread per byte pair
+// of elements, the first n values.
+__global__ __launch_bounds__(256) void ocp_dequant_kernel(const uint8_t *blocks, int64_t n, float *out) {
+    const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;  // element pair 2p, 2p + 1
+    const int64_t i = 2 * p;
+    if (i >= n) return;
+    const uint8_t *blk = blocks + (i / 32) * 17;
+    const uint32_t e = blk[0], byte = blk[1 + (i % 32) / 2];
+    out[i] = fp4_decode(byte & 15u, e);
+    if (i + 1 < n) out[i + 1] = fp4_decode(byte >> 4, e);
 }
 
 // one workgroup per (column block, row block) fragment; thread = (row, byte column)
@@ -934,6 +951,14 @@ int launch_moe_dequant(const MoeDev &d, int64_t e, float *gate_up, float *down, 
         hipLaunchKernelGGL(moe_dequant_kernel, dim3((unsigned)((N / 32) * (K / 32))), dim3(512), 0, st,
                            d.dn_q + e * per / 2, d.dn_s + e * per / 32, K, N, down);
     }
+    return (int)hipGetLastError();
+}
+
+int launch_ocp_dequant(const uint8_t *blocks, int64_t n, float *out, void *stream) {
+    if (n <= 0) return 0;
+    const int64_t pairs = (n + 1) / 2;
+    hipLaunchKernelGGL(ocp_dequant_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       blocks, n, out);
     return (int)hipGetLastError();
 }
 

@@ -231,7 +231,7 @@ namespace nnq {
 // block) -> per (expert, 32-column block, 32-row block) fragments whose bytes each
 // lane of a 16x16x32 MFMA wave needs; see MoeDev.
 void moe_repack(const uint8_t *packed, const uint8_t *scales, int64_t E, int64_t K, int64_t N, uint8_t *dc,
-                uint8_t *ds) {
+                uint8_t *ds, bool gptoss_scales) {
     const int64_t NB = N / 32, KB = K / 32;
     for (int64_t e = 0; e < E; e++)
         for (int64_t nb = 0; nb < NB; nb++)
@@ -245,8 +245,19 @@ void moe_repack(const uint8_t *packed, const uint8_t *scales, int64_t E, int64_t
                             c[(16 * p + col) * 8 + i] = packed[(e * K + row) * (N / 2) + nb * 16 + col];
                         }
                 uint8_t *s = ds + frag * 32;
-                for (int r = 0; r < 32; r++) s[r] = scales[(e * K + kb * 32 + r) * NB + nb];
+                for (int r = 0; r < 32; r++) {
+                    const uint8_t v = scales[(e * K + kb * 32 + r) * NB + nb];
+                    s[r] = (gptoss_scales && v == 0) ? 1 : v;
+                }
             }
+}
+
+void ocp_split(const uint8_t *blocks, size_t nblocks, uint8_t *packed, uint8_t *scales) {
+    for (size_t b = 0; b < nblocks; b++) {
+        const uint8_t *blk = blocks + b * 17;
+        scales[b] = blk[0];
+        for (int p = 0; p < 16; p++) packed[b * 16 + p] = (uint8_t)((blk[1 + p] << 4) | (blk[1 + p] >> 4));
+    }
 }
 
 }  // namespace nnq

@@ -133,6 +133,7 @@ class Layout(enum.IntEnum):
     GGUF = 0       # GGUF spec: Q8_0, nn-core BlockQ4K
     NN_GGUF = 1    # nn-gguf's own Q4_K / Q6_K decoders
     GPTOSS = 2     # GPT-OSS Mxfp4Tensor
+    OCP = 3        # nn-core Mxfp4Block / Mxfp4Tensor (17-byte blocks, low nibble first)
 
 
 _DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
@@ -492,6 +493,37 @@ class QuantizedMoE:
         self._h = h
         self._router = None
         self.num_experts, self.hidden, self.inter, self.device = E, H, I, device
+        self._attach_router(router_weight, router_bias)
+
+    @classmethod
+    def from_ocp(cls, num_experts, hidden, inter, gu_blocks, gu_bias, dn_blocks, dn_bias, device: int = 0,
+                 router_weight=None, router_bias=None) -> "QuantizedMoE":
+        """The same layer from nn-core OCP MXFP4 tensors (mxfp4.rs quantize_tensor of the
+        flat [E, hidden, 2*inter] and [E, inter, hidden] weights: 17-byte blocks)."""
+        E, H, I = int(num_experts), int(hidden), int(inter)
+        gb_, db_ = _as_u8(gu_blocks), _as_u8(dn_blocks)
+        if gb_.size != E * H * 2 * I // 32 * 17:
+            raise DataLengthMismatch("gate_up OCP MXFP4 byte count does not match [E, hidden, 2*inter]")
+        if db_.size != E * I * H // 32 * 17:
+            raise DataLengthMismatch("down OCP MXFP4 byte count does not match [E, inter, hidden]")
+        gb = np.ascontiguousarray(np.asarray(gu_bias, np.float32).reshape(E, 2 * I))
+        db = np.ascontiguousarray(np.asarray(dn_bias, np.float32).reshape(E, H))
+        init(device)
+        h = ctypes.c_void_p()
+        vp = ctypes.c_void_p
+        with torch.cuda.device(device):
+            _check(_lib.load().nnq_moe_create_ocp(E, H, I, gb_.ctypes.data_as(vp), gb.ctypes.data_as(vp),
+                                                  db_.ctypes.data_as(vp), db.ctypes.data_as(vp), ctypes.byref(h)))
+        self = object.__new__(cls)
+        self._h = h
+        self._router = None
+        self.num_experts, self.hidden, self.inter, self.device = E, H, I, device
+        self._attach_router(router_weight, router_bias)
+        return self
+
+    def _attach_router(self, router_weight, router_bias):
+        E, H, device = self.num_experts, self.hidden, self.device
+        vp = ctypes.c_void_p
         if router_weight is not None:
             rw = np.ascontiguousarray(np.asarray(router_weight, np.float32))
             if rw.shape != (E, H):
@@ -627,6 +659,30 @@ def quantize_mxfp4(values):
                                           packed.ctypes.data_as(ctypes.c_void_p),
                                           scales.ctypes.data_as(ctypes.c_void_p)))
     return packed, scales
+
+
+def quantize_mxfp4_ocp(values) -> np.ndarray:
+    """nn-core mxfp4 quantize_tensor (crates/nn-core/src/layers/quantized/mxfp4.rs:293-315)
+    of the flattened values: ceil(n / 32) 17-byte blocks; NonFiniteData on NaN / inf."""
+    v = _f32c(values)
+    out = np.zeros(((v.size + 31) // 32) * 17, np.uint8)
+    _check(_lib.load().nnq_quantize_mxfp4_ocp(v.ctypes.data_as(ctypes.c_void_p), v.size,
+                                              out.ctypes.data_as(ctypes.c_void_p)))
+    return out
+
+
+def dequantize_mxfp4_ocp(blocks, n: int, device: int = 0) -> torch.Tensor:
+    """nn-core mxfp4 dequantize_tensor on the device (bit-exact): the first n values of
+    the 17-byte blocks (a host array or a device uint8 tensor), as a device f32 tensor."""
+    if isinstance(blocks, torch.Tensor) and blocks.is_cuda:
+        b = blocks.contiguous().view(torch.uint8)
+    else:
+        b = torch.from_numpy(_as_u8(blocks).copy()).to(f"cuda:{device}")
+    if b.numel() < ((int(n) + 31) // 32) * 17:
+        raise DataLengthMismatch(f"{b.numel()} bytes hold fewer than {n} values")
+    out = torch.empty(int(n), dtype=torch.float32, device=b.device)
+    _check(_lib.load().nnq_dequant_mxfp4_ocp(_ptr(b), int(n), _ptr(out), _stream(out)))
+    return out
 
 
 def synth_normal(seed: int, tensor_id: int, shape, sigma: float = 1.0) -> np.ndarray:

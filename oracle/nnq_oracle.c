@@ -811,6 +811,92 @@ done:
     return rc;
 }
 
+/* ------------------------------------------------------------------------ */
+/* nn-core OCP MXFP4: crates/nn-core/src/layers/quantized/mxfp4.rs.          */
+/* A block is [shared_exp u8][16 packed bytes] (Mxfp4Block, :70-84, 17 bytes, */
+/* BLOCK_STORAGE_BYTES :52); element 2i is the LOW nibble of byte i (:209-213,*/
+/* :232-237); blocks run along the flattened order, the last one zero-padded  */
+/* (quantize_tensor :293-315).  The 4-bit codes are the e2m1 values the file */
+/* calls E1M2 (:58-64).                                                       */
+/* ------------------------------------------------------------------------ */
+
+static const float OCP_MAG[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+
+/* block_scale_from_exp (:177-186): 2^(e - 127) in f64, cast to f32 (e = 0 gives the
+ * f32 subnormal 2^-127, e = 255 overflows to +inf) */
+float orc_ocp_block_scale(uint8_t shared_exp) { return (float)ldexp(1.0, (int)shared_exp - 127); }
+
+/* compute_shared_exponent (:142-170): ceil(log2(max|v| / 6)) + 127 in f32, clamped to
+ * [0, 254]; 0 for an all-zero block.  The values are finite (quantize_block checks
+ * first). */
+uint8_t orc_ocp_shared_exp(const float *v32) {
+    float max_abs = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        const float a = fabsf(v32[i]);
+        if (a > max_abs) max_abs = a;
+    }
+    if (max_abs == 0.0f) return 0;
+    const float log2_ratio = log2f(max_abs / 6.0f);
+    const int exp_biased = (int)ceilf(log2_ratio) + 127;
+    return (uint8_t)(exp_biased < 0 ? 0 : (exp_biased > 254 ? 254 : exp_biased));
+}
+
+/* encode_e1m2 (:96-117): 0 for a zero value or scale; else the nearest magnitude of
+ * |v| / scale (strict <, so ties keep the lower index) with the sign in bit 3 */
+uint8_t orc_ocp_encode(float v, float block_scale) {
+    if (v == 0.0f || block_scale == 0.0f) return 0;
+    const int sign = v < 0.0f;
+    const float abs_scaled = fabsf(v) / block_scale;
+    uint8_t best = 0;
+    float best_dist = 3.40282347e38f;
+    for (uint8_t i = 0; i < 8; i++) {
+        const float dist = fabsf(abs_scaled - OCP_MAG[i]);
+        if (dist < best_dist) {
+            best_dist = dist;
+            best = i;
+        }
+    }
+    return (uint8_t)((sign ? 0x8 : 0x0) | best);
+}
+
+/* decode_e1m2 (:124-134): magnitude * scale, negated when bit 3 is set */
+float orc_ocp_decode(uint8_t code, float block_scale) {
+    const float value = OCP_MAG[code & 7] * block_scale;
+    return (code >> 3) & 1 ? -value : value;
+}
+
+/* quantize_tensor (:293-315) over quantize_block (:194-220); blocks holds
+ * ceil(n / 32) * 17 bytes.  Returns -1 (ValueOutOfRange) on a non-finite value. */
+int orc_ocp_quantize_tensor(const float *data, size_t n, uint8_t *blocks) {
+    for (size_t i = 0; i < n; i++)
+        if (!isfinite(data[i])) return -1;
+    const size_t nb = (n + 31) / 32;
+    for (size_t b = 0; b < nb; b++) {
+        float v[32] = {0};
+        for (size_t i = 0; i < 32 && b * 32 + i < n; i++) v[i] = data[b * 32 + i];
+        const uint8_t e = orc_ocp_shared_exp(v);
+        const float scale = orc_ocp_block_scale(e);
+        uint8_t *blk = blocks + b * 17;
+        blk[0] = e;
+        memset(blk + 1, 0, 16);
+        for (int i = 0; i < 32; i++) {
+            const uint8_t code = orc_ocp_encode(v[i], scale);
+            blk[1 + i / 2] |= (i % 2 == 0) ? code : (uint8_t)(code << 4);
+        }
+    }
+    return 0;
+}
+
+/* dequantize_tensor (:320-333) over dequantize_block (:226-244): the first n values */
+void orc_ocp_dequantize_tensor(const uint8_t *blocks, size_t n, float *out) {
+    for (size_t i = 0; i < n; i++) {
+        const uint8_t *blk = blocks + (i / 32) * 17;
+        const size_t j = i % 32;
+        const uint8_t byte = blk[1 + j / 2];
+        out[i] = orc_ocp_decode(j % 2 == 0 ? (byte & 0x0F) : (byte >> 4), orc_ocp_block_scale(blk[0]));
+    }
+}
+
 /* splitmix64 mixer: crates/nn-core/src/test_prng.rs:18-22 */
 uint64_t orc_splitmix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;

@@ -77,6 +77,14 @@ int orc_topk_rows(const float *x, size_t rows, size_t cols, size_t k, float *val
 int orc_q4k_linear(const float *x, size_t rows, size_t k, const uint8_t *w, size_t n, float *y);
 int orc_q6k_linear(const float *x, size_t rows, size_t k, const uint8_t *w, size_t n, float *y);
 
+/* ---- nn-core OCP MXFP4 (17-byte blocks [shared_exp][16 packed], low nibble first) */
+float orc_ocp_block_scale(uint8_t shared_exp);
+uint8_t orc_ocp_shared_exp(const float *v32);
+uint8_t orc_ocp_encode(float v, float block_scale);
+float orc_ocp_decode(uint8_t code, float block_scale);
+int orc_ocp_quantize_tensor(const float *data, size_t n, uint8_t *blocks);
+void orc_ocp_dequantize_tensor(const uint8_t *blocks, size_t n, float *out);
+
 /* ---- GPT-OSS MXFP4 mixture-of-experts layer ---------------------------------- */
 int orc_moe_forward_mxfp4(const float *x, size_t n_tokens, size_t hidden, const float *router_logits,
                           size_t num_experts, size_t top_k, const uint8_t *gu_packed, const uint8_t *gu_scales,

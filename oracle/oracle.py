@@ -68,6 +68,12 @@ def lib():
             "orc_mxfp4_quantize_fp4": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_float]),
             "orc_mxfp4_quantize": (None, [_f32p, _sz, _u8p, _u8p]),
             "orc_mxfp4_dequantize": (None, [_u8p, _u8p, _sz, _sz, _f32p]),
+            "orc_ocp_block_scale": (ctypes.c_float, [ctypes.c_uint8]),
+            "orc_ocp_shared_exp": (ctypes.c_uint8, [_f32p]),
+            "orc_ocp_encode": (ctypes.c_uint8, [ctypes.c_float, ctypes.c_float]),
+            "orc_ocp_decode": (ctypes.c_float, [ctypes.c_uint8, ctypes.c_float]),
+            "orc_ocp_quantize_tensor": (ctypes.c_int, [_f32p, _sz, _u8p]),
+            "orc_ocp_dequantize_tensor": (None, [_u8p, _sz, _f32p]),
             "orc_matmul_xwt": (None, [_f32p, _sz, _sz, _f32p, _sz, _f32p]),
             "orc_matmul_xw": (None, [_f32p, _sz, _sz, _f32p, _sz, _f32p]),
             "orc_argmax": (ctypes.c_int, [_f32p, _sz, _u32p]),
@@ -220,6 +226,44 @@ def mxfp4_dequantize(packed, scales, total):
     scales = _u8(scales)
     out = np.zeros(total, np.float32)
     lib().orc_mxfp4_dequantize(_p(packed, _u8p), _p(scales, _u8p), scales.size, total, _p(out, _f32p))
+    return out
+
+
+def ocp_block_scale(e):
+    """block_scale_from_exp (crates/nn-core/src/layers/quantized/mxfp4.rs:177-186)."""
+    return float(lib().orc_ocp_block_scale(int(e)))
+
+
+def ocp_shared_exp(v32):
+    v = _f32(v32).ravel()
+    assert v.size == 32
+    return int(lib().orc_ocp_shared_exp(_p(v, _f32p)))
+
+
+def ocp_encode(v, scale):
+    return int(lib().orc_ocp_encode(ctypes.c_float(v), ctypes.c_float(scale)))
+
+
+def ocp_decode(code, scale):
+    return float(np.float32(lib().orc_ocp_decode(int(code), ctypes.c_float(scale))))
+
+
+def ocp_quantize(v):
+    """nn-core mxfp4 quantize_tensor (mxfp4.rs:293-315): ceil(n / 32) 17-byte blocks
+    [shared_exp][16 packed, low nibble first]; OracleError on a non-finite value."""
+    v = _f32(v).ravel()
+    out = np.zeros(((v.size + 31) // 32) * 17, np.uint8)
+    if lib().orc_ocp_quantize_tensor(_p(v, _f32p), v.size, _p(out, _u8p)) != 0:
+        raise OracleError("mxfp4 quantize: non-finite input value")
+    return out
+
+
+def ocp_dequantize(blocks, n):
+    """nn-core mxfp4 dequantize_tensor (mxfp4.rs:320-333): the first n values."""
+    blocks = _u8(blocks)
+    assert blocks.size >= ((n + 31) // 32) * 17
+    out = np.zeros(n, np.float32)
+    lib().orc_ocp_dequantize_tensor(_p(blocks, _u8p), n, _p(out, _f32p))
     return out
 
 

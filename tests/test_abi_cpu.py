@@ -147,3 +147,20 @@ def test_host_tensors_are_refused_before_any_launch():
     moe.num_experts, moe.hidden, moe.inter, moe.device = 4, 64, 64, 0
     with pytest.raises(nn_amd.Unsupported):
         moe.forward(torch.zeros(2, 64), torch.zeros(2, 4))
+
+
+def test_ocp_mxfp4_encoder_matches_oracle(O):
+    """nnq_quantize_mxfp4_ocp (nn-core quantize_tensor) byte for byte against the
+    oracle, over lengths that pad the last block and values across the whole exponent
+    range: zeros, tiny blocks whose shared_exp clamps to 0, large ones clamped to 254."""
+    import nn_amd
+    rng = np.random.default_rng(3)
+    for n in (0, 1, 31, 50, 64, 1000, 32 * 257 + 5):
+        v = (rng.standard_normal(n) * 10.0 ** rng.uniform(-45, 38, n)).astype(np.float32)
+        v[::7] = 0.0
+        assert np.array_equal(nn_amd.quantize_mxfp4_ocp(v), O.ocp_quantize(v)), n
+    for scale in (1e-40, 1e-38, 3e37, 3.4e38):
+        v = (rng.uniform(-1, 1, 96) * scale).astype(np.float32)
+        assert np.array_equal(nn_amd.quantize_mxfp4_ocp(v), O.ocp_quantize(v)), scale
+    with pytest.raises(nn_amd.NonFiniteData):
+        nn_amd.quantize_mxfp4_ocp(np.array([0.0, np.inf], np.float32))

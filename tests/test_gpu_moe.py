@@ -231,3 +231,88 @@ def test_moe_block_nonfinite_raises(O, dev):
         moe.block_forward(x, top_k=2)
     x[2, 5] = 1.0
     moe.block_forward(x, top_k=2)  # the status is cleared by every call
+
+
+# ---- nn-core OCP MXFP4 layout (crates/nn-core/src/layers/quantized/mxfp4.rs) -------------
+
+
+def test_ocp_dequant_bit_exact(O, dev):
+    """nnq_dequant_mxfp4_ocp against the oracle's dequantize_tensor, f32 bit patterns
+    equal: random codes under every shared_exp 0..254 (byte 0 is 2^-127, subnormal
+    results included), a length that ends inside a block; shared_exp 255 scales by +inf
+    (infinities equal, NaN where the code is a zero)."""
+    import nn_amd
+    rng = np.random.default_rng(11)
+    nb = 255 * 4
+    blocks = rng.integers(0, 256, (nb, 17), dtype=np.uint8)
+    blocks[:, 0] = np.arange(nb) % 255
+    n = nb * 32 - 13
+    got = nn_amd.dequantize_mxfp4_ocp(blocks.ravel(), n).cpu().numpy()
+    ref = O.ocp_dequantize(blocks.ravel(), n)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    inf_blocks = rng.integers(0, 256, (8, 17), dtype=np.uint8)
+    inf_blocks[:, 0] = 255
+    got = nn_amd.dequantize_mxfp4_ocp(inf_blocks.ravel(), 256).cpu().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = O.ocp_dequantize(inf_blocks.ravel(), 256)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
+
+
+def make_layer_ocp(E, H, I, seed):
+    import nn_amd
+    gb_ = nn_amd.quantize_mxfp4_ocp(nn_amd.synth_normal(seed, 1, (E, H, 2 * I), 0.02))
+    db_ = nn_amd.quantize_mxfp4_ocp(nn_amd.synth_normal(seed, 2, (E, I, H), 0.02))
+    return dict(gblk=gb_, dblk=db_, gb=nn_amd.synth_normal(seed, 3, (E, 2 * I), 0.02),
+                db=nn_amd.synth_normal(seed, 4, (E, H), 0.02))
+
+
+def ref_f64_ocp(O, x, logits, k, L, E, H, I, limit=7.0):
+    """moe_forward with the oracle's routing and the OCP decode, expert math in f64."""
+    probs = O.softmax_rows(logits)
+    tw, ti = O.topk_rows(probs, k)
+    tw = (tw / tw.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    out = np.zeros((x.shape[0], H), np.float64)
+    gper, dper = H * 2 * I, I * H
+    Wg_all = O.ocp_dequantize(L["gblk"], E * gper).reshape(E, H, 2 * I).astype(np.float64)
+    Wd_all = O.ocp_dequantize(L["dblk"], E * dper).reshape(E, I, H).astype(np.float64)
+    for e in range(E):
+        rows = [(t, s) for t in range(x.shape[0]) for s in range(k) if ti[t, s] == e]
+        if not rows:
+            continue
+        toks = np.array([t for t, _ in rows])
+        w = np.array([tw[t, s] for t, s in rows], np.float64)
+        gu = x[toks].astype(np.float64) @ Wg_all[e] + L["gb"][e].astype(np.float64)
+        g, u = gu[:, :I], gu[:, I:]
+        h = np.clip(g / (1.0 + np.exp(-g)), -limit, limit) * u
+        out[toks] += w[:, None] * (h @ Wd_all[e] + L["db"][e].astype(np.float64))
+    return out.astype(np.float32), ti, tw
+
+
+@pytest.mark.parametrize("E,H,I,T,k,xdt", [(8, 256, 320, 64, 4, "bf16"), (6, 128, 96, 40, 3, "f32"),
+                                          (4, 96, 64, 130, 2, "bf16")])
+def test_moe_ocp_vs_oracle(O, dev, E, H, I, T, k, xdt):
+    """The MoE layer on nn-core OCP MXFP4 experts (nnq_moe_create_ocp): routing equal to
+    the oracle's, outputs within the linear bars of the oracle's OCP decode with the
+    expert math in f64, and each expert's device decode bit-exact with dequantize_tensor,
+    with some blocks forced to shared_exp 0 (2^-127)."""
+    import nn_amd
+    L = make_layer_ocp(E, H, I, seed=E * 5 + I)
+    L["gblk"].reshape(-1, 17)[::97, 0] = 0
+    moe = nn_amd.QuantizedMoE.from_ocp(E, H, I, L["gblk"], L["gb"], L["dblk"], L["db"])
+    x = torch.from_numpy(nn_amd.synth_normal(13, 5, (T, H), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    logits = torch.from_numpy(nn_amd.synth_normal(13, 6, (T, E), 1.0)).to(dev)
+    y, ti, tw = moe.forward(x, logits, top_k=k, return_routing=True)
+    ref, rti, rtw = ref_f64_ocp(O, x.float().cpu().numpy(), logits.cpu().numpy(), k, L, E, H, I)
+    assert np.array_equal(ti.cpu().numpy().astype(np.uint32), rti), "routing differs"
+    assert np.allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    check_close(ref, y.cpu().numpy(), f"moe ocp E={E} H={H} I={I} T={T} k={k} x={xdt}")
+    gper, dper = H * 2 * I, I * H
+    Wg = O.ocp_dequantize(L["gblk"], E * gper).reshape(E, H, 2 * I)
+    Wd = O.ocp_dequantize(L["dblk"], E * dper).reshape(E, I, H)
+    for e in (0, E - 1):
+        gu, dn = moe.dequant_expert(e)
+        assert np.array_equal(gu.cpu().numpy().view(np.uint32), Wg[e].view(np.uint32))
+        assert np.array_equal(dn.cpu().numpy().view(np.uint32), Wd[e].view(np.uint32))

@@ -662,3 +662,124 @@ def test_sample_token_top_k_none_keeps_pos_inf(O):
         counts[O.sample_token(lg, temperature=1.0, top_k=10, top_p=None, seed=s)] += 1
     assert counts[1] == 0 and counts[4] == 0
     assert np.abs(counts[[0, 2, 3]] / 10000.0 - p).max() <= 2e-4
+
+
+# ---- nn-core OCP MXFP4 (crates/nn-core/src/layers/quantized/mxfp4.rs) ------------
+
+
+def _ocp_block(O, values):
+    v = np.zeros(32, np.float32)
+    v[:len(values)] = values
+    return O.ocp_quantize(v), v
+
+
+def test_ocp_mxfp4_reference_cases(O):
+    """The reference's own tests (crates/nn-core/src/layers/quantized/mxfp4_tests.rs)
+    restated through the oracle's block and tensor functions."""
+    b, _ = _ocp_block(O, [])
+    assert b[0] == 0 and (O.ocp_dequantize(b, 32) == 0).all()  # zeros, shared_exp 0 (:10-18, :330-335)
+    v = (np.arange(32, dtype=np.float32) / 31.0) * 2.0 - 1.0  # [-1, 1] round trip (:22-51)
+    out = O.ocp_dequantize(O.ocp_quantize(v), 32)
+    assert np.isfinite(out).all() and np.abs(out - v).max() < 1.0
+    v = (np.arange(32, dtype=np.float32) - 16.0) * 100.0  # large values stay finite (:54-66)
+    assert np.isfinite(O.ocp_dequantize(O.ocp_quantize(v), 32)).all()
+    out = O.ocp_dequantize(O.ocp_quantize(np.full(32, 3.14, np.float32)), 32)  # constant block (:69-90)
+    assert (out == out[0]).all() and abs(out[0] - 3.14) < 2.0
+    v = -(np.arange(32, dtype=np.float32) + 1.0) * 0.1  # negatives stay non-positive (:93-107)
+    assert (O.ocp_dequantize(O.ocp_quantize(v), 32) <= 0.0).all()
+    b, _ = _ocp_block(O, [1e10, 1e-10])  # dynamic range: the tiny value becomes 0 (:112-131)
+    out = O.ocp_dequantize(b, 32)
+    assert np.isfinite(out[:2]).all() and out[1] == 0.0
+    for bad in (np.nan, np.inf, -np.inf):  # non-finite rejected (:136-166, :232-236)
+        v = np.zeros(64, np.float32)
+        v[33] = bad
+        with pytest.raises(O.OracleError):
+            O.ocp_quantize(v)
+    # tensor lengths: 64 -> 2 blocks, 50 -> 2 (padded), 1 -> 1, 0 -> 0 (:169-228)
+    for n, nb in ((64, 2), (50, 2), (1, 1), (0, 0)):
+        data = (np.arange(n, dtype=np.float32) - n / 2) * 0.1
+        b = O.ocp_quantize(data)
+        assert b.size == nb * 17
+        assert O.ocp_dequantize(b, n).shape == (n,)
+    assert O.ocp_quantize(np.ones(1024, np.float32)).size == 32 * 17  # 544 bytes (:241-252)
+    # the eight magnitudes round-trip exactly at scale 1 (shared_exp 127), both signs (:258-283)
+    for m in (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0):
+        assert O.ocp_decode(O.ocp_encode(m, 1.0), 1.0) == m
+        if m:
+            assert O.ocp_decode(O.ocp_encode(-m, 1.0), 1.0) == -m
+    assert O.ocp_encode(42.0, 0.0) == 0  # zero scale encodes 0 (:286-290)
+    assert O.ocp_block_scale(127) == 1.0 and O.ocp_block_scale(128) == 2.0 and O.ocp_block_scale(126) == 0.5
+    assert 0.0 < O.ocp_block_scale(0) < np.inf  # (:293-303)
+    v = np.array([(1 if i % 2 == 0 else -1) * (i + 1) * 0.5 for i in range(32)], np.float32)  # signs (:306-333)
+    out = O.ocp_dequantize(O.ocp_quantize(v), 32)
+    assert ((v > 0) <= (out >= 0)).all() and ((v < 0) <= (out <= 0)).all()
+    v = np.zeros(32, np.float32)
+    v[:2] = (1.0, -1.0)  # unit range: the scale holds max |v| = 1 (:343-362)
+    assert 6.0 * O.ocp_block_scale(O.ocp_shared_exp(v)) >= 1.0
+
+
+def test_ocp_mxfp4_kani_invariants_exhaustive(O):
+    """The Kani harnesses' properties (mxfp4.rs:350-770, kani_mxfp4_extra.rs), checked
+    over every input they quantify: each scale byte 0..254 is a positive finite power of
+    two with scale(127) = 1 and scale(e + 1) = 2 scale(e), and byte 0 is exactly 2^-127
+    (the f64 computation keeps the f32 subnormal); codes 0..7 decode monotonically to
+    the magnitudes <= 6, code 8 + i is the negation of code i, codes 0 and 8 are zeros;
+    and every (scale byte, code) pair decodes to the exact value magnitude * 2^(e - 127)
+    (closed form in f64, rounded once)."""
+    mags = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    assert O.ocp_block_scale(0) == np.float32(2.0 ** -127)
+    for e in range(255):
+        s = O.ocp_block_scale(e)
+        assert 0.0 < s < np.inf and np.frexp(s)[0] == 0.5
+        if e < 254:
+            assert O.ocp_block_scale(e + 1) == 2.0 * s
+        prev = -1.0
+        for code in range(16):
+            got = O.ocp_decode(code, s)
+            want = np.float32((-1.0 if code & 8 else 1.0) * mags[code & 7] * 2.0 ** (e - 127))
+            assert np.float32(got).view(np.uint32) == want.view(np.uint32), (e, code)
+            if code < 8:
+                assert got >= prev and got <= np.float32(6.0) * np.float32(s)  # f32: 6 * 2^127 is +inf
+                prev = got
+    assert O.ocp_block_scale(127) == 1.0 and O.ocp_block_scale(255) == np.inf
+    # nibble independence: the low nibble holds the even element, the high the odd one
+    for code_lo in range(16):
+        for code_hi in range(16):
+            v = np.zeros(32, np.float32)
+            v[0], v[1] = O.ocp_decode(code_lo, 1.0), O.ocp_decode(code_hi, 1.0)
+            v[2] = 6.0  # fixes shared_exp at 127 (6 / 6 = 1 -> log2 0)
+            b = O.ocp_quantize(v)
+            # encode_e1m2 gives code 0 for either zero (:99-101), so code 8 re-encodes as 0
+            lo, hi = (code_lo if code_lo & 7 else 0), (code_hi if code_hi & 7 else 0)
+            assert b[0] == 127 and b[1] == (hi << 4) | lo, (code_lo, code_hi)
+
+
+def test_ocp_mxfp4_shared_exp_brute_force(O):
+    """compute_shared_exponent (mxfp4.rs:142-170) against an f64 brute force over 2000
+    block maxima across the whole range: the smallest e with max |v| <= 6 * 2^(e - 127),
+    clamped to [0, 254] (away from the few maxima where log2f rounding decides), and
+    every value's code is its nearest magnitude at that scale (ties to the lower)."""
+    rng = np.random.default_rng(7)
+    mags = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+    for _ in range(2000):
+        mx = np.float32(6.0 * 2.0 ** rng.uniform(-140, 130))
+        if not np.isfinite(mx) or mx == 0:
+            continue
+        v = (rng.uniform(-1, 1, 32) * mx).astype(np.float32)
+        v[rng.integers(32)] = mx
+        e = O.ocp_shared_exp(v)
+        amax = float(np.abs(v).max())
+        want = int(np.ceil(np.log2(amax / 6.0))) + 127
+        r = np.log2(amax / 6.0)
+        if abs(r - round(r)) > 1e-5:
+            assert e == min(max(want, 0), 254), (amax, e, want)
+        s = O.ocp_block_scale(e)
+        b = O.ocp_quantize(v)
+        assert b[0] == e
+        for i in range(32):
+            code = (b[1 + i // 2] >> (4 * (i % 2))) & 15
+            q = abs(float(np.float32(abs(v[i]) / np.float32(s))))
+            d = np.abs(q - mags)
+            best = int(np.argmin(d)) if v[i] != 0 else 0
+            assert code & 7 == best, (i, v[i], q, code)
+            assert (code >> 3) == (1 if v[i] < 0 else 0)
