@@ -256,7 +256,9 @@ int nnq_moe_destroy(nnq_moe *moe);
 /* y[t, hidden] (f32) = MoE(x[t, hidden]) with router logits [t, E] (f32):
  * softmax -> top_k -> renormalise -> per expert clamp(silu(x@Wg+bg), -limit, limit)
  * * (x@Wu+bu) -> @Wd + bd -> weighted sum.  x: NNQ_F32 or NNQ_BF16, 16-byte aligned;
- * tokens * top_k <= 16384, top_k <= 8.  Routing, permutation and combine run on the
+ * any number of tokens (batches beyond 16384 token-expert assignments run as token
+ * chunks of that size, one after another on the stream), top_k <= 8.  Routing,
+ * permutation and combine run on the
  * device (no host synchronisation); the expert outputs are summed per token in
  * ascending expert order, as moe_forward's index_add does.
  * Optional outputs topk_idx [t, top_k] u32 and topk_w [t, top_k] f32 (device).

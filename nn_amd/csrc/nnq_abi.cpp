@@ -68,6 +68,9 @@ int hip_fail(hipError_t e, const char *what) {
         if (_e != hipSuccess) return hip_fail(_e, what); \
     } while (0)
 
+// token-expert assignments per MoE launch sequence; longer batches run in token chunks
+constexpr int64_t kMoeChunkAssign = 16384;
+
 size_t block_elems(int fmt) { return fmt == NNQ_FMT_Q8_0 ? 32 : 256; }
 size_t block_bytes(int fmt) {
     switch (fmt) {
@@ -156,6 +159,14 @@ struct Scratch {
         return stream_workspace(st, n ? n : 16, &p, &owned);
     }
 };
+
+inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// The kernels load activations as 16-byte vectors and store outputs as 4-byte words (or
+// wider); an input or output at an address that does not allow that (a narrowed view)
+// goes through the call's workspace with a device copy.
+inline bool misaligned_in(const void *p) { return ((uintptr_t)p & 15) != 0; }
+inline bool misaligned_out(const void *p) { return ((uintptr_t)p & 3) != 0; }
 
 template <class F>
 void parallel_for(int64_t n, F &&fn) {
@@ -317,8 +328,6 @@ static int check_linear(const nnq_weight *w, const void *x, nnq_dtype xd, int64_
     if (m > 0 && (!x || !y)) return fail(NNQ_ERR_INVALID_ARGUMENT, "x or y is null");
     if (xd != NNQ_F32 && xd != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d (f32 or bf16)", (int)xd);
     if (yd != NNQ_F32 && yd != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "output dtype %d (f32 or bf16)", (int)yd);
-    if ((uintptr_t)x & 15) return fail(NNQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
-    if ((uintptr_t)y & 3) return fail(NNQ_ERR_INVALID_ARGUMENT, "y must be 4-byte aligned");
     return NNQ_OK;
 }
 
@@ -411,7 +420,22 @@ int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m,
                int64_t bias_len, void *y, nnq_dtype y_dtype, void *stream) {
     int rc = check_linear(w, x, x_dtype, m, k, bias, bias_len, y, y_dtype);
     if (rc) return rc;
-    return dispatch_linear(w, x, x_dtype, m, bias, y, y_dtype, stream);
+    if (m == 0) return NNQ_OK;
+    const bool xm = misaligned_in(x), ym = misaligned_out(y);
+    if (!xm && !ym) return dispatch_linear(w, x, x_dtype, m, bias, y, y_dtype, stream);
+    const hipStream_t st = (hipStream_t)stream;
+    const size_t xbytes = (size_t)m * k * (x_dtype == NNQ_BF16 ? 2 : 4);
+    const size_t ybytes = (size_t)m * w->L.n * (y_dtype == NNQ_BF16 ? 2 : 4);
+    const size_t xb = xm ? al256(xbytes) : 0, yb = ym ? al256(ybytes) : 0, lb = linear_scratch_bytes(w, m, x_dtype);
+    Scratch s;
+    HIP_TRY(s.alloc(xb + yb + lb, st), "scratch alloc");
+    uint8_t *base = reinterpret_cast<uint8_t *>(s.p);
+    if (xm) HIP_TRY(hipMemcpyAsync(base, x, xbytes, hipMemcpyDeviceToDevice, st), "stage x");
+    rc = dispatch_linear(w, xm ? base : x, x_dtype, m, bias, ym ? base + xb : y, y_dtype, stream, 0, nullptr, 0,
+                         lb ? base + xb + yb : nullptr);
+    if (rc) return rc;
+    if (ym) HIP_TRY(hipMemcpyAsync(y, base + xb, ybytes, hipMemcpyDeviceToDevice, st), "copy y out");
+    return NNQ_OK;
 }
 
 int nnq_argmax_f32(const float *logits, int64_t n, uint32_t *idx, int32_t *status_dev, void *stream) {
@@ -431,9 +455,18 @@ int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const floa
     int rc = check_linear(w, x, NNQ_F32, 1, k, bias, bias_len, logits, NNQ_F32);
     if (rc) return rc;
     if (!idx) return fail(NNQ_ERR_INVALID_ARGUMENT, "idx is null");
+    if (misaligned_out(logits)) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits must be 4-byte aligned");
     const Layout &L = w->L;
+    const size_t kb = al256((size_t)L.ntile * sizeof(unsigned long long));
+    const bool xm = misaligned_in(x);
     Scratch s;
-    HIP_TRY(s.alloc((size_t)L.ntile * sizeof(unsigned long long), (hipStream_t)stream), "scratch alloc");
+    HIP_TRY(s.alloc(kb + (xm ? (size_t)k * 4 : 0), (hipStream_t)stream), "scratch alloc");
+    if (xm) {
+        HIP_TRY(hipMemcpyAsync(reinterpret_cast<uint8_t *>(s.p) + kb, x, (size_t)k * 4, hipMemcpyDeviceToDevice,
+                               (hipStream_t)stream),
+                "stage x");
+        x = reinterpret_cast<const float *>(reinterpret_cast<uint8_t *>(s.p) + kb);
+    }
     GemvArgs a{};
     a.qs = w->dev;
     a.hdr = w->dev + L.qs_bytes;
@@ -564,17 +597,30 @@ int nnq_moe_forward(const nnq_moe *m, const void *x, nnq_dtype x_dtype, int64_t 
     if (x_dtype != NNQ_F32 && x_dtype != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d", (int)x_dtype);
     if (tokens == 0) return NNQ_OK;
     if (!x || !router_logits || !y) return fail(NNQ_ERR_INVALID_ARGUMENT, "null pointer");
-    if ((uintptr_t)x & 15) return fail(NNQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
-    if (tokens * top_k > 16384)
-        return fail(NNQ_ERR_UNSUPPORTED, "at most 16384 token-expert assignments per call (%lld)",
-                    (long long)(tokens * top_k));
+    if (misaligned_out(y) || misaligned_out(router_logits))
+        return fail(NNQ_ERR_INVALID_ARGUMENT, "y and router_logits must be 4-byte aligned");
+    // tokens are routed independently, so a long batch runs as chunks of at most
+    // kMoeChunkAssign token-expert assignments, one after another on the stream
+    const int64_t tc = std::min<int64_t>(tokens, kMoeChunkAssign / top_k);
+    const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, xbytes = (size_t)tokens * m->d.H * xe;
+    const size_t msb = al256(moe_scratch_bytes(tc, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16));
+    const bool xm = misaligned_in(x);
     Scratch s;
-    HIP_TRY(s.alloc(moe_scratch_bytes(tokens, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16),
-                    (hipStream_t)stream),
-            "scratch alloc");
-    int e = launch_moe(m->d, x, x_dtype == NNQ_BF16, tokens, router_logits, 1, nullptr, top_k, swiglu_limit, y,
-                       topk_idx, topk_w, nullptr, s.p, stream);
-    if (e) return hip_fail((hipError_t)e, "moe launch");
+    HIP_TRY(s.alloc(msb + (xm ? xbytes : 0), (hipStream_t)stream), "scratch alloc");
+    if (xm) {
+        HIP_TRY(hipMemcpyAsync(reinterpret_cast<uint8_t *>(s.p) + msb, x, xbytes, hipMemcpyDeviceToDevice,
+                               (hipStream_t)stream),
+                "stage x");
+        x = reinterpret_cast<uint8_t *>(s.p) + msb;
+    }
+    for (int64_t t0 = 0; t0 < tokens; t0 += tc) {
+        const int64_t n = std::min(tc, tokens - t0);
+        int e = launch_moe(m->d, (const uint8_t *)x + (size_t)t0 * m->d.H * xe, x_dtype == NNQ_BF16, n,
+                           router_logits + t0 * m->d.E, 1, nullptr, top_k, swiglu_limit, y + t0 * m->d.H,
+                           topk_idx ? topk_idx + t0 * top_k : nullptr, topk_w ? topk_w + t0 * top_k : nullptr, nullptr,
+                           s.p, stream);
+        if (e) return hip_fail((hipError_t)e, "moe launch");
+    }
     return NNQ_OK;
 }
 
@@ -639,28 +685,15 @@ int nnq_mlp_destroy(nnq_mlp *p) {
     return NNQ_OK;
 }
 
-int nnq_mlp_forward(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t m, int64_t k, void *y,
-                    nnq_dtype y_dtype, int32_t *status_dev, void *stream) {
-    if (!p) return fail(NNQ_ERR_INVALID_ARGUMENT, "MLP handle is null");
-    int rc = check_linear(p->gu, x, x_dtype, m, k, nullptr, 0, y, y_dtype);
-    if (rc) return rc;
-    if (m == 0) return NNQ_OK;
+}  // extern "C"
+
+// the MLP's launches on prepared pointers (nnq_mlp_forward)
+static int mlp_run(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t m, void *y, nnq_dtype y_dtype,
+                   int32_t *status_dev, void *stream, uint8_t *base, size_t gu_bytes, void *lin, bool fused,
+                   bool hout) {
     const int64_t I = p->inter;
-    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    // m <= 2: interleaved Q4_K gate | up -> the GEMV writes h = silu(gate) * up and the
-    // down GEMV reads h; otherwise the down GEMV takes gate | up and applies SwiGLU while
-    // staging.  m > 2: linear, swiglu_kernel, linear.
-    const bool fused = m <= 2, hout = fused && p->interleaved8;
-    // one scratch: gate | up [m, 2I] f32 (h [m, I] when hout), h [m, I] f32, then the GEMM
-    // scratch of either linear
-    const size_t gu_bytes = al((size_t)m * (hout ? 1 : 2) * I * 4), h_bytes = fused ? 0 : al((size_t)m * I * 4);
-    const size_t lin_bytes =
-        std::max(linear_scratch_bytes(p->gu, m, x_dtype), fused ? 0 : linear_scratch_bytes(p->down, m, NNQ_F32));
-    Scratch s;
-    HIP_TRY(s.alloc(gu_bytes + h_bytes + lin_bytes, (hipStream_t)stream), "scratch alloc");
-    uint8_t *base = reinterpret_cast<uint8_t *>(s.p);
+    int rc = 0;
     float *gu = reinterpret_cast<float *>(base);
-    void *lin = lin_bytes ? base + gu_bytes + h_bytes : nullptr;
     rc = dispatch_linear(p->gu, x, x_dtype, m, nullptr, gu, NNQ_F32, stream, 0, status_dev, fused ? 1 : 0, lin,
                          hout ? 1 : 0);
     if (rc) return rc;
@@ -675,6 +708,46 @@ int nnq_mlp_forward(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t 
         e = launch_nonfinite_check(y, y_dtype == NNQ_BF16, m * p->hidden, status_dev, stream);
         if (e) return hip_fail((hipError_t)e, "output check launch");
     }
+    return NNQ_OK;
+}
+
+extern "C" {
+
+int nnq_mlp_forward(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t m, int64_t k, void *y,
+                    nnq_dtype y_dtype, int32_t *status_dev, void *stream) {
+    if (!p) return fail(NNQ_ERR_INVALID_ARGUMENT, "MLP handle is null");
+    int rc = check_linear(p->gu, x, x_dtype, m, k, nullptr, 0, y, y_dtype);
+    if (rc) return rc;
+    if (m == 0) return NNQ_OK;
+    const int64_t I = p->inter;
+    auto al = [](size_t v) { return al256(v); };
+    // m <= 2: interleaved Q4_K gate | up -> the GEMV writes h = silu(gate) * up and the
+    // down GEMV reads h; otherwise the down GEMV takes gate | up and applies SwiGLU while
+    // staging.  m > 2: linear, swiglu_kernel, linear.
+    const bool fused = m <= 2, hout = fused && p->interleaved8;
+    // one scratch: gate | up [m, 2I] f32 (h [m, I] when hout), h [m, I] f32, then the GEMM
+    // scratch of either linear
+    const size_t gu_bytes = al((size_t)m * (hout ? 1 : 2) * I * 4), h_bytes = fused ? 0 : al((size_t)m * I * 4);
+    const size_t lin_bytes =
+        std::max(linear_scratch_bytes(p->gu, m, x_dtype), fused ? 0 : linear_scratch_bytes(p->down, m, NNQ_F32));
+    // a misaligned x or y goes through the workspace (after the other regions)
+    const size_t xbytes = (size_t)m * k * (x_dtype == NNQ_BF16 ? 2 : 4);
+    const size_t ybytes = (size_t)m * p->hidden * (y_dtype == NNQ_BF16 ? 2 : 4);
+    const bool xm = misaligned_in(x), ym = misaligned_out(y);
+    const size_t main_bytes = gu_bytes + h_bytes + al256(lin_bytes);
+    Scratch s;
+    HIP_TRY(s.alloc(main_bytes + (xm ? al256(xbytes) : 0) + (ym ? ybytes : 0), (hipStream_t)stream), "scratch alloc");
+    uint8_t *base = reinterpret_cast<uint8_t *>(s.p);
+    void *lin = lin_bytes ? base + gu_bytes + h_bytes : nullptr;
+    void *const y_user = y;
+    if (xm) {
+        HIP_TRY(hipMemcpyAsync(base + main_bytes, x, xbytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "stage x");
+        x = base + main_bytes;
+    }
+    if (ym) y = base + main_bytes + (xm ? al256(xbytes) : 0);
+    rc = mlp_run(p, x, x_dtype, m, y, y_dtype, status_dev, stream, base, gu_bytes, lin, fused, hout);
+    if (rc) return rc;
+    if (ym) HIP_TRY(hipMemcpyAsync(y_user, y, ybytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "copy y out");
     return NNQ_OK;
 }
 
@@ -721,7 +794,13 @@ static int check_router_input(const nnq_router *r, const void *x, nnq_dtype x_dt
     if (tokens < 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "tokens < 0");
     if (x_dtype != NNQ_F32 && x_dtype != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d", (int)x_dtype);
     if (tokens > 0 && !x) return fail(NNQ_ERR_INVALID_ARGUMENT, "x is null");
-    if ((uintptr_t)x & 15) return fail(NNQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    return NNQ_OK;
+}
+
+// a misaligned x of the router / MoE block copied to `dst` (the call's workspace)
+static int stage_tokens(const void **x, size_t bytes, uint8_t *dst, void *stream) {
+    HIP_TRY(hipMemcpyAsync(dst, *x, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "stage x");
+    *x = dst;
     return NNQ_OK;
 }
 
@@ -731,9 +810,13 @@ int nnq_router_logits(const nnq_router *r, const void *x, nnq_dtype x_dtype, int
     if (rc) return rc;
     if (tokens == 0) return NNQ_OK;
     if (!logits) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits is null");
+    if (misaligned_out(logits)) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits must be 4-byte aligned");
     const size_t pb = router_partial_bytes(tokens, r->H, (int)r->E);
+    const size_t xbytes = (size_t)tokens * r->H * (x_dtype == NNQ_BF16 ? 2 : 4);
+    const bool xm = misaligned_in(x);
     Scratch s;
-    if (pb) HIP_TRY(s.alloc(pb, (hipStream_t)stream), "scratch alloc");
+    if (pb || xm) HIP_TRY(s.alloc(al256(pb) + (xm ? xbytes : 0), (hipStream_t)stream), "scratch alloc");
+    if (xm && (rc = stage_tokens(&x, xbytes, reinterpret_cast<uint8_t *>(s.p) + al256(pb), stream))) return rc;
     int ks = 1;
     int e = launch_router_logits(x, x_dtype == NNQ_BF16, tokens, r->H, r->w, r->b, (int)r->E,
                                  pb ? reinterpret_cast<float *>(s.p) : logits, &ks, nullptr, stream);
@@ -758,25 +841,34 @@ int nnq_moe_block_forward(const nnq_moe *m, const nnq_router *r, const void *x, 
         return fail(NNQ_ERR_INVALID_SHAPE, "topk k=%d out of range for %lld experts", top_k, (long long)m->d.E);
     if (tokens == 0) return NNQ_OK;
     if (!y) return fail(NNQ_ERR_INVALID_ARGUMENT, "y is null");
-    if (tokens * top_k > 16384)
-        return fail(NNQ_ERR_UNSUPPORTED, "at most 16384 token-expert assignments per call (%lld)",
-                    (long long)(tokens * top_k));
-    const size_t lg_bytes =
-        (std::max(router_partial_bytes(tokens, r->H, (int)r->E), (size_t)tokens * m->d.E * 4) + 255) & ~(size_t)255;
+    if (misaligned_out(y)) return fail(NNQ_ERR_INVALID_ARGUMENT, "y must be 4-byte aligned");
+    // chunks of at most kMoeChunkAssign token-expert assignments (tokens are independent)
+    const int64_t tc = std::min<int64_t>(tokens, kMoeChunkAssign / top_k);
+    const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, xbytes = (size_t)tokens * m->d.H * xe;
+    const size_t lg_bytes = al256(std::max(router_partial_bytes(tc, r->H, (int)r->E), (size_t)tc * m->d.E * 4));
+    const size_t msb = al256(moe_scratch_bytes(tc, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16));
+    const bool xm = misaligned_in(x);
     Scratch s;
-    HIP_TRY(s.alloc(lg_bytes + moe_scratch_bytes(tokens, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16),
-                    (hipStream_t)stream),
-            "scratch alloc");
+    HIP_TRY(s.alloc(lg_bytes + msb + (xm ? xbytes : 0), (hipStream_t)stream), "scratch alloc");
+    if (xm && (rc = stage_tokens(&x, xbytes, reinterpret_cast<uint8_t *>(s.p) + lg_bytes + msb, stream))) return rc;
     float *logits = reinterpret_cast<float *>(s.p);
-    int ks = 1;
-    int e = launch_router_logits(x, x_dtype == NNQ_BF16, tokens, r->H, r->w, r->b, (int)r->E, logits, &ks, status_dev,
-                                 stream);
-    if (e) return hip_fail((hipError_t)e, "router launch");
-    // the routing kernel sums the K-part slabs and adds the bias (with one part the
-    // router kernel already did)
-    e = launch_moe(m->d, x, x_dtype == NNQ_BF16, tokens, logits, ks, ks > 1 ? r->b : nullptr, top_k, swiglu_limit, y,
-                   topk_idx, topk_w, status_dev, reinterpret_cast<uint8_t *>(s.p) + lg_bytes, stream);
-    if (e) return hip_fail((hipError_t)e, "moe launch");
+    for (int64_t t0 = 0; t0 < tokens; t0 += tc) {
+        const int64_t n = std::min(tc, tokens - t0);
+        const void *xc = (const uint8_t *)x + (size_t)t0 * m->d.H * xe;
+        int ks = 1;
+        // the router clears the status of the call, so only the first chunk passes it; every
+        // chunk's combine flags a non-finite output
+        int e = launch_router_logits(xc, x_dtype == NNQ_BF16, n, r->H, r->w, r->b, (int)r->E, logits, &ks,
+                                     t0 == 0 ? status_dev : nullptr, stream);
+        if (e) return hip_fail((hipError_t)e, "router launch");
+        // the routing kernel sums the K-part slabs and adds the bias (with one part the
+        // router kernel already did)
+        e = launch_moe(m->d, xc, x_dtype == NNQ_BF16, n, logits, ks, ks > 1 ? r->b : nullptr, top_k, swiglu_limit,
+                       y + t0 * m->d.H, topk_idx ? topk_idx + t0 * top_k : nullptr,
+                       topk_w ? topk_w + t0 * top_k : nullptr, status_dev,
+                       reinterpret_cast<uint8_t *>(s.p) + lg_bytes, stream);
+        if (e) return hip_fail((hipError_t)e, "moe launch");
+    }
     return NNQ_OK;
 }
 
@@ -837,6 +929,13 @@ int nnq_linear_sample(const nnq_weight *w, const float *x, int64_t k, const floa
     if (rc) return rc;
     rc = check_sampling(cfg, past_tokens, n_past, token);
     if (rc) return rc;
+    if (misaligned_out(logits)) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits must be 4-byte aligned");
+    Scratch xs;  // a misaligned x: staged in the workspace, read by the GEMV before the sampling reuses it
+    if (misaligned_in(x)) {
+        HIP_TRY(xs.alloc((size_t)k * 4, (hipStream_t)stream), "scratch alloc");
+        HIP_TRY(hipMemcpyAsync(xs.p, x, (size_t)k * 4, hipMemcpyDeviceToDevice, (hipStream_t)stream), "stage x");
+        x = reinterpret_cast<const float *>(xs.p);
+    }
     rc = dispatch_linear(w, x, NNQ_F32, 1, bias, logits, NNQ_F32, stream);
     if (rc) return rc;
     return run_sample(logits, w->L.n, past_tokens, n_past, cfg, token, stream);
@@ -849,6 +948,9 @@ int nnq_linear_sample_noalloc(const nnq_weight *w, const float *x, int64_t k, co
     if (rc) return rc;
     rc = check_sampling(cfg, past_tokens, n_past, token);
     if (rc) return rc;
+    if (misaligned_in(x) || misaligned_out(logits))
+        return fail(NNQ_ERR_INVALID_ARGUMENT,
+                    "x must be 16-byte and logits 4-byte aligned (this entry point has no workspace to stage them)");
     int64_t kk = 0;
     rc = sample_k(cfg, w->L.n, &kk);
     if (rc) return rc;

@@ -360,3 +360,43 @@ def test_host_bias_moves_to_the_device(O, dev):
     assert torch.equal(lh, ld) and int(th) == int(td)
     ref = oracle_linear(O, "q6_k", b, n, k, x.cpu().numpy()) + bias_h.numpy()
     check_close(ref, ld.cpu().numpy()[None, :], "q6_k linear + host bias")
+
+
+@pytest.mark.parametrize("fmt,m", [("q4_k", 1), ("q4_k", 40), ("q6_k", 3), ("q8_0", 12)])
+def test_misaligned_views(O, dev, fmt, m):
+    """Narrowed views whose data pointer is not 16-byte aligned (an f32 row offset by one
+    element, a bf16 one by one element) are staged through the workspace: the results
+    equal those of the same values at aligned addresses, bit for bit; an output pointer
+    offset by 2 bytes (bf16) is computed in the workspace and copied out."""
+    import ctypes
+
+    import nn_amd
+    from nn_amd import _lib
+    n, k = 256, 1024
+    b = quantized_weight_bytes(fmt, n, k, seed=5 + m, O=O)
+    w = make_weight(fmt, b, n, k)
+    for dt in (torch.float32, torch.bfloat16):
+        x = torch.from_numpy(nn_amd.synth_normal(7 + m, 2, (m, k), 1.0)).to(dev).to(dt)
+        big = torch.zeros(m * k + 8, dtype=dt, device=dev)
+        big[1:1 + m * k] = x.reshape(-1)
+        xv = big[1:1 + m * k].view(m, k)
+        assert xv.data_ptr() % 16 != 0
+        assert torch.equal(nn_amd.quantized_linear(xv, w), nn_amd.quantized_linear(x, w))
+        ybig = torch.zeros(m * n + 8, dtype=torch.bfloat16, device=dev)
+        yv = ybig[1:1 + m * n]
+        rc = _lib.load().nnq_linear(w.handle, ctypes.c_void_p(xv.data_ptr()), 2 if dt == torch.bfloat16 else 0, m, k,
+                                    None, 0, ctypes.c_void_p(yv.data_ptr()), 2,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0, _lib.last_error()
+        ref = nn_amd.quantized_linear(x, w, out_dtype=torch.bfloat16).reshape(-1)
+        assert torch.equal(yv, ref)
+    if m == 1:
+        x = torch.from_numpy(nn_amd.synth_normal(9, 2, (k,), 1.0)).to(dev)
+        big = torch.zeros(k + 4, device=dev)
+        big[1:1 + k] = x
+        la, ia = nn_amd.linear_argmax(big[1:1 + k], w)
+        lb, ib = nn_amd.linear_argmax(x, w)
+        assert torch.equal(la, lb) and int(ia) == int(ib)
+        la, ta = nn_amd.linear_sample(big[1:1 + k], w, seed=3)
+        lb, tb = nn_amd.linear_sample(x, w, seed=3)
+        assert torch.equal(la, lb) and int(ta) == int(tb)

@@ -116,3 +116,17 @@ def test_mlp_graph_replay(O, dev, m):
         other = mlp(x * 0.5)  # eager call between replays
         torch.cuda.synchronize()
         assert torch.isfinite(other).all()
+
+
+def test_mlp_misaligned_x(O, dev):
+    """The fused MLP on a narrowed input view (not 16-byte aligned) equals the aligned call."""
+    import nn_amd
+    H, I = 256, 512
+    g, u, d = (nn_amd.quantize_q4_k(nn_amd.synth_normal(61, j, s, 0.02)) for j, s in ((1, (I, H)), (2, (I, H)),
+                                                                                        (3, (H, I))))
+    mlp = nn_amd.QuantizedMLP(g, u, d, nn_amd.QuantType.Q4_K, H, I)
+    for m in (1, 2, 5, 20):
+        x = torch.from_numpy(nn_amd.synth_normal(62 + m, 4, (m, H), 1.0)).to(dev)
+        big = torch.zeros(m * H + 4, device=dev)
+        big[1:1 + m * H] = x.reshape(-1)
+        assert torch.equal(mlp(big[1:1 + m * H].view(m, H)), mlp(x))

@@ -316,3 +316,55 @@ def test_moe_ocp_vs_oracle(O, dev, E, H, I, T, k, xdt):
         gu, dn = moe.dequant_expert(e)
         assert np.array_equal(gu.cpu().numpy().view(np.uint32), Wg[e].view(np.uint32))
         assert np.array_equal(dn.cpu().numpy().view(np.uint32), Wd[e].view(np.uint32))
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_moe_long_batch_chunks(O, dev, xdt):
+    """Beyond 16384 token-expert assignments the layer runs in token chunks: 4500 tokens
+    at top-4 (18000 assignments, a chunk boundary at token 4096) against the oracle, with
+    the logits given and with the router on the device; a NaN in a first-chunk token still
+    raises after the second chunk (the second chunk's router must not clear the status)."""
+    import nn_amd
+    E, H, I, T, k = 8, 96, 64, 4500, 4
+    L = make_layer(E, H, I, seed=41)
+    rw, rb = make_router(E, H, seed=42)
+    moe = nn_amd.QuantizedMoE(E, H, I, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"],
+                              router_weight=rw, router_bias=rb)
+    x = torch.from_numpy(nn_amd.synth_normal(43, 5, (T, H), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    xf = x.float().cpu().numpy()
+    logits = torch.from_numpy(nn_amd.synth_normal(43, 6, (T, E), 1.0)).to(dev)
+    y, ti, tw = moe.forward(x, logits, top_k=k, return_routing=True)
+    ref, rti, rtw = O.moe_forward(xf, logits.cpu().numpy(), k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    assert np.array_equal(ti.cpu().numpy().astype(np.uint32), rti)
+    check_close(ref, y.cpu().numpy(), f"moe long batch x={xdt}")
+    yb, tib, _ = moe.block_forward(x, top_k=k, return_routing=True)
+    lg = O.router_logits(xf, rw, rb)
+    refb, rtib, _ = O.moe_forward(xf, lg, k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    assert np.array_equal(tib.cpu().numpy().astype(np.uint32), rtib)
+    check_close(refb, yb.cpu().numpy(), f"moe block long batch x={xdt}")
+    x[10, 3] = float("nan")
+    with pytest.raises(nn_amd.NonFiniteData):
+        moe.block_forward(x, top_k=k)
+
+
+def test_moe_misaligned_x(O, dev):
+    """A token batch at an address that is not 16-byte aligned (a narrowed view) gives the
+    same routing and outputs as the aligned batch, through the router and the experts."""
+    import nn_amd
+    E, H, I, T, k = 8, 96, 64, 20, 2
+    L = make_layer(E, H, I, seed=51)
+    rw, rb = make_router(E, H, seed=52)
+    moe = nn_amd.QuantizedMoE(E, H, I, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"],
+                              router_weight=rw, router_bias=rb)
+    for dt in (torch.float32, torch.bfloat16):
+        x = torch.from_numpy(nn_amd.synth_normal(53, 5, (T, H), 1.0)).to(dev).to(dt)
+        big = torch.zeros(T * H + 8, dtype=dt, device=dev)
+        big[1:1 + T * H] = x.reshape(-1)
+        xv = big[1:1 + T * H].view(T, H)
+        assert xv.data_ptr() % 16 != 0
+        logits = torch.from_numpy(nn_amd.synth_normal(53, 6, (T, E), 1.0)).to(dev)
+        assert torch.equal(moe.forward(xv, logits, top_k=k), moe.forward(x, logits, top_k=k))
+        assert torch.equal(moe.block_forward(xv, top_k=k), moe.block_forward(x, top_k=k))
+        assert torch.equal(moe.router_logits(xv), moe.router_logits(x))
