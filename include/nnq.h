@@ -16,6 +16,12 @@
  *    are asynchronous on `stream` and never synchronize the host.
  *  - Weight handles are immutable after creation and may be shared across
  *    threads and streams.
+ *  - Scratch memory: eager calls on a stream share that stream's workspace (grown
+ *    and freed stream-ordered); calls captured into a HIP graph use a workspace of
+ *    their capture sequence, so a graph may be replayed on any stream while eager
+ *    calls run elsewhere.  Two replays of one graph that overlap in time share that
+ *    graph's workspace and must be ordered by the caller.  A capture's workspace is
+ *    kept until the process ends; nnq_release_workspace frees a stream's eager one.
  *  - Weights are row-major W[n, k] (out_features x in_features) with blocks
  *    along k, as QuantizedStorage / QuantizedWeight store them
  *    (crates/nn-core/src/dyn_tensor/quantized.rs:109-172,
@@ -103,6 +109,12 @@ int nnq_init(int device);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char *nnq_last_error(void);
+
+/* Free the scratch workspace that eager calls on `stream` (current device) hold, stream-
+ * ordered on that stream; call it before destroying the stream.  No counterpart in the
+ * reference (its CPU path allocates per call); the next call on the stream allocates
+ * again. */
+int nnq_release_workspace(void *stream);
 
 /* ---- weights ------------------------------------------------------------------ */
 

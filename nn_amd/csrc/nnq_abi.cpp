@@ -81,44 +81,53 @@ size_t block_bytes(int fmt) {
     return 0;
 }
 
-// Per-(device, stream) workspace: calls on one stream run in order, so they can share
-// one buffer.  It grows by allocating a larger buffer; a replaced buffer is kept until
-// the process ends, because a graph captured earlier may still replay with it.  While a
-// stream is being captured it grows with the capture's ban on allocation relaxed for
-// this thread; where that is refused, the call takes a stream-ordered allocation.
+// Workspaces.  Calls on one stream run in order, so they can share one buffer:
+//  - eager calls use the stream's workspace (keyed by device and stream).  It grows by a
+//    stream-ordered allocation, and the buffer it replaces is freed stream-ordered, after
+//    the work already queued on the stream;
+//  - calls captured into a HIP graph use a workspace of their capture sequence (keyed by
+//    device, stream and capture id), allocated with the capture's ban on allocation calls
+//    relaxed for this thread, so the graph holds no allocation nodes.  A graph keeps
+//    reading that buffer whenever and on whatever stream it is replayed, so it is never
+//    shared with eager calls or other captures, and it is kept until the process ends
+//    (the library cannot know when the graph is destroyed).  A buffer outgrown within one
+//    capture is kept as well, since the calls captured before hold it.
+// If the relaxed allocation is refused, the call takes a stream-ordered allocation that
+// becomes nodes of the graph (freed by the graph after the call's work).
 struct Workspace {
     int dev;
     hipStream_t st;
+    unsigned long long capture;  // 0: eager
     void *p;
     size_t n;
 };
 std::mutex g_ws_mu;
 std::vector<Workspace> g_ws;
-std::vector<void *> g_ws_retired;
+std::vector<void *> g_capture_retired;
 
 hipError_t stream_workspace(hipStream_t st, size_t n, void **out, bool *owned) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    e = hipStreamGetCaptureInfo(st, &cs, &cid);
+    if (e != hipSuccess) return e;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (!capturing) cid = 0;
     std::lock_guard<std::mutex> g(g_ws_mu);
     Workspace *w = nullptr;
     for (auto &x : g_ws)
-        if (x.dev == dev && x.st == st) w = &x;
+        if (x.dev == dev && x.st == st && x.capture == cid) w = &x;
     if (w && w->n >= n) {
         *out = w->p;
         *owned = false;
         return hipSuccess;
     }
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    e = hipStreamIsCapturing(st, &cs);
-    if (e != hipSuccess) return e;
     size_t sz = std::max<size_t>(n, (size_t)1 << 20);
     if (w) sz = std::max(sz, 2 * w->n);
     void *p = nullptr;
-    if (cs != hipStreamCaptureStatusNone) {
-        // under capture this thread opts out of the capture's ban on allocation calls
-        // for the one hipMalloc (relaxed mode); if that is refused, a stream-ordered
-        // allocation of the call's own becomes a node of the graph
+    if (capturing) {
         hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
         (void)hipThreadExchangeStreamCaptureMode(&mode);
         e = hipMalloc(&p, sz);
@@ -128,19 +137,41 @@ hipError_t stream_workspace(hipStream_t st, size_t n, void **out, bool *owned) {
             *owned = true;
             return hipMallocAsync(out, n, st);
         }
+        if (w) g_capture_retired.push_back(w->p);
     } else {
-        e = hipMalloc(&p, sz);
+        e = hipMallocAsync(&p, sz, st);
         if (e != hipSuccess) return e;
+        if (w) {
+            e = hipFreeAsync(w->p, st);  // after the work queued on st that uses it
+            if (e != hipSuccess) {
+                (void)hipFreeAsync(p, st);
+                return e;
+            }
+        }
     }
     if (w) {
-        g_ws_retired.push_back(w->p);
         w->p = p;
         w->n = sz;
     } else {
-        g_ws.push_back(Workspace{dev, st, p, sz});
+        g_ws.push_back(Workspace{dev, st, cid, p, sz});
     }
     *out = p;
     *owned = false;
+    return hipSuccess;
+}
+
+// frees the eager workspace of `st` on the current device (stream-ordered on st)
+hipError_t release_stream_workspace(hipStream_t st) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> g(g_ws_mu);
+    for (size_t i = 0; i < g_ws.size(); i++)
+        if (g_ws[i].dev == dev && g_ws[i].st == st && g_ws[i].capture == 0) {
+            e = hipFreeAsync(g_ws[i].p, st);
+            g_ws.erase(g_ws.begin() + (ptrdiff_t)i);
+            return e;
+        }
     return hipSuccess;
 }
 
@@ -194,6 +225,12 @@ int nnq::set_error(int code, const char *msg) {
 extern "C" {
 
 const char *nnq_last_error(void) { return g_err.c_str(); }
+
+int nnq_release_workspace(void *stream) {
+    hipError_t e = release_stream_workspace((hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "release workspace");
+    return NNQ_OK;
+}
 
 int nnq_device_count(int *count) {
     if (!count) return fail(NNQ_ERR_INVALID_ARGUMENT, "count is null");

@@ -112,7 +112,8 @@ def test_gemm_baseline_shapes(O, dev, m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(130, 256, 4096), (256, 384, 2048), (128, 192, 256), (300, 640, 1280),
                                    (384, 1024, 4096), (128, 4096, 4096), (9, 128, 256), (17, 4096, 12288),
-                                   (40, 384, 4096), (64, 192, 2048), (33, 768, 8192), (100, 1152, 1024)])
+                                   (40, 384, 4096), (64, 192, 2048), (33, 768, 8192), (100, 1152, 1024),
+                                   (20, 576, 2048), (50, 576, 4096), (24, 1536, 4096)])
 def test_gemm_ring_edges(O, dev, m, n, k):
     """The LDS-ring kernel's edges (bf16 activations): 32-, 64- and 128-row tiles with a
     ragged last row tile, 128- and 192-wide column tiles, a single super-block, K split
@@ -158,3 +159,43 @@ def test_gemm_graph_replay(O, dev):
         other = nn_amd.quantized_linear(x, w)  # eager call on another stream's workspace
         torch.cuda.synchronize()
         assert torch.equal(other, ref)
+
+
+def test_graph_replay_on_other_stream_concurrent_with_eager(O, dev):
+    """A graph captured on stream S keeps its own scratch: replayed on stream A while eager
+    GEMMs with other inputs run on S, with no host synchronisation in between, every
+    replay and every eager call gives its own eager result.  Then the stream's eager
+    workspace is released and the next call allocates again."""
+    import ctypes
+
+    import nn_amd
+    from nn_amd import _lib
+    m, n, k = 256, 4096, 4096
+    w = make_weight("q4_k", q4k_bytes(n, k, seed=21), n, k)
+    x1 = torch.from_numpy(nn_amd.synth_normal(21, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    x2 = torch.from_numpy(nn_amd.synth_normal(22, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    ref1 = nn_amd.quantized_linear(x1, w)
+    ref2 = nn_amd.quantized_linear(x2, w)
+    S, A = torch.cuda.Stream(), torch.cuda.Stream()
+    S.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(S):
+        nn_amd.quantized_linear(x2, w)  # S's eager workspace exists before the capture
+        with torch.cuda.graph(g, stream=S):
+            yg = nn_amd.quantized_linear(x1, w)
+    torch.cuda.synchronize()
+    eager = []
+    for _ in range(3):
+        with torch.cuda.stream(A):
+            g.replay()
+        with torch.cuda.stream(S):
+            eager.append(nn_amd.quantized_linear(x2, w))
+    torch.cuda.synchronize()
+    assert torch.equal(yg, ref1)
+    for y in eager:
+        assert torch.equal(y, ref2)
+    with torch.cuda.stream(S):
+        assert _lib.load().nnq_release_workspace(ctypes.c_void_p(S.cuda_stream)) == 0
+        y = nn_amd.quantized_linear(x2, w)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref2)
