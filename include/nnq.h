@@ -188,8 +188,10 @@ typedef struct nnq_sampling {
  * of the original logits (argmax_slice).  logits is left unchanged.  Equal logits at the
  * k-th place keep the lower index (the reference's unstable sort leaves that open).
  * NNQ_ERR_INVALID_ARGUMENT for n = 0 or a temperature that is not positive and finite
- * (sample_token panics there); NNQ_ERR_UNSUPPORTED when ceil(n / 2048) * min(k, 2048)
- * exceeds 16384 (k = min(top_k, n), n with top_k None).
+ * (sample_token panics there).  Any top_k over any vocabulary below 2^32 logits: up to
+ * ceil(n / 2048) * min(k, 2048) <= 16384 candidates (k = min(top_k, n), n with top_k
+ * None) a two-pass top-k, beyond that every key sorted on the device (slower: the tail's
+ * sums run in candidate order over all candidates, as the reference adds them).
  * Replaces sample_token (crates/nn-gptoss/src/sampling.rs:136-185). */
 int nnq_sample_token(const float *logits, int64_t n, const uint32_t *past_tokens, int64_t n_past,
                      const nnq_sampling *cfg, uint32_t *token, void *stream);

@@ -916,8 +916,8 @@ int nnq_moe_block_forward(const nnq_moe *m, const nnq_router *r, const void *x, 
 static int sample_k(const nnq_sampling *cfg, int64_t n, int64_t *k) {
     *k = cfg->top_k < 0 ? n : std::min<int64_t>(cfg->top_k, n);
     if (!sample_supported(n, *k))
-        return fail(NNQ_ERR_UNSUPPORTED, "top_k %lld over %lld logits exceeds the device top-k capacity",
-                    (long long)*k, (long long)n);
+        return fail(NNQ_ERR_UNSUPPORTED, "sampling over %lld logits: at most 2^32 - 1 (u32 token indices)",
+                    (long long)n);
     return NNQ_OK;
 }
 
@@ -992,9 +992,11 @@ int nnq_linear_sample_noalloc(const nnq_weight *w, const float *x, int64_t k, co
     rc = sample_k(cfg, w->L.n, &kk);
     if (rc) return rc;
     const size_t need = sample_scratch_bytes(w->L.n, kk);
-    if (need > kSampleStaticScratchBytes)
-        return fail(NNQ_ERR_UNSUPPORTED, "top_k %lld over %lld logits needs %zu bytes of scratch; the fixed scratch holds %zu",
-                    (long long)kk, (long long)w->L.n, need, kSampleStaticScratchBytes);
+    if (!sample_two_pass(w->L.n, kk) || need > kSampleStaticScratchBytes)
+        return fail(NNQ_ERR_UNSUPPORTED,
+                    "top_k %lld over %lld logits exceeds the allocation-free top-k capacity (ceil(n / 2048) * "
+                    "min(k, 2048) <= 16384 candidates in %zu bytes of fixed scratch)",
+                    (long long)kk, (long long)w->L.n, kSampleStaticScratchBytes);
     void *scr = nullptr;
     HIP_TRY((hipError_t)sample_static_scratch(&scr), "fixed scratch address");
     // the single-token GEMV takes no scratch; the sampling kernels write every scratch

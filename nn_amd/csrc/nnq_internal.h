@@ -97,9 +97,11 @@ int launch_swiglu(const float *gu, int64_t m, int64_t inter, float *h, int32_t *
 int launch_nonfinite_check(const void *y, int y_bf16, int64_t count, int32_t *status, void *stream);
 
 // Token sampling over device logits[n] (k = min(top_k, n), 0: none): scratch bytes, whether
-// the shape fits the two-pass top-k (ceil(n / 2048) * min(k, 2048) <= 16384), and the launch
+// the device path takes the shape (any k, n < 2^32), whether it fits the two-pass top-k
+// (ceil(n / 2048) * min(k, 2048) <= 16384; else every key is sorted), and the launch
 size_t sample_scratch_bytes(int64_t n, int64_t k);
 bool sample_supported(int64_t n, int64_t k);
+bool sample_two_pass(int64_t n, int64_t k);
 // The fixed per-device scratch of nnq_linear_sample_noalloc: its size, and its device
 // address on the current device (looked up once per device; returns a hipError_t).
 constexpr size_t kSampleStaticScratchBytes = 384 * 1024;

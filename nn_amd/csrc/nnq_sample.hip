@@ -176,14 +176,13 @@ struct SampleParams {
     uint64_t seed;
 };
 
-__global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, int64_t n, const uint32_t *past,
-                                                           int64_t n_past, SampleParams sp, int kk, uint64_t *cand) {
-    __shared__ int cnt[kSampleBlock];
-    __shared__ int hist[5 * 256];
-    __shared__ uint64_t bcast[1];
-    __shared__ int nout;
+// The keys of the kSampleBlock logits from `base` (E per thread of 256, element r * 256 +
+// tid): repetition / frequency penalties per occurrence of past_tokens (counted in LDS
+// `cnt`), temperature, orderable key; 0 past n.  Every thread of the workgroup calls it.
+template <int E>
+__device__ void block_keys(const float *logits, int64_t n, const uint32_t *past, int64_t n_past,
+                           const SampleParams &sp, int64_t base, int *cnt, uint64_t (&e)[E]) {
     const int tid = threadIdx.x;
-    const int64_t base = (int64_t)blockIdx.x * kSampleBlock;
     const bool pen = (sp.rep_on || sp.freq_on) && n_past > 0;
     if (pen) {
         for (int j = tid; j < kSampleBlock; j += 256) cnt[j] = 0;
@@ -193,10 +192,7 @@ __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, 
             if (t >= base && t < base + kSampleBlock && t < n) atomicAdd(&cnt[t - base], 1);
         }
     }
-    if (tid == 0) nout = 0;
     __syncthreads();
-    constexpr int E = kSampleBlock / 256;
-    uint64_t e[E];
 #pragma unroll
     for (int r = 0; r < E; r++) {
         const int j = r * 256 + tid;  // coalesced
@@ -216,6 +212,20 @@ __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, 
         }
         e[r] = key;
     }
+}
+
+__global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, int64_t n, const uint32_t *past,
+                                                           int64_t n_past, SampleParams sp, int kk, uint64_t *cand) {
+    __shared__ int cnt[kSampleBlock];
+    __shared__ int hist[5 * 256];
+    __shared__ uint64_t bcast[1];
+    __shared__ int nout;
+    const int tid = threadIdx.x;
+    const int64_t base = (int64_t)blockIdx.x * kSampleBlock;
+    if (tid == 0) nout = 0;
+    constexpr int E = kSampleBlock / 256;
+    uint64_t e[E];
+    block_keys<E>(logits, n, past, n_past, sp, base, cnt, e);
     // the block's real logits may be fewer than kk: keep them all, pad the slots with 0
     const int real = (int)std::min<int64_t>(kSampleBlock, n - base);
     const int kb = std::min(kk, real);
@@ -406,19 +416,306 @@ __global__ __launch_bounds__(NTH) void sample_final_kernel(const float *logits, 
     if (tid == 0) *token = i < nc ? idx[i] : idx[nc - 1];
 }
 
+// ---------------------------------------------------------------------------------
+// Any top-k over any vocabulary (beyond the two-pass capacity): every key, sorted on the
+// device.  sample_keys_kernel writes the keys in index order (A) and a copy padded with
+// zeros to a power of two P (B); a bitonic network sorts B in descending order (chunks of
+// kSortChunk keys in LDS, longer strides in global passes); sample_large_final_kernel
+// takes the k-th largest key as the threshold and the candidates either as a prefix of B
+// (top-p walks the descending order) or, compacted in index order, from A, and wave 0
+// runs the reference's tail over them with every sum in candidate order.
+// ---------------------------------------------------------------------------------
+constexpr int kSortChunk = 8192;  // keys per LDS bitonic chunk (64 KiB)
+constexpr int kStage = 4096;      // values per LDS chunk of the ordered sums
+
+__global__ __launch_bounds__(256) void sample_keys_kernel(const float *logits, int64_t n, const uint32_t *past,
+                                                          int64_t n_past, SampleParams sp, int64_t P, uint64_t *A,
+                                                          uint64_t *B) {
+    __shared__ int cnt[kSampleBlock];
+    constexpr int E = kSampleBlock / 256;
+    const int64_t base = (int64_t)blockIdx.x * kSampleBlock;
+    uint64_t e[E];
+    block_keys<E>(logits, n, past, n_past, sp, base, cnt, e);
+#pragma unroll
+    for (int r = 0; r < E; r++) {
+        const int64_t i = base + r * 256 + threadIdx.x;
+        if (i < n) A[i] = e[r];
+        if (i < P) B[i] = e[r];  // zeros past n
+    }
+}
+
+// bitonic steps inside chunks of `chunk` keys (a power of two <= kSortChunk): for every
+// size in [size_lo, size_hi] (powers of two), the strides below min(size, chunk); the
+// direction of a pair follows its global index (descending where index & size == 0)
+__global__ __launch_bounds__(1024) void bitonic_lds_kernel(uint64_t *keys, int chunk, int64_t size_lo,
+                                                           int64_t size_hi) {
+    __shared__ uint64_t a[kSortChunk];
+    const int64_t c0 = (int64_t)blockIdx.x * chunk;
+    for (int j = threadIdx.x; j < chunk; j += 1024) a[j] = keys[c0 + j];
+    __syncthreads();
+    for (int64_t size = size_lo; size <= size_hi; size <<= 1) {
+        for (int stride = (int)std::min<int64_t>(size, chunk) >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < chunk / 2; i += 1024) {
+                const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+                const bool desc = ((c0 + lo) & size) == 0;
+                const uint64_t x = a[lo], y = a[hi];
+                if ((x < y) == desc) {
+                    a[lo] = y;
+                    a[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int j = threadIdx.x; j < chunk; j += 1024) keys[c0 + j] = a[j];
+}
+
+// one bitonic step with a stride of at least a chunk: one pair per thread
+__global__ __launch_bounds__(256) void bitonic_global_kernel(uint64_t *keys, int64_t P, int64_t size, int64_t stride) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= P / 2) return;
+    const int64_t lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+    const bool desc = (lo & size) == 0;
+    const uint64_t x = keys[lo], y = keys[hi];
+    if ((x < y) == desc) {
+        keys[lo] = y;
+        keys[hi] = x;
+    }
+}
+
+// The f32 sum ((s + p[0]) + p[1]) + ... of a global array in element order, the same in
+// every lane of the calling wave: chunks staged in LDS by the wave, then ordered_sum.
+__device__ float ordered_sum_g(const float *p, int64_t n, float *stage, float s) {
+    const int lane = threadIdx.x & 63;
+    for (int64_t c0 = 0; c0 < n; c0 += kStage) {
+        const int cn = (int)std::min<int64_t>(kStage, n - c0);
+        for (int j = 4 * lane; j < cn; j += 256)
+            *reinterpret_cast<floatx4 *>(stage + j) = *reinterpret_cast<const floatx4 *>(p + c0 + j);
+        wave_sync();
+        for (int i = 0; i < cn; i += 4) {
+            const floatx4 v = *reinterpret_cast<const floatx4 *>(stage + i);
+            s += v[0];
+            if (i + 1 < cn) s += v[1];
+            if (i + 2 < cn) s += v[2];
+            if (i + 3 < cn) s += v[3];
+        }
+        wave_sync();
+    }
+    return s;
+}
+
+// within one staged chunk: continue the cumulative sum `cum` over v[0..cn) in order (16-byte
+// broadcast reads), returning the first index where it meets `stop`, or -1
+template <class F>
+__device__ __forceinline__ int walk_chunk(const float *v, int cn, float &cum, F stop) {
+    for (int i = 0; i < cn; i += 4) {
+        const floatx4 q = *reinterpret_cast<const floatx4 *>(v + i);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (i + j >= cn) return -1;
+            cum += q[j];
+            if (stop(cum)) return i + j;
+        }
+    }
+    return -1;
+}
+
+// the first i with (cumulative sum of p[0..i] in order) meeting `stop` (n when none)
+template <class F>
+__device__ int64_t walk_g(const float *p, int64_t n, float *stage, F stop) {
+    const int lane = threadIdx.x & 63;
+    float cum = 0.0f;
+    for (int64_t c0 = 0; c0 < n; c0 += kStage) {
+        const int cn = (int)std::min<int64_t>(kStage, n - c0);
+        for (int j = 4 * lane; j < cn; j += 256)
+            *reinterpret_cast<floatx4 *>(stage + j) = *reinterpret_cast<const floatx4 *>(p + c0 + j);
+        wave_sync();
+        const int hit = walk_chunk(stage, cn, cum, stop);
+        wave_sync();
+        if (hit >= 0) return c0 + hit;
+    }
+    return n;
+}
+
+// softmax_candidates (sampling.rs:371-391) of val[0..n) into p, by wave 0, global arrays
+__device__ void softmax_g(const float *val, int64_t n, float *ex, float *p, float *stage) {
+    const int lane = threadIdx.x & 63;
+    float mx = -INFINITY;
+    for (int64_t i = lane; i < n; i += 64) mx = fmaxf(mx, val[i]);
+    mx = wave_max(mx);
+    if (!(fabsf(mx) <= 3.402823466e38f)) {
+        for (int64_t i = lane; i < n; i += 64) p[i] = 1.0f / (float)n;
+        __threadfence_block();
+        wave_sync();
+        return;
+    }
+    for (int64_t i = lane; i < n; i += 64) ex[i] = expf(val[i] - mx);
+    __threadfence_block();
+    wave_sync();
+    const float sum = ordered_sum_g(ex, n, stage, 0.0f);
+    if (!(fabsf(sum) <= 3.402823466e38f) || sum == 0.0f) {
+        for (int64_t i = lane; i < n; i += 64) p[i] = 1.0f / (float)n;
+    } else {
+        for (int64_t i = lane; i < n; i += 64) p[i] = ex[i] / sum;
+    }
+    __threadfence_block();
+    wave_sync();
+}
+
+// work: val | ex | prob (f32) | idx (u32), each n + 4 long from 16-byte aligned starts
+__global__ __launch_bounds__(1024) void sample_large_final_kernel(const float *logits, int64_t n, const uint64_t *A,
+                                                                 const uint64_t *B, SampleParams sp, float *work,
+                                                                 int64_t stride, uint32_t *token) {
+    __shared__ float stage[kStage];
+    __shared__ int64_t wsum[16][2];
+    __shared__ int64_t nc_s;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t k = sp.k;
+    float *val = work, *ex = work + stride, *prob = work + 2 * stride;
+    uint32_t *idx = reinterpret_cast<uint32_t *>(work + 3 * stride);
+    const bool keep_inf = sp.keep_inf != 0;
+    if (k > 0) {
+        if (sp.use_top_p) {
+            // descending order: the candidates are B[a, a + f) (a: the +inf keys in front
+            // that are not candidates, only when top_k is Some)
+            int64_t f = 0, a = 0;
+            for (int64_t j = tid; j < k; j += 1024) {
+                const uint64_t s = B[j];
+                f += key_cand(s, keep_inf) ? 1 : 0;
+                a += (!keep_inf && (uint32_t)(s >> 32) == kOrdPosInf) ? 1 : 0;
+            }
+            for (int o = 32; o > 0; o >>= 1) {
+                f += __shfl_xor(f, o, 64);
+                a += __shfl_xor(a, o, 64);
+            }
+            if (lane == 0) {
+                wsum[wv][0] = f;
+                wsum[wv][1] = a;
+            }
+            __syncthreads();
+            f = a = 0;
+            for (int w = 0; w < 16; w++) {
+                f += wsum[w][0];
+                a += wsum[w][1];
+            }
+            for (int64_t j = tid; j < f; j += 1024) {
+                const uint64_t s = B[a + j];
+                val[j] = key_val(s);
+                idx[j] = key_idx(s);
+            }
+            if (tid == 0) nc_s = f;
+        } else {
+            // index order: the keys of A at or above the k-th largest, candidates only;
+            // thread t compacts its contiguous range, offsets from a block scan
+            const uint64_t T = B[k - 1];
+            const int64_t per = (n + 1023) / 1024, i0 = tid * per, i1 = std::min<int64_t>(n, i0 + per);
+            int64_t c = 0;
+            for (int64_t i = i0; i < i1; i++) c += (A[i] >= T && key_cand(A[i], keep_inf)) ? 1 : 0;
+            int64_t incl = c;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int64_t v = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += v;
+            }
+            if (lane == 63) wsum[wv][0] = incl;
+            __syncthreads();
+            int64_t before = incl - c;
+            for (int w = 0; w < wv; w++) before += wsum[w][0];
+            for (int64_t i = i0; i < i1; i++) {
+                const uint64_t s = A[i];
+                if (s >= T && key_cand(s, keep_inf)) {
+                    val[before] = key_val(s);
+                    idx[before] = (uint32_t)i;
+                    before++;
+                }
+            }
+            if (tid == 1023) nc_s = before;
+        }
+    } else if (tid == 0) {
+        nc_s = 0;
+    }
+    __threadfence_block();
+    __syncthreads();
+    if (tid >= 64) return;
+    int64_t nc = nc_s;
+    if (sp.use_top_p && nc > 0) {
+        softmax_g(val, nc, ex, prob, stage);
+        const float tp = sp.top_p;
+        const int64_t i = walk_g(prob, nc, stage, [tp](float cum) { return cum >= tp; });
+        nc = i < nc ? i + 1 : nc;
+    }
+    if (nc == 0) {
+        if (tid == 0) {  // argmax_slice of the original logits (sampling.rs:394-400)
+            int64_t best = 0;
+            float bv = logits[0];
+            for (int64_t j = 1; j < n; j++) {
+                const float v = logits[j];
+                if (!(bv > v)) {
+                    best = j;
+                    bv = v;
+                }
+            }
+            *token = (uint32_t)best;
+        }
+        return;
+    }
+    if (nc == 1) {
+        if (tid == 0) *token = idx[0];
+        return;
+    }
+    softmax_g(val, nc, ex, prob, stage);
+    const float selector = (float)(sp.seed % 10000ull) / 10000.0f;
+    const int64_t i = walk_g(prob, nc, stage, [selector](float cum) { return selector < cum; });
+    if (tid == 0) *token = i < nc ? idx[i] : idx[nc - 1];
+}
+
+int64_t pow2_at_least(int64_t n) {
+    int64_t p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+struct LargeScratch {
+    uint64_t *A, *B;
+    float *work;
+    int64_t stride, P;
+};
+
+LargeScratch large_carve(void *base, int64_t n, size_t *bytes) {
+    LargeScratch L;
+    L.P = pow2_at_least(std::max<int64_t>(n, 2));
+    L.stride = (n + 4 + 63) / 64 * 64;
+    uint8_t *b = reinterpret_cast<uint8_t *>(base);
+    size_t off = 0;
+    L.A = reinterpret_cast<uint64_t *>(b + off);
+    off += ((size_t)n * 8 + 255) & ~(size_t)255;
+    L.B = reinterpret_cast<uint64_t *>(b + off);
+    off += ((size_t)L.P * 8 + 255) & ~(size_t)255;
+    L.work = reinterpret_cast<float *>(b + off);
+    off += (size_t)L.stride * 16;
+    if (bytes) *bytes = off;
+    return L;
+}
+
 }  // namespace
 
+bool sample_two_pass(int64_t n, int64_t k) {
+    const int64_t blocks = (n + kSampleBlock - 1) / kSampleBlock;
+    const int64_t kk = std::min<int64_t>(std::max<int64_t>(k, 1), kSampleBlock);
+    return blocks * kk <= kSampleMaxCand;
+}
+
 size_t sample_scratch_bytes(int64_t n, int64_t k) {
+    if (!sample_two_pass(n, k)) {
+        size_t b = 0;
+        large_carve(nullptr, n, &b);
+        return b;
+    }
     const int64_t blocks = (n + kSampleBlock - 1) / kSampleBlock;
     const int64_t kk = std::min<int64_t>(std::max<int64_t>(k, 1), kSampleBlock);
     return (((size_t)blocks * kk * 8 + 255) & ~(size_t)255) + (size_t)kSampleMaxCand * 16;
 }
 
-bool sample_supported(int64_t n, int64_t k) {
-    const int64_t blocks = (n + kSampleBlock - 1) / kSampleBlock;
-    const int64_t kk = std::min<int64_t>(std::max<int64_t>(k, 1), kSampleBlock);
-    return blocks * kk <= kSampleMaxCand && n <= 0xFFFFFFFFll;
-}
+bool sample_supported(int64_t n, int64_t k) { return n >= 1 && n <= 0xFFFFFFFFll && k >= 0; }
 
 // ---- fixed device scratch for the allocation-free entry point -----------------------
 //
@@ -467,6 +764,25 @@ int launch_sample(const float *logits, int64_t n, const uint32_t *past, int64_t 
     sp.k = k;
     sp.seed = seed;
     const int64_t blocks = (n + kSampleBlock - 1) / kSampleBlock;
+    if (!sample_two_pass(n, k)) {
+        hipStream_t st = (hipStream_t)stream;
+        const LargeScratch L = large_carve(scratch, n, nullptr);
+        hipLaunchKernelGGL(sample_keys_kernel, dim3((unsigned)((L.P + kSampleBlock - 1) / kSampleBlock)), dim3(256), 0,
+                           st, logits, n, past, n_past, sp, L.P, L.A, L.B);
+        const int chunk = (int)std::min<int64_t>(L.P, kSortChunk);
+        hipLaunchKernelGGL(bitonic_lds_kernel, dim3((unsigned)(L.P / chunk)), dim3(1024), 0, st, L.B, chunk, (int64_t)2,
+                           (int64_t)chunk);
+        for (int64_t size = 2 * (int64_t)chunk; size <= L.P; size <<= 1) {
+            for (int64_t stride = size / 2; stride >= chunk; stride >>= 1)
+                hipLaunchKernelGGL(bitonic_global_kernel, dim3((unsigned)((L.P / 2 + 255) / 256)), dim3(256), 0, st,
+                                   L.B, L.P, size, stride);
+            hipLaunchKernelGGL(bitonic_lds_kernel, dim3((unsigned)(L.P / chunk)), dim3(1024), 0, st, L.B, chunk, size,
+                               size);
+        }
+        hipLaunchKernelGGL(sample_large_final_kernel, dim3(1), dim3(1024), 0, st, logits, n, L.A, L.B, sp, L.work,
+                           L.stride, token);
+        return (int)hipGetLastError();
+    }
     const int kk = (int)std::min<int64_t>(std::max<int64_t>(k, 1), kSampleBlock);
     uint64_t *cand = reinterpret_cast<uint64_t *>(scratch);
     float *work = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) +

@@ -401,7 +401,7 @@ def sample_token(logits, temperature=0.7, top_k=50, top_p=0.9, repetition_penalt
     """sample_token (crates/nn-gptoss/src/sampling.rs:136-185); top_k / top_p None disable
     the step, as the reference's Option fields do."""
     lg = _f32(logits).ravel()
-    past = np.ascontiguousarray(np.asarray(past_tokens, np.uint32).ravel())
+    past = np.ascontiguousarray(np.asarray(() if past_tokens is None else past_tokens, np.uint32).ravel())
     out = ctypes.c_uint32()
     rc = lib().orc_sample_token(_p(lg, _f32p), lg.size, _p(past, _u32p) if past.size else None, past.size,
                                 ctypes.c_float(temperature), -1 if top_k is None else int(top_k),

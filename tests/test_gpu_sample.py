@@ -1,7 +1,8 @@
 """GPU parity for token sampling (sample_token, crates/nn-gptoss/src/sampling.rs:136-185).
 
-nnq_sample_token runs penalties, temperature, a two-pass top-k over the whole vocabulary,
-top-p, softmax and the selector walk on the device.  The picked token must equal the
+nnq_sample_token runs penalties, temperature, the top-k over the whole vocabulary (a
+two-pass select up to 16384 candidates, every key sorted beyond), top-p, softmax and the
+selector walk on the device.  The picked token must equal the
 oracle's restatement of sample_token on the same logits, for every configuration and
 seed tried (the only freedom the reference leaves, the order of exactly equal logits at
 the k-th place, does not arise with these inputs).  nnq_linear_sample (Q6_K LM head +
@@ -87,8 +88,6 @@ def test_sample_top_k_none_small_vocab(O, dev):
 def test_sample_errors(O, dev):
     import nn_amd
     t = torch.zeros(151936, device=dev)
-    with pytest.raises(nn_amd.Unsupported):
-        nn_amd.sample_token(t, top_k=None)
     with pytest.raises(nn_amd.TensorError):
         nn_amd.sample_token(t, temperature=0.0)
     with pytest.raises(nn_amd.TensorError):
@@ -154,3 +153,47 @@ def test_sample_top_k_none_pos_inf(O, dev, n, top_p):
         for seed in (11, 4321):
             got = int(nn_amd.sample_token(t2, temperature=0.8, top_k=None, top_p=top_p, seed=seed).item())
             assert got == O.sample_token(lg2, temperature=0.8, top_k=None, top_p=top_p, seed=seed), (n, top_p, seed)
+
+
+# Beyond the two-pass capacity (ceil(n / 2048) * min(k, 2048) > 16384 candidates) every
+# key is sorted on the device: top_k None and large k over the Qwen3 vocabulary, with and
+# without top-p, penalties, and infinite / NaN logits.
+LARGE = [
+    dict(temperature=0.7, top_k=None, top_p=None),
+    dict(temperature=0.7, top_k=None, top_p=0.9),
+    dict(temperature=1.0, top_k=None, top_p=0.5, repetition_penalty=1.3, frequency_penalty=0.2),
+    dict(temperature=0.9, top_k=5000, top_p=None),
+    dict(temperature=1.1, top_k=60000, top_p=0.95),
+    dict(temperature=0.8, top_k=151936, top_p=None),
+]
+
+
+@pytest.mark.parametrize("ci", range(len(LARGE)))
+@pytest.mark.parametrize("n", [151936, 20000])
+def test_sample_large_candidate_sets(O, dev, n, ci):
+    import nn_amd
+    cfg = dict(LARGE[ci])
+    lg = nn_amd.synth_normal(n + 31 * ci, 1, (n,), 3.0)
+    past = [5, 5, 77, 1000, n - 1] if "repetition_penalty" in cfg else None
+    t = torch.from_numpy(lg).to(dev)
+    for seed in (0, 4321, 9999):
+        got = int(nn_amd.sample_token(t, seed=seed, past_tokens=past, **cfg).item())
+        want = O.sample_token(lg, seed=seed, past_tokens=past, **cfg)
+        assert got == want, (n, cfg, seed)
+
+
+@pytest.mark.parametrize("top_k,top_p", [(None, None), (None, 0.7), (30000, None), (30000, 0.99)])
+def test_sample_large_infinite_logits(O, dev, top_k, top_p):
+    """+inf, -inf and NaN logits in the sorted path: with top_k None a +inf logit is a
+    candidate and the softmax uniform (sampling.rs:158-165, 371-391); with Some(k) only
+    finite logits are candidates."""
+    import nn_amd
+    n = 40000
+    lg = nn_amd.synth_normal(77, 1, (n,), 2.0)
+    lg[[10, 20000]] = np.inf
+    lg[[11, 39999]] = -np.inf
+    lg[[12, 30000]] = np.nan
+    t = torch.from_numpy(lg).to(dev)
+    for seed in (1, 5000, 9998):
+        got = int(nn_amd.sample_token(t, temperature=1.0, top_k=top_k, top_p=top_p, seed=seed).item())
+        assert got == O.sample_token(lg, temperature=1.0, top_k=top_k, top_p=top_p, seed=seed), (top_k, top_p, seed)
