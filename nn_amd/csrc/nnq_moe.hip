@@ -568,12 +568,6 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
                                 __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs[b], so, kb * 32, 2));
                     }
             };
-            floatx4 acc[NBW][4][2];
-#pragma unroll
-            for (int b = 0; b < NBW; b++)
-#pragma unroll
-                for (int mt = 0; mt < 4; mt++) acc[b][mt][0] = acc[b][mt][1] = zero4();
-
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __syncthreads();  // the previous round / pass has finished reading the ring
             if constexpr (SL) {
@@ -600,9 +594,62 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
             };
 #pragma unroll
             for (int t = 1 - NBUF; t < 0; t++) step(t, ((t + PF) % (PF + 1) + (PF + 1)) % (PF + 1));
-            // MTN: live 16-row tiles of this pass (a constant per instantiation)
+            // lane holds rows 4p + i of each tile; acc[.][.][0]: column 2 * l16 of the block,
+            // [1]: 2 * l16 + 1
+            auto epilogue = [&](auto &acc) {
+                constexpr int MTN = (int)std::extent<std::remove_reference_t<decltype(acc)>, 1>::value;
+                if (GU) {
+                    const int64_t col0 = (int64_t)st * 32;
+#pragma unroll
+                    for (int mt = 0; mt < MTN; mt++) {
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int32_t r = m0 + mt * 16 + 4 * p + i;
+                            if (r >= ne) continue;
+                            uint32_t hh = 0, hl = 0;
+#pragma unroll
+                            for (int o = 0; o < 2; o++) {
+                                const int64_t c = col0 + 2 * l16 + o;
+                                const float gt = acc[0][mt][o][i] + d.gu_b[e * 2 * I + c];
+                                const float up = acc[1][mt][o][i] + d.gu_b[e * 2 * I + I + c];
+                                // silu (crates/nn-core/src/dyn_tensor/ops/math.rs:140), clamped to +-limit
+                                float sg = gt / (1.0f + expf(-gt));
+                                sg = sg < -run.limit ? -run.limit : (sg > run.limit ? run.limit : sg);
+                                const float h = sg * up;
+                                const uint32_t bh = bf16_rne(h);
+                                hh |= bh << (16 * o);
+                                hl |= (uint32_t)bf16_rne(h - bf16_to_f32(bh)) << (16 * o);
+                            }
+                            const int64_t o2 = (int64_t)(r0 + r) * I + col0 + 2 * l16;
+                            *reinterpret_cast<uint32_t *>(sc.hb + o2) = hh;
+                            *reinterpret_cast<uint32_t *>(sc.hb + run.A * I + o2) = hl;
+                        }
+                    }
+                } else {
+                    const int64_t col0 = (int64_t)st * 32 + 2 * l16;
+                    const float b0 = d.dn_b[e * H + col0], b1 = d.dn_b[e * H + col0 + 1];
+#pragma unroll
+                    for (int mt = 0; mt < MTN; mt++) {
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int32_t r = m0 + mt * 16 + 4 * p + i;
+                            if (r >= ne) continue;
+                            *reinterpret_cast<float2 *>(sc.yb + (int64_t)(r0 + r) * H + col0) =
+                                float2{acc[0][mt][0][i] + b0, acc[0][mt][1][i] + b1};
+                        }
+                    }
+                }
+            };
+            // MTN: live 16-row tiles of this pass (a constant per instantiation); the
+            // accumulators and the epilogue are sized by it, so the passes over fewer rows
+            // hold fewer registers
             auto pass = [&](auto mtn_c) {
                 constexpr int MTN = decltype(mtn_c)::value;
+                floatx4 acc[NBW][MTN][2];
+#pragma unroll
+                for (int b = 0; b < NBW; b++)
+#pragma unroll
+                    for (int mt = 0; mt < MTN; mt++) acc[b][mt][0] = acc[b][mt][1] = zero4();
                 auto body = [&](int ch, int slot) {
                     wait_vmcnt<(NBUF - 2) * (LPA + WPS)>();  // this thread's copies of chunk ch
                     __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): this wave's reads of chunk ch - 1
@@ -658,6 +705,9 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
 #pragma unroll
                 for (int u = 0; u < PF; u++)
                     if (nfull + u < nch) body(nfull + u, u);
+                __builtin_amdgcn_s_waitcnt(0);  // trailing copies and weight loads (unused)
+                if (!active) return;
+                epilogue(acc);
             };
             switch (mtn) {
             case 1: pass(std::integral_constant<int, 1>{}); break;
@@ -665,55 +715,10 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
             case 3: pass(std::integral_constant<int, 3>{}); break;
             default: pass(std::integral_constant<int, 4>{}); break;
             }
-            __builtin_amdgcn_s_waitcnt(0);  // trailing copies and weight loads (unused)
-            if (!active) continue;
-            // lane holds rows 4p + i of each tile; acc[.][.][0]: column 2 * l16 of the block, [1]: 2 * l16 + 1
-            if (GU) {
-                const int64_t col0 = (int64_t)st * 32;
-#pragma unroll
-                for (int mt = 0; mt < 4; mt++) {
-                    if (mt >= mtn) break;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int32_t r = m0 + mt * 16 + 4 * p + i;
-                        if (r >= ne) continue;
-                        uint32_t hh = 0, hl = 0;
-#pragma unroll
-                        for (int o = 0; o < 2; o++) {
-                            const int64_t c = col0 + 2 * l16 + o;
-                            const float gt = acc[0][mt][o][i] + d.gu_b[e * 2 * I + c];
-                            const float up = acc[1][mt][o][i] + d.gu_b[e * 2 * I + I + c];
-                            // silu (crates/nn-core/src/dyn_tensor/ops/math.rs:140), clamped to +-limit
-                            float sg = gt / (1.0f + expf(-gt));
-                            sg = sg < -run.limit ? -run.limit : (sg > run.limit ? run.limit : sg);
-                            const float h = sg * up;
-                            const uint32_t bh = bf16_rne(h);
-                            hh |= bh << (16 * o);
-                            hl |= (uint32_t)bf16_rne(h - bf16_to_f32(bh)) << (16 * o);
-                        }
-                        const int64_t o2 = (int64_t)(r0 + r) * I + col0 + 2 * l16;
-                        *reinterpret_cast<uint32_t *>(sc.hb + o2) = hh;
-                        *reinterpret_cast<uint32_t *>(sc.hb + run.A * I + o2) = hl;
-                    }
-                }
-            } else {
-                const int64_t col0 = (int64_t)st * 32 + 2 * l16;
-                const float b0 = d.dn_b[e * H + col0], b1 = d.dn_b[e * H + col0 + 1];
-#pragma unroll
-                for (int mt = 0; mt < 4; mt++) {
-                    if (mt >= mtn) break;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int32_t r = m0 + mt * 16 + 4 * p + i;
-                        if (r >= ne) continue;
-                        *reinterpret_cast<float2 *>(sc.yb + (int64_t)(r0 + r) * H + col0) =
-                            float2{acc[0][mt][0][i] + b0, acc[0][mt][1][i] + b1};
-                    }
-                }
-            }
         }
     }
 }
+
 // y[t] = ((0 + w_a * y_a) + w_b * y_b) + ... over the token's experts a < b < ...
 // A NaN or infinite output sets *status (when given) to NNQ_ERR_NON_FINITE, the
 // check_output_finite of moe_forward (crates/nn-core/src/layers/nan_check.rs:113-140).
