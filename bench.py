@@ -283,13 +283,20 @@ def bench_lm_head(steps, warmup, seed=3):
                 wbytes=wb, x=x)
 
 
-def bench_gemm(m, n, k, steps, warmup, min_bytes=256 << 20):
-    """Config 4: X [m, k] bf16 ~ N(0,1) times Q4_K W [n, k]^T -> Y [m, n] bf16, f32 accumulate."""
+def bench_gemm(m, n, k, steps, warmup, min_bytes=256 << 20, fmt="q4_k"):
+    """Config 4: X [m, k] bf16 ~ N(0,1) times Q4_K W [n, k]^T -> Y [m, n] bf16, f32 accumulate
+    (fmt q8_0 / q6_k: the same product over those formats' prefill GEMM)."""
     import torch
 
     import nn_amd
-    wb = nn_amd.quantize_q4_k(nn_amd.synth_normal(4, k, (n, k), 0.02))
-    copies = make_copies(wb, nn_amd.QuantType.Q4_K, n, k, min_bytes)
+    w = nn_amd.synth_normal(4, k, (n, k), 0.02)
+    if fmt == "q8_0":
+        wb, qt, lay = nn_amd.quantize_q8_0(w), nn_amd.QuantType.Q8_0, nn_amd.Layout.GGUF
+    elif fmt == "q6_k":
+        wb, qt, lay = nn_amd.quantize_q6_k(w), nn_amd.QuantType.Q6_K, nn_amd.Layout.NN_GGUF
+    else:
+        wb, qt, lay = nn_amd.quantize_q4_k(w), nn_amd.QuantType.Q4_K, nn_amd.Layout.GGUF
+    copies = make_copies(wb, qt, n, k, min_bytes, layout=lay)
     dev = torch.device("cuda:0")
     x = torch.from_numpy(nn_amd.synth_normal(4, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
     ys = [torch.empty((m, n), device=dev, dtype=torch.bfloat16) for _ in copies]
@@ -580,6 +587,13 @@ def main():
                 c["frac_of_torch_f16_gemm"] = round(g["tflops"] / blas[(n, k)], 4)
                 gemms[name] = dict(shape=(m, n, k), wbytes=g["wbytes"], x=g["x"])
             configs[name] = c
+            log(f"  {c}")
+        for fmt, (m, n, k) in [("q8_0", (512, 4096, 4096)), ("q6_k", (512, 4096, 12288))]:
+            log(f"bench: {fmt} prefill GEMM M={m} N={n} K={k} (bf16 in/out)")
+            g = bench_gemm(m, n, k, max(20, K // 20), 10, fmt=fmt)
+            c = {**ms3(g["st"]), "TFLOPs": round(g["tflops"], 2), "frac_mfma16": round(g["tflops"] / MFMA16_PEAK_TFLOPS, 4),
+                 "tokens_per_s": round(m / g["st"]["median"], 1)}
+            configs[f"{fmt}_prefill_gemm_{m}x{n}x{k}"] = c
             log(f"  {c}")
     mi = None
     if want("moe"):

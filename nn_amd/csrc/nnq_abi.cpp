@@ -391,12 +391,13 @@ static GemmArgs gemm_args(const nnq_weight *w, const void *x, nnq_dtype x_dtype,
     g.m = m;
     g.ntile = L.ntile;
     g.nblk = L.nblk;
+    g.blk = L.fmt == NNQ_FMT_Q4_K ? 0 : L.fmt;
     return g;
 }
 
 // scratch a linear call of m tokens needs (the prefill GEMM's staging and split-K slabs)
 static size_t linear_scratch_bytes(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
-    if (w->L.fmt != NNQ_FMT_Q4_K || m <= 8) return 0;
+    if (m <= 8) return 0;
     return gemm_scratch_bytes(gemm_args(w, nullptr, x_dtype, m, nullptr, nullptr, NNQ_F32));
 }
 
@@ -409,8 +410,8 @@ static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype
     const Layout &L = w->L;
     const int64_t k = L.k;
     const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, ye = y_dtype == NNQ_BF16 ? 2 : 4;
-    if (L.fmt == NNQ_FMT_Q4_K && m > 8 && !x_swiglu) {
-        // prefill: LDS-staged MFMA GEMM
+    if (m > 8 && !x_swiglu) {
+        // prefill: MFMA GEMM (Q4_K: nnq_gemm*.hip; Q8_0 / Q6_K: nnq_gemm_blk.hip)
         GemmArgs g = gemm_args(w, x, x_dtype, m, bias, y, y_dtype);
         Scratch s;
         if (ext_scratch)
@@ -419,7 +420,7 @@ static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype
             HIP_TRY(s.alloc(gemm_scratch_bytes(g), (hipStream_t)stream), "scratch alloc");
             g.scratch = s.p;
         }
-        int e = launch_gemm_q4k(g, stream);
+        int e = g.blk ? launch_gemm_blk(g, stream) : launch_gemm_q4k(g, stream);
         if (e) return hip_fail((hipError_t)e, "gemm launch");
         return NNQ_OK;
     }

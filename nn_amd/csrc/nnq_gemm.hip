@@ -38,11 +38,13 @@ namespace {
 
 inline size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
-// the LDS-ring kernel (nnq_gemm_ring.hip) takes every shape its plan accepts
-bool use_ring(const GemmArgs &a) { return gemm_ring_plan(a, nullptr) > 0; }
+// the LDS-ring kernel (nnq_gemm_ring.hip) takes every Q4_K shape its plan accepts
+bool use_ring(const GemmArgs &a) { return !a.blk && gemm_ring_plan(a, nullptr) > 0; }
+
+}  // namespace
 
 // scratch layout: xh | xs | rowback | ysplit; base null: offsets from 0 (sizing)
-GemmScratch carve(void *base, const GemmArgs &a, size_t *bytes) {
+GemmScratch gemm_carve(void *base, const GemmArgs &a, size_t *bytes) {
     const int P = a.x_bf16 ? 1 : 2;
     uint8_t *b = reinterpret_cast<uint8_t *>(base);
     size_t off = 0;
@@ -53,7 +55,7 @@ GemmScratch carve(void *base, const GemmArgs &a, size_t *bytes) {
     off += al256((size_t)2 * a.m * (a.k / 32) * 2);
     s.rowback = reinterpret_cast<float *>(b + off);
     off += al256((size_t)a.m * 4);
-    s.ksplit = use_ring(a) ? gemm_ring_plan(a, nullptr) : 1;
+    s.ksplit = a.blk ? gemm_blk_plan(a, nullptr) : (use_ring(a) ? gemm_ring_plan(a, nullptr) : 1);
     s.ysplit = nullptr;
     if (s.ksplit > 1) {
         s.ysplit = reinterpret_cast<float *>(b + off);
@@ -62,6 +64,8 @@ GemmScratch carve(void *base, const GemmArgs &a, size_t *bytes) {
     if (bytes) *bytes = off;
     return s;
 }
+
+namespace {
 
 __device__ __forceinline__ void load8(const void *x, int x_bf16, int64_t off, float v[8]) {
     if (x_bf16) {
@@ -451,7 +455,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_q4k_kernel(GemmArgs a, Gem
 // ---------------------------------------------------------------------------------
 size_t gemm_scratch_bytes(const GemmArgs &a) {
     size_t bytes = 0;
-    carve(nullptr, a, &bytes);
+    gemm_carve(nullptr, a, &bytes);
     return bytes;
 }
 
@@ -497,18 +501,22 @@ static void launch_prep(const GemmArgs &a, const GemmScratch &sc, hipStream_t st
     return launch_prep_ng<P, 0>(a, sc, st);
 }
 
-int launch_gemm_q4k(const GemmArgs &a, void *stream) {
-    if (a.m <= 0) return 0;
-    const int P = a.x_bf16 ? 1 : 2;
-    const GemmScratch sc = carve(a.scratch, a, nullptr);
+int launch_gemm_prep(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     hipStream_t st = (hipStream_t)stream;
-    if (P == 1)
+    if (a.x_bf16)
         launch_prep<1>(a, sc, st);
     else
         launch_prep<2>(a, sc, st);
-    int e = (int)hipGetLastError();
+    return (int)hipGetLastError();
+}
+
+int launch_gemm_q4k(const GemmArgs &a, void *stream) {
+    if (a.m <= 0) return 0;
+    const GemmScratch sc = gemm_carve(a.scratch, a, nullptr);
+    hipStream_t st = (hipStream_t)stream;
+    int e = launch_gemm_prep(a, sc, st);
     if (e) return e;
-    return P == 1 ? launch_p<1>(a, sc, st) : launch_p<2>(a, sc, st);
+    return a.x_bf16 ? launch_p<1>(a, sc, st) : launch_p<2>(a, sc, st);
 }
 
 }  // namespace nnq

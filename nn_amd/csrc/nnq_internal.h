@@ -126,8 +126,13 @@ struct GemmArgs {
     int64_t n, k, m;
     int64_t ntile, nblk;
     void *scratch;
+    int blk;  // 0: Q4_K; NNQ_FMT_Q8_0 / NNQ_FMT_Q6_K: the block-scaled GEMM (nnq_gemm_blk.hip)
 };
 int launch_gemm_q4k(const GemmArgs &a, void *stream);
+// Q8_0 / Q6_K prefill GEMM (M > 8): the activation staging below, then one kernel
+int launch_gemm_blk(const GemmArgs &a, void *stream);
+// its K split (and tile height, when bm is given)
+int gemm_blk_plan(const GemmArgs &a, int *bm);
 size_t gemm_scratch_bytes(const GemmArgs &a);
 // staged activation (gemm_prep_kernel): P = 1 (bf16 x) or 2 (f32 x, hi + lo planes)
 struct GemmScratch {
@@ -141,6 +146,9 @@ struct GemmScratch {
 // the kernel; bn and bm, when given, receive the tile width and height), and its launch
 int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm = nullptr);
 int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream);
+// the staging scratch of a GEMM call (base null: sizes only) and the staging kernel
+GemmScratch gemm_carve(void *base, const GemmArgs &a, size_t *bytes);
+int launch_gemm_prep(const GemmArgs &a, const GemmScratch &sc, void *stream);
 
 // MoE (GPT-OSS MXFP4).  Expert weights [E][K][N] with 32-element blocks along N
 // (Mxfp4Tensor of the flat tensor) are repacked per (expert, 32-column block nb,
