@@ -246,8 +246,8 @@ int nnq_mlp_forward(const nnq_mlp *mlp, const void *x, nnq_dtype x_dtype, int64_
  *           (packed bytes E*hidden*2*inter/2, scales E*hidden*2*inter/32),
  *  down:    Mxfp4Tensor of the flat [E, inter, hidden] tensor,
  *  biases:  f32 [E, 2*inter] and [E, hidden] (host).
- * hidden and inter must be multiples of 32 (NNQ_ERR_INVALID_SHAPE), at most 256
- * experts.  The codes are repacked on upload into per-(expert, 32-column block,
+ * hidden and inter must be multiples of 32 (NNQ_ERR_INVALID_SHAPE), at most 4096
+ * experts (NNQ_ERR_UNSUPPORTED beyond).  The codes are repacked on upload into per-(expert, 32-column block,
  * 32-row block) fragments in MFMA lane order (a permutation of the bytes).
  * Replaces QuantizedDecoderLayer::load's expert tensors
  * (crates/nn-gptoss/src/quantized_model.rs:70-78). */
@@ -283,7 +283,7 @@ int nnq_moe_forward(const nnq_moe *moe, const void *x, nnq_dtype x_dtype, int64_
                     float *topk_w, void *stream);
 
 /* Upload the GPT-OSS router Linear: weight f32 [num_experts, hidden], bias f32
- * [num_experts] or NULL (host).  hidden a multiple of 32, at most 256 experts.
+ * [num_experts] or NULL (host).  hidden a multiple of 32, at most 4096 experts.
  * Replaces QuantizedDecoderLayer::load's router (crates/nn-gptoss/src/quantized_model.rs:63-67),
  * which keeps it at full precision. */
 int nnq_router_create(int64_t num_experts, int64_t hidden, const float *weight, const float *bias, nnq_router **out);

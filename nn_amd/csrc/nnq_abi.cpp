@@ -70,6 +70,9 @@ int hip_fail(hipError_t e, const char *what) {
 
 // token-expert assignments per MoE launch sequence; longer batches run in token chunks
 constexpr int64_t kMoeChunkAssign = 16384;
+// experts of a MoE layer: the routing kernels keep a token's E probabilities (4 tokens per
+// workgroup) and the permutation its E running counts in LDS
+constexpr int kMoeMaxExperts = 4096;
 
 size_t block_elems(int fmt) { return fmt == NNQ_FMT_Q8_0 ? 32 : 256; }
 size_t block_bytes(int fmt) {
@@ -543,7 +546,7 @@ static int moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed,
     if (H % 32 || I % 32)
         return fail(NNQ_ERR_INVALID_SHAPE, "MoE hidden (%lld) and intermediate (%lld) sizes must be multiples of 32",
                     (long long)H, (long long)I);
-    if (E > 256) return fail(NNQ_ERR_UNSUPPORTED, "at most 256 experts");
+    if (E > kMoeMaxExperts) return fail(NNQ_ERR_UNSUPPORTED, "at most %d experts", kMoeMaxExperts);
     const size_t gu_el = (size_t)E * H * 2 * I, dn_el = (size_t)E * I * H;
     nnq_moe *m = new nnq_moe;
     hipGetDevice(&m->device);
@@ -795,8 +798,8 @@ int nnq_router_create(int64_t num_experts, int64_t hidden, const float *weight, 
     if (!out) return fail(NNQ_ERR_INVALID_ARGUMENT, "out is null");
     *out = nullptr;
     if (!weight) return fail(NNQ_ERR_INVALID_ARGUMENT, "router weight is null");
-    if (num_experts <= 0 || num_experts > 256)
-        return fail(NNQ_ERR_INVALID_SHAPE, "router experts %lld (1..256)", (long long)num_experts);
+    if (num_experts <= 0 || num_experts > kMoeMaxExperts)
+        return fail(NNQ_ERR_INVALID_SHAPE, "router experts %lld (1..%d)", (long long)num_experts, kMoeMaxExperts);
     if (hidden <= 0 || hidden % 32)
         return fail(NNQ_ERR_INVALID_SHAPE, "router hidden %lld is not a positive multiple of 32", (long long)hidden);
     nnq_router *r = new nnq_router;

@@ -127,7 +127,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }  // namespace
 
 // ---------------------------------------------------------------------------------
-// routing: one wave per token, lane c holds logits c, c + 64, ... (E <= 256)
+// routing: one wave per token, lane c holds logits c, c + 64, ... (E <= 256; more: moe_route_any_kernel)
 // ---------------------------------------------------------------------------------
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
@@ -246,16 +246,102 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *logits, int
     }
 }
 
+// Routing for E > 256 experts: the same computation as moe_route_kernel with the
+// token's values in LDS (one row of E floats per wave, dynamic shared memory); the
+// selection rounds mark a chosen expert by key 0 (every probability key is above it).
+__global__ __launch_bounds__(256) void moe_route_any_kernel(const float *logits, int nsplit, const float *bias,
+                                                            int64_t T, int E, int k, uint32_t *ti, float *tw,
+                                                            uint32_t *ti_out, float *tw_out) {
+    extern __shared__ __attribute__((aligned(16))) float rowbuf[];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t t = (int64_t)blockIdx.x * 4 + wv;
+    if (t >= T) return;  // wave-uniform; no barrier below
+    float *v = rowbuf + (size_t)wv * E;
+    uint32_t *key = reinterpret_cast<uint32_t *>(v);
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    float mx = -INFINITY;
+    int ninf = 0;
+    for (int c = lane; c < E; c += 64) {
+        float lv = logits[t * E + c];
+        for (int sp = 1; sp < nsplit; sp++) lv += logits[((int64_t)sp * T + t) * E + c];
+        if (bias) lv += bias[c];
+        v[c] = lv;
+        mx = fmaxf(mx, lv);
+        ninf += lv == INFINITY;
+    }
+    mx = wave_max(mx);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ninf += __shfl_xor(ninf, o, 64);
+    // probabilities (softmax with the sum in index order, as moe_route_kernel)
+    if (mx == -INFINITY || mx == INFINITY) {
+        for (int c = lane; c < E; c += 64) v[c] = (mx == INFINITY && v[c] == INFINITY) ? 1.0f / (float)ninf : 0.0f;
+        wave_sync();
+    } else {
+        for (int c = lane; c < E; c += 64) v[c] = expf(v[c] - mx);
+        wave_sync();
+        float sum = -0.0f;
+        for (int c = 0; c < E; c++) sum = sum + v[c];
+        wave_sync();
+        for (int c = lane; c < E; c += 64) v[c] = v[c] / sum;
+        wave_sync();
+    }
+    // top-k: descending by total order, ties to the lowest index; the probability keys
+    // replace the values in LDS (a chosen expert's key becomes 0)
+    uint32_t idx[8];
+    float val[8];
+    for (int c = lane; c < E; c += 64) key[c] = (uint32_t)total_key(v[c]) ^ 0x80000000u;
+    wave_sync();
+    for (int s = 0; s < k; s++) {
+        uint64_t best = 0;
+        for (int c = lane; c < E; c += 64) {
+            const uint64_t kk = ((uint64_t)key[c] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)c);
+            if (key[c] != 0u) best = kk > best ? kk : best;
+        }
+        best = wave_max_u64(best);
+        const uint32_t c = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu);
+        const uint32_t o = (uint32_t)(best >> 32) ^ 0x80000000u;  // back to the total-order key
+        // the key -> float inverse of total_key
+        const int32_t b = (int32_t)o;
+        idx[s] = c;
+        val[s] = __int_as_float(b ^ (int32_t)((uint32_t)(b >> 31) >> 1));
+        wave_sync();
+        if (lane == 0) key[c] = 0u;
+        wave_sync();
+    }
+    float ssum = -0.0f;
+    for (int s = 0; s < k; s++) ssum = ssum + val[s];
+    if (lane < k) {
+        uint32_t ci = 0;
+        float cv = 0.0f;
+        for (int s = 0; s < k; s++)
+            if (s == lane) {
+                ci = idx[s];
+                cv = val[s];
+            }
+        const float w = cv / ssum;
+        ti[t * k + lane] = ci;
+        tw[t * k + lane] = w;
+        if (ti_out) ti_out[t * k + lane] = ci;
+        if (tw_out) tw_out[t * k + lane] = w;
+    }
+}
+
 // One workgroup of 1024 threads, one token per thread per chunk of 1024 tokens.  For
 // each expert a ballot gives every token its rank among the wave's tokens that chose
 // the expert; per-wave counts in LDS turn that into the rank over all earlier tokens.
 // Expert e's rows are then its tokens in ascending order (stable by token, the order
 // moe_forward's grouping loop builds, crates/nn-gptoss/src/quantized_model.rs:157-169).
+// Experts go in groups of 256 (the per-wave count table); the running per-expert
+// totals live in dynamic shared memory (E ints).
 template <int k>
 __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, int64_t T, int E, int32_t *off,
                                                            int32_t *stok, int32_t *pos) {
     __shared__ int32_t wcnt[16][256];
-    __shared__ int32_t base[256];
+    extern __shared__ int32_t base[];  // [E]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
     for (int e = tid; e < E; e += 1024) base[e] = 0;
@@ -263,71 +349,81 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, i
     for (int64_t t0 = 0; t0 < T; t0 += 1024) {
         const int64_t t = t0 + tid;
         uint32_t ex[k];
-        int32_t rk[k];
 #pragma unroll
-        for (int s = 0; s < k; s++) {
-            ex[s] = t < T ? ti[t * k + s] : 0xFFFFFFFFu;
-            rk[s] = 0;
-        }
-        for (int e = 0; e < E; e++) {
-            bool hit = false;
+        for (int s = 0; s < k; s++) ex[s] = t < T ? ti[t * k + s] : 0xFFFFFFFFu;
+        for (int g0 = 0; g0 < E; g0 += 256) {
+            const int ge = min(256, E - g0);
+            int32_t rk[k];
 #pragma unroll
-            for (int s = 0; s < k; s++) hit |= ex[s] == (uint32_t)e;
-            const uint64_t m = __ballot(hit);
-            const int32_t r = __popcll(m & lt);
+            for (int s = 0; s < k; s++) rk[s] = 0;
+            for (int e = 0; e < ge; e++) {
+                const uint32_t ee = (uint32_t)(g0 + e);
+                bool hit = false;
 #pragma unroll
-            for (int s = 0; s < k; s++)
-                if (ex[s] == (uint32_t)e) rk[s] = r;
-            if (lane == 0) wcnt[wv][e] = __popcll(m);
-        }
-        __syncthreads();
-        // per expert (one per thread): wcnt[w][e] becomes the count of earlier tokens,
-        // base[e] plus the waves before w (the 16 loads independent of each other)
-        for (int e = tid; e < E; e += 1024) {
-            int32_t c[16];
+                for (int s = 0; s < k; s++) hit |= ex[s] == ee;
+                const uint64_t m = __ballot(hit);
+                const int32_t r = __popcll(m & lt);
 #pragma unroll
-            for (int w = 0; w < 16; w++) c[w] = wcnt[w][e];
-            int32_t run = base[e];
-#pragma unroll
-            for (int w = 0; w < 16; w++) {
-                wcnt[w][e] = run;
-                run += c[w];
+                for (int s = 0; s < k; s++)
+                    if (ex[s] == ee) rk[s] = r;
+                if (lane == 0) wcnt[wv][e] = __popcll(m);
             }
-            base[e] = run;
-        }
-        __syncthreads();
-        if (t < T)
+            __syncthreads();
+            // per expert (one per thread): wcnt[w][e] becomes the count of earlier tokens,
+            // base plus the waves before w (the 16 loads independent of each other)
+            for (int e = tid; e < ge; e += 1024) {
+                int32_t c[16];
 #pragma unroll
-            for (int s = 0; s < k; s++)
-                pos[t * k + s] = wcnt[wv][ex[s]] + rk[s];  // rank within the expert; offset below
-        __syncthreads();  // wcnt is rewritten by the next chunk
+                for (int w = 0; w < 16; w++) c[w] = wcnt[w][e];
+                int32_t run = base[g0 + e];
+#pragma unroll
+                for (int w = 0; w < 16; w++) {
+                    wcnt[w][e] = run;
+                    run += c[w];
+                }
+                base[g0 + e] = run;
+            }
+            __syncthreads();
+            if (t < T)
+#pragma unroll
+                for (int s = 0; s < k; s++)
+                    if (ex[s] >= (uint32_t)g0 && ex[s] < (uint32_t)(g0 + ge))
+                        pos[t * k + s] = wcnt[wv][ex[s] - g0] + rk[s];  // rank within the expert; offset below
+            __syncthreads();  // wcnt is rewritten by the next group / chunk
+        }
     }
     if (tid < 64) {
-        // exclusive scan of the expert counts: lane l holds experts 4l .. 4l + 3 (E <= 256)
-        int32_t c[4], sum = 0;
+        // exclusive scan of the expert counts, 256 at a time: lane l holds experts
+        // c0 + 4l .. c0 + 4l + 3, the carry is the total of the earlier groups
+        int32_t carry = 0;
+        for (int c0 = 0; c0 < E; c0 += 256) {
+            int32_t c[4], sum = 0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int e = 4 * tid + j;
-            c[j] = e < E ? base[e] : 0;
-            sum += c[j];
-        }
-        int32_t before = sum;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int32_t v = __shfl_up(before, o, 64);
-            if (tid >= o) before += v;
-        }
-        if (tid == 63) off[E] = before;  // the total
-        before -= sum;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int e = 4 * tid + j;
-            if (e < E) {
-                base[e] = before;
-                off[e] = before;
+            for (int j = 0; j < 4; j++) {
+                const int e = c0 + 4 * tid + j;
+                c[j] = e < E ? base[e] : 0;
+                sum += c[j];
             }
-            before += c[j];
+            int32_t before = sum;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int32_t v = __shfl_up(before, o, 64);
+                if (tid >= o) before += v;
+            }
+            const int32_t total = __shfl(before, 63, 64);
+            before += carry - sum;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = c0 + 4 * tid + j;
+                if (e < E) {
+                    base[e] = before;
+                    off[e] = before;
+                }
+                before += c[j];
+            }
+            carry += total;
         }
+        if (tid == 0) off[E] = carry;  // the total
     }
     __syncthreads();
     for (int64_t i = tid; i < T * k; i += 1024) {
@@ -863,13 +959,17 @@ int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const floa
     MoeRun run;
     run.A = T * k;
     run.limit = limit;
-    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, nsplit, bias, T,
-                       (int)d.E, k, sc.ti, sc.tw, topk_idx, topk_w);
+    if (d.E <= 256)
+        hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, nsplit, bias, T,
+                           (int)d.E, k, sc.ti, sc.tw, topk_idx, topk_w);
+    else
+        hipLaunchKernelGGL(moe_route_any_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), (size_t)4 * d.E * 4, st,
+                           logits, nsplit, bias, T, (int)d.E, k, sc.ti, sc.tw, topk_idx, topk_w);
     switch (k) {
 #define NNQ_PERM(K)                                                                                              \
     case K:                                                                                                      \
-        hipLaunchKernelGGL(moe_permute_kernel<K>, dim3(1), dim3(1024), 0, st, sc.ti, T, (int)d.E, sc.off, sc.stok, \
-                           sc.pos);                                                                              \
+        hipLaunchKernelGGL(moe_permute_kernel<K>, dim3(1), dim3(1024), (size_t)d.E * 4, st, sc.ti, T, (int)d.E, sc.off, \
+                           sc.stok, sc.pos);                                                                     \
         break;
         NNQ_PERM(1) NNQ_PERM(2) NNQ_PERM(3) NNQ_PERM(4) NNQ_PERM(5) NNQ_PERM(6) NNQ_PERM(7) NNQ_PERM(8)
 #undef NNQ_PERM

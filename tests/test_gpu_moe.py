@@ -119,6 +119,30 @@ def test_moe_uneven_loads_vs_oracle(O, dev, E, H, I, T, k, xdt, skew):
     check_close(ref, y.cpu().numpy(), f"moe uneven E={E} H={H} I={I} T={T} k={k} x={xdt} skew={skew}")
 
 
+# More than 256 experts (Kimi-K2-style 384, odd counts, a batch over two 1024-token
+# permutation chunks): routing keeps the token's probabilities in LDS, the permutation
+# walks the experts in groups of 256.
+@pytest.mark.parametrize("E,H,I,T,k,xdt", [(384, 64, 64, 100, 8, "bf16"), (1000, 96, 64, 300, 4, "f32"),
+                                          (300, 64, 64, 1100, 2, "bf16"), (257, 64, 32, 64, 6, "f32")])
+def test_moe_many_experts_vs_oracle(O, dev, E, H, I, T, k, xdt):
+    import nn_amd
+    L = make_layer(E, H, I, seed=E + T)
+    moe = upload(L, E, H, I)
+    x = torch.from_numpy(nn_amd.synth_normal(17, 5, (T, H), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    lg = nn_amd.synth_normal(17, 6, (T, E), 1.0)
+    lg[0, 5] = np.inf       # a +inf logit: uniform over the +inf entries of that token
+    lg[1, : E // 2] = -np.inf  # zero probabilities for half of the experts
+    lg[2, E - 1] = 40.0     # the last expert first
+    logits = torch.from_numpy(lg).to(dev)
+    y, ti, tw = moe.forward(x, logits, top_k=k, return_routing=True)
+    ref, rti, rtw = O.moe_forward(x.float().cpu().numpy(), lg, k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    assert np.array_equal(ti.cpu().numpy().astype(np.uint32), rti), "routing differs"
+    assert np.allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    check_close(ref, y.cpu().numpy(), f"moe E={E} H={H} I={I} T={T} k={k} x={xdt}")
+
+
 def test_moe_expert_dequant_bit_exact(O, dev):
     E, H, I = 3, 96, 64
     L = make_layer(E, H, I, seed=5)
@@ -174,7 +198,8 @@ def make_router(E, H, seed):
     return nn_amd.synth_normal(seed, 7, (E, H), 0.02), nn_amd.synth_normal(seed, 8, (E,), 0.1)
 
 
-@pytest.mark.parametrize("E,H,T,xdt", [(32, 2880, 256, "bf16"), (32, 2880, 37, "f32"), (20, 96, 5, "bf16")])
+@pytest.mark.parametrize("E,H,T,xdt", [(32, 2880, 256, "bf16"), (32, 2880, 37, "f32"), (20, 96, 5, "bf16"),
+                                      (384, 128, 33, "f32")])
 def test_router_logits_vs_oracle(O, dev, E, H, T, xdt):
     """The router Linear on the f32 MFMA against the oracle's f32 x @ W^T + b (same
     products, another summation order): max abs difference <= 1e-5 of the peak."""
@@ -193,7 +218,7 @@ def test_router_logits_vs_oracle(O, dev, E, H, T, xdt):
 
 
 @pytest.mark.parametrize("E,H,I,T,k,xdt", [(8, 256, 320, 64, 4, "bf16"), (16, 96, 64, 150, 4, "f32"),
-                                          (32, 2880, 2880, 256, 4, "bf16")])
+                                          (32, 2880, 2880, 256, 4, "bf16"), (300, 64, 64, 40, 4, "f32")])
 def test_moe_block_vs_oracle(O, dev, E, H, I, T, k, xdt):
     """moe_forward with its router: device logits, routing, experts and combine against
     the oracle's router Linear followed by its moe_forward restatement."""
