@@ -50,13 +50,6 @@ __device__ __forceinline__ uint32_t pk_mul_bcast(uint32_t a, uint32_t s) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) * b);
 }
 
-// s_waitcnt vmcnt(N) only (expcnt and lgkmcnt left at their maxima)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 #define NNQ_GPTR(p) ((const __attribute__((address_space(1))) void *)(p))
 #define NNQ_LPTR(p) ((__attribute__((address_space(3))) void *)(p))
 

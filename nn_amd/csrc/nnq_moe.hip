@@ -117,13 +117,6 @@ __device__ __forceinline__ void fp4_b_operands(const uint8_t *codes, const uint8
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 
-// s_waitcnt vmcnt(N) only (expcnt and lgkmcnt left at their maxima)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------------------------
