@@ -687,20 +687,31 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
             // [1]: 2 * l16 + 1
             auto epilogue = [&](auto &acc) {
                 constexpr int MTN = (int)std::extent<std::remove_reference_t<decltype(acc)>, 1>::value;
+                // the bases, the row range and the row lengths pass through an empty asm
+                // here, so the row offsets and row masks below are formed after the K loop
+                // (hoisted above it, they were 16 live 64-bit offsets and 16 masks per lane
+                // across the loop, i.e. register spills)
+                uint16_t *hbp = sc.hb;
+                float *ybp = sc.yb;
+                const float *gub = d.gu_b, *dnb = d.dn_b;
+                int64_t Ie = I, He = H;
+                int32_t r0e = r0, nee = ne, m0e = m0;
+                asm volatile("" : "+s"(hbp), "+s"(ybp), "+s"(gub), "+s"(dnb), "+s"(Ie), "+s"(He), "+s"(r0e), "+s"(nee),
+                             "+s"(m0e));
                 if (GU) {
                     const int64_t col0 = (int64_t)st * 32;
 #pragma unroll
                     for (int mt = 0; mt < MTN; mt++) {
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
-                            const int32_t r = m0 + mt * 16 + 4 * p + i;
-                            if (r >= ne) continue;
+                            const int32_t r = m0e + mt * 16 + 4 * p + i;
+                            if (r >= nee) continue;
                             uint32_t hh = 0, hl = 0;
 #pragma unroll
                             for (int o = 0; o < 2; o++) {
                                 const int64_t c = col0 + 2 * l16 + o;
-                                const float gt = acc[0][mt][o][i] + d.gu_b[e * 2 * I + c];
-                                const float up = acc[1][mt][o][i] + d.gu_b[e * 2 * I + I + c];
+                                const float gt = acc[0][mt][o][i] + gub[e * 2 * Ie + c];
+                                const float up = acc[1][mt][o][i] + gub[e * 2 * Ie + Ie + c];
                                 // silu (crates/nn-core/src/dyn_tensor/ops/math.rs:140), clamped to +-limit
                                 float sg = gt / (1.0f + expf(-gt));
                                 sg = sg < -run.limit ? -run.limit : (sg > run.limit ? run.limit : sg);
@@ -709,21 +720,21 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
                                 hh |= bh << (16 * o);
                                 hl |= (uint32_t)bf16_rne(h - bf16_to_f32(bh)) << (16 * o);
                             }
-                            const int64_t o2 = (int64_t)(r0 + r) * I + col0 + 2 * l16;
-                            *reinterpret_cast<uint32_t *>(sc.hb + o2) = hh;
-                            *reinterpret_cast<uint32_t *>(sc.hb + run.A * I + o2) = hl;
+                            const int64_t o2 = (int64_t)(r0e + r) * Ie + col0 + 2 * l16;
+                            *reinterpret_cast<uint32_t *>(hbp + o2) = hh;
+                            *reinterpret_cast<uint32_t *>(hbp + run.A * Ie + o2) = hl;
                         }
                     }
                 } else {
                     const int64_t col0 = (int64_t)st * 32 + 2 * l16;
-                    const float b0 = d.dn_b[e * H + col0], b1 = d.dn_b[e * H + col0 + 1];
+                    const float b0 = dnb[e * He + col0], b1 = dnb[e * He + col0 + 1];
 #pragma unroll
                     for (int mt = 0; mt < MTN; mt++) {
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
-                            const int32_t r = m0 + mt * 16 + 4 * p + i;
-                            if (r >= ne) continue;
-                            *reinterpret_cast<float2 *>(sc.yb + (int64_t)(r0 + r) * H + col0) =
+                            const int32_t r = m0e + mt * 16 + 4 * p + i;
+                            if (r >= nee) continue;
+                            *reinterpret_cast<float2 *>(ybp + (int64_t)(r0e + r) * He + col0) =
                                 float2{acc[0][mt][0][i] + b0, acc[0][mt][1][i] + b1};
                         }
                     }
