@@ -547,6 +547,8 @@ static int moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed,
         return fail(NNQ_ERR_INVALID_SHAPE, "MoE hidden (%lld) and intermediate (%lld) sizes must be multiples of 32",
                     (long long)H, (long long)I);
     if (E > kMoeMaxExperts) return fail(NNQ_ERR_UNSUPPORTED, "at most %d experts", kMoeMaxExperts);
+    // the expert kernels address a chunk's activation planes with 32-bit byte offsets
+    if (H > 32768 || I > 32768) return fail(NNQ_ERR_UNSUPPORTED, "MoE hidden and intermediate sizes at most 32768");
     const size_t gu_el = (size_t)E * H * 2 * I, dn_el = (size_t)E * I * H;
     nnq_moe *m = new nnq_moe;
     hipGetDevice(&m->device);

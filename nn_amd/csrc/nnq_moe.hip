@@ -600,8 +600,13 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
 
     for (int32_t m0 = 0; m0 < ne; m0 += 64) {
         const int mtn = (ne - m0) >= 64 ? 4 : (ne - m0 + 15) / 16;  // live row tiles
-        // copy sources of this pass: granule c -> (plane, row, slot); chunk ch at + ch * CKB * 32 k
-        const uint16_t *asrc[LPA];
+        // copy sources of this pass: granule c -> (plane, row, slot); chunk ch at + ch * CKB * 32 k.
+        // A 32-bit byte offset per lane from one uniform base (the planes of an activation
+        // are one buffer: x hi / lo at xa[0] and xa[0] + T H, h hi / lo at hb and hb + A I;
+        // the host keeps them under 4 GB), so a copy address costs one VGPR, not two
+        const unsigned char *abase = reinterpret_cast<const unsigned char *>(GU ? run.xa[0] : sc.hb);
+        const int64_t pstride = GU ? (run.xa[1] ? run.xa[1] - run.xa[0] : 0) : run.A * I;  // elements per plane
+        uint32_t aoff[LPA];
 #pragma unroll
         for (int j = 0; j < LPA; j++) {
             const int c = min(j * NTH + tid, C::ACH - 1);
@@ -609,17 +614,17 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
             const int r = rem / C::ROWG, slot = rem % C::ROWG;
             const int kc = moe_slot(slot, r);  // the row's 16-byte granule held at this slot
             const int32_t rr = r0 + m0 + min(r, ne - m0 - 1);  // rows past the expert repeat its last row
-            asrc[j] = (GU ? run.xa[pl] + (int64_t)sc.stok[rr] * H : sc.hb + (int64_t)pl * run.A * I + (int64_t)rr * I) +
-                      8 * kc;
+            aoff[j] = (uint32_t)(2 * ((int64_t)pl * pstride + (GU ? (int64_t)sc.stok[rr] * H : (int64_t)rr * I) + 8 * kc));
         }
         auto issue = [&](int ch) {
             const int cv = min(ch, nch - 1);  // past the end: re-copy the last chunk
             unsigned char *buf = smem + (size_t)(ch % NBUF) * C::BUF;
+            const unsigned char *cb = abase + (size_t)cv * CKB * 64;
 #pragma unroll
             for (int j = 0; j < LPA; j++)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)(asrc[j] + (int64_t)cv * CKB * 32),
-                    (__attribute__((address_space(3))) void *)(buf + (size_t)(j * NTH + wv * 64) * 16), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(cb + aoff[j]),
+                                                 (__attribute__((address_space(3))) void *)(buf + (size_t)(j * NTH + wv * 64) * 16),
+                                                 16, 0, 0);
         };
         const int nround = (s_hi - s_lo + kMoeWaves - 1) / kMoeWaves;
         for (int rd = 0; rd < nround; rd++) {
