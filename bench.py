@@ -117,7 +117,12 @@ def time_windows(fn_list, steps, warmup, windows):
     return stats(per)
 
 
+WINDOWS = None  # --windows: a fixed window count (profiler runs), else sized to a time budget
+
+
 def windows_for(steps, per_call_s, budget_s=0.5, lo=5, hi=40):
+    if WINDOWS:
+        return WINDOWS
     return int(max(lo, min(hi, budget_s / max(steps * per_call_s, 1e-9))))
 
 
@@ -513,7 +518,11 @@ def main():
     ap.add_argument("--only", default="", help="comma list: headline,q8_0,gateup,mlp,lm_head,gemm,moe,floor")
     ap.add_argument("--only-headline", action="store_true", help="same as --only headline --no-single")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--windows", type=int, default=0,
+                    help="timed replays per config (default: as many as fit 0.5 s, 5 to 40)")
     args = ap.parse_args()
+    global WINDOWS
+    WINDOWS = args.windows if args.windows > 0 else None
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every box in this run has one MI355X, and the quantized-linear "
               "kernels run on one device's share (the multi-GPU sharding is a design note only)", file=sys.stderr)
