@@ -11,9 +11,10 @@
 //   B: the raw tile16 bytes of group p: tile x plane x 16 rows x 16 bytes;
 // and the super-block headers ride along with the first stage of each super-block.
 //
-// Four waves side by side, each a BM x BN/4 wave tile (WGN = 4; WGN = 2 gives 2 x 2
-// waves of BM/2 x BN/2); every wave dequantizes the raw bytes of its own columns in
-// registers (no dequantized copy through LDS):
+// NW waves (4 or 8) in WGN wave columns: four side by side, each a BM x BN/4 wave tile
+// (WGN = 4; WGN = 2 gives 2 x 2 waves of BM/2 x BN/2), or eight as 2 x 4 of BM/2 x BN/4;
+// every wave dequantizes the raw bytes of its own columns in registers (no dequantized
+// copy through LDS):
 // consumer lane 16G + r takes bytes 8G .. 8G + 7 of row r's group (plane G >> 1), whose
 // low nibbles are k = 64p + 8G + i of sub-block 2p and high nibbles k = 64p + 32 + 8G + i
 // of sub-block 2p + 1, so each stage is two MFMA steps of 32 k, one sub-block each, and
@@ -53,11 +54,11 @@ __device__ __forceinline__ uint32_t pk_mul_bcast(uint32_t a, uint32_t s) {
 #define NNQ_GPTR(p) ((const __attribute__((address_space(1))) void *)(p))
 #define NNQ_LPTR(p) ((__attribute__((address_space(3))) void *)(p))
 
-template <int BN, int NBUF, int WGN, int BM_>
+template <int BN, int NBUF, int WGN, int BM_, int NW>
 struct RK {
-    // WGN wave columns x (4 / WGN) wave rows, wave tile WM x (BN / WGN)
-    static constexpr int BM = BM_, NTH = 256, NTILE = BN / 16, NT = NTILE / WGN;
-    static constexpr int WM = BM * WGN / 4, MT = WM / 16;
+    // NW waves: WGN wave columns x (NW / WGN) wave rows, wave tile WM x (BN / WGN)
+    static constexpr int BM = BM_, NTH = NW * 64, NTILE = BN / 16, NT = NTILE / WGN;
+    static constexpr int WM = BM * WGN / NW, MT = WM / 16;
     static constexpr int A_CH = BM * 8, B_CH = NTILE * 32, CH = A_CH + B_CH;
     static constexpr int LPT = (CH + NTH - 1) / NTH;  // copy instructions per thread and stage
     static constexpr int BUF = LPT * NTH * 16;
@@ -96,9 +97,9 @@ constexpr int rk_wait(int p) {
     return n;
 }
 
-template <int BN, int NBUF, int WGN, int BM_>
-__global__ __launch_bounds__(256) void gemm_q4k_rk_kernel(GemmArgs a, GemmScratch sc) {
-    using C = RK<BN, NBUF, WGN, BM_>;
+template <int BN, int NBUF, int WGN, int BM_, int NW>
+__global__ __launch_bounds__(NW * 64) void gemm_q4k_rk_kernel(GemmArgs a, GemmScratch sc) {
+    using C = RK<BN, NBUF, WGN, BM_, NW>;
     constexpr int MT = C::MT, NT = C::NT, LPT = C::LPT, NTH = C::NTH, BM = C::BM;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     unsigned char *ring = smem;
@@ -400,18 +401,18 @@ __global__ __launch_bounds__(256) void gemm_finalize_kernel(const float *ys, int
         *reinterpret_cast<floatx4 *>(reinterpret_cast<float *>(y) + i) = v;
 }
 
-template <int BN, int NBUF, int WGN, int BM>
+template <int BN, int NBUF, int WGN, int BM, int NW>
 int launch_rk(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    using C = RK<BN, NBUF, WGN, BM>;
+    using C = RK<BN, NBUF, WGN, BM, NW>;
     static bool attr_set = false;  // idempotent attribute write; races only repeat it
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_rk_kernel<BN, NBUF, WGN, BM>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_rk_kernel<BN, NBUF, WGN, BM, NW>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
     }
     const int nct = (int)((a.ntile * 16 + BN - 1) / BN), nrt = (int)((a.m + C::BM - 1) / C::BM);
-    hipLaunchKernelGGL((gemm_q4k_rk_kernel<BN, NBUF, WGN, BM>), dim3((unsigned)(nct * nrt * sc.ksplit)), dim3(C::NTH), C::LDS,
+    hipLaunchKernelGGL((gemm_q4k_rk_kernel<BN, NBUF, WGN, BM, NW>), dim3((unsigned)(nct * nrt * sc.ksplit)), dim3(C::NTH), C::LDS,
                        st, a, sc);
     int e = (int)hipGetLastError();
     if (e || sc.ksplit == 1) return e;
@@ -465,13 +466,16 @@ int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     const int ksplit = gemm_ring_plan(a, &bn, &bm);
     if (ksplit == 0 || sc.ksplit != ksplit || (ksplit > 1 && !sc.ysplit)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
-    // waves side by side (BM rows x BN / 4 columns each): measured 4-5% faster on MI355X
-    // than 2 x 2 (BM / 2 x BN / 2), which halves the A reads from LDS but doubles the
-    // dequantization of every column
-    // the smaller row tiles leave LDS for a deeper ring (more stages in flight)
-    if (bm == 32) return bn == 192 ? launch_rk<192, 6, 4, 32>(a, sc, st) : launch_rk<128, 6, 4, 32>(a, sc, st);
-    if (bm == 64) return bn == 192 ? launch_rk<192, 6, 4, 64>(a, sc, st) : launch_rk<128, 6, 4, 64>(a, sc, st);
-    return bn == 192 ? launch_rk<192, 4, 4, 128>(a, sc, st) : launch_rk<128, 4, 4, 128>(a, sc, st);
+    // four waves side by side (BM rows x BN / 4 columns each): measured 4-5% faster on
+    // MI355X than 2 x 2 (BM / 2 x BN / 2), which halves the A reads from LDS but doubles
+    // the dequantization of every column.  128 x 192 tiles take eight waves (2 x 4 of
+    // 64 x 48, two per SIMD, 178 registers each): 3-7% faster at M = 128 and 512; the
+    // 128-wide tiles measured 3% slower with eight, and 4 x 2 waves of 32 x 96 (four
+    // dequantizations per column) 30-40% slower.
+    // The smaller row tiles leave LDS for a deeper ring (more stages in flight).
+    if (bm == 32) return bn == 192 ? launch_rk<192, 6, 4, 32, 4>(a, sc, st) : launch_rk<128, 6, 4, 32, 4>(a, sc, st);
+    if (bm == 64) return bn == 192 ? launch_rk<192, 6, 4, 64, 4>(a, sc, st) : launch_rk<128, 6, 4, 64, 4>(a, sc, st);
+    return bn == 192 ? launch_rk<192, 4, 4, 128, 8>(a, sc, st) : launch_rk<128, 4, 4, 128, 4>(a, sc, st);
 }
 
 }  // namespace nnq

@@ -143,6 +143,32 @@ def test_moe_many_experts_vs_oracle(O, dev, E, H, I, T, k, xdt):
     check_close(ref, y.cpu().numpy(), f"moe E={E} H={H} I={I} T={T} k={k} x={xdt}")
 
 
+# Routing on batches across the 1024-token permutation chunk and small to medium
+# expert counts, with special rows: a +inf logit, half the experts at -inf, exact ties
+# that go to the lowest index, the last expert first.
+@pytest.mark.parametrize("E,T,k", [(32, 1024, 4), (32, 1025, 4), (20, 7, 3), (33, 300, 4), (32, 1, 8), (2, 600, 2)])
+def test_moe_routing_special_rows(O, dev, E, T, k):
+    import nn_amd
+    H, I = 64, 32
+    L = make_layer(E, H, I, seed=E * 3 + T)
+    moe = upload(L, E, H, I)
+    x = torch.from_numpy(nn_amd.synth_normal(19, 5, (T, H), 1.0)).to(dev).to(torch.bfloat16)
+    lg = nn_amd.synth_normal(19, 6, (T, E), 2.0)
+    if T > 3:
+        lg[1, min(3, E - 1)] = np.inf
+        lg[2, : E // 2] = -np.inf
+        lg[3, :] = 0.5  # every probability equal: experts 0 .. k-1
+    lg[-1, E - 1] = 40.0
+    logits = torch.from_numpy(lg).to(dev)
+    y, ti, tw = moe.forward(x, logits, top_k=k, return_routing=True)
+    ref, rti, rtw = O.moe_forward(x.float().cpu().numpy(), lg, k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    assert np.array_equal(ti.cpu().numpy().astype(np.uint32), rti), "routing differs"
+    assert np.allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    if T > 3:
+        assert list(rti[3]) == list(range(k))
+    check_close(ref, y.cpu().numpy(), f"moe routing E={E} T={T} k={k}")
+
+
 def test_moe_expert_dequant_bit_exact(O, dev):
     E, H, I = 3, 96, 64
     L = make_layer(E, H, I, seed=5)
