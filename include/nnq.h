@@ -246,9 +246,10 @@ int nnq_mlp_forward(const nnq_mlp *mlp, const void *x, nnq_dtype x_dtype, int64_
  *           (packed bytes E*hidden*2*inter/2, scales E*hidden*2*inter/32),
  *  down:    Mxfp4Tensor of the flat [E, inter, hidden] tensor,
  *  biases:  f32 [E, 2*inter] and [E, hidden] (host).
- * hidden and inter must be multiples of 32 (NNQ_ERR_INVALID_SHAPE), at most 4096
- * experts (NNQ_ERR_UNSUPPORTED beyond).  The codes are repacked on upload into per-(expert, 32-column block,
- * 32-row block) fragments in MFMA lane order (a permutation of the bytes).
+ * hidden and inter must be multiples of 32 (NNQ_ERR_INVALID_SHAPE), at most 32768 each and
+ * at most 4096 experts (NNQ_ERR_UNSUPPORTED beyond; checked before any allocation).  The
+ * codes are repacked on upload into per-(expert, 32-column block, 32-row block)
+ * fragments in MFMA lane order (a permutation of the bytes).
  * Replaces QuantizedDecoderLayer::load's expert tensors
  * (crates/nn-gptoss/src/quantized_model.rs:70-78). */
 int nnq_moe_create(int64_t num_experts, int64_t hidden, int64_t inter, const uint8_t *gu_packed,
@@ -257,7 +258,8 @@ int nnq_moe_create(int64_t num_experts, int64_t hidden, int64_t inter, const uin
 
 /* The same upload from nn-core OCP MXFP4 tensors (NNQ_LAYOUT_OCP): gu_blocks holds the
  * quantize_tensor blocks of the flat [E, hidden, 2*inter] tensor (E*hidden*2*inter/32
- * blocks of 17 bytes), dn_blocks those of [E, inter, hidden]; biases as nnq_moe_create.
+ * blocks of 17 bytes), dn_blocks those of [E, inter, hidden]; biases and shape limits as
+ * nnq_moe_create.
  * Both layouts decode to the same values on the device: every E8M0 byte e scales by
  * 2^(e - 127), GPT-OSS's byte 0 being stored as 1.  Replaces the expert tensors of an MoE
  * whose weights come from mxfp4_quantize_tensor

@@ -533,6 +533,18 @@ int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const floa
 
 }  // extern "C"
 
+// The expert shapes the kernels take: hidden and intermediate multiples of 32, at most
+// 32768 (the expert kernels address a chunk's activation planes with 32-bit byte
+// offsets), at most kMoeMaxExperts experts; checked before any allocation or copy.
+static int moe_check_shape(int64_t E, int64_t H, int64_t I) {
+    if (H % 32 || I % 32)
+        return fail(NNQ_ERR_INVALID_SHAPE, "MoE hidden (%lld) and intermediate (%lld) sizes must be multiples of 32",
+                    (long long)H, (long long)I);
+    if (E > kMoeMaxExperts) return fail(NNQ_ERR_UNSUPPORTED, "at most %d experts", kMoeMaxExperts);
+    if (H > 32768 || I > 32768) return fail(NNQ_ERR_UNSUPPORTED, "MoE hidden and intermediate sizes at most 32768");
+    return 0;
+}
+
 // Upload of one layer's experts from GPT-OSS-ordered packed bytes and scale bytes
 // (gptoss_scales: GPT-OSS E8M0 semantics, byte 0 = 2^-126; else nn-core OCP, 2^-127).
 static int moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed, const uint8_t *gu_scales,
@@ -543,12 +555,7 @@ static int moe_create(int64_t E, int64_t H, int64_t I, const uint8_t *gu_packed,
     if (E <= 0 || H <= 0 || I <= 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "bad MoE shape");
     if (!gu_packed || !gu_scales || !gu_bias || !dn_packed || !dn_scales || !dn_bias)
         return fail(NNQ_ERR_INVALID_ARGUMENT, "null weight pointer");
-    if (H % 32 || I % 32)
-        return fail(NNQ_ERR_INVALID_SHAPE, "MoE hidden (%lld) and intermediate (%lld) sizes must be multiples of 32",
-                    (long long)H, (long long)I);
-    if (E > kMoeMaxExperts) return fail(NNQ_ERR_UNSUPPORTED, "at most %d experts", kMoeMaxExperts);
-    // the expert kernels address a chunk's activation planes with 32-bit byte offsets
-    if (H > 32768 || I > 32768) return fail(NNQ_ERR_UNSUPPORTED, "MoE hidden and intermediate sizes at most 32768");
+    if (int rc = moe_check_shape(E, H, I)) return rc;
     const size_t gu_el = (size_t)E * H * 2 * I, dn_el = (size_t)E * I * H;
     nnq_moe *m = new nnq_moe;
     hipGetDevice(&m->device);
@@ -605,9 +612,7 @@ int nnq_moe_create_ocp(int64_t E, int64_t H, int64_t I, const uint8_t *gu_blocks
     *out = nullptr;
     if (E <= 0 || H <= 0 || I <= 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "bad MoE shape");
     if (!gu_blocks || !dn_blocks) return fail(NNQ_ERR_INVALID_ARGUMENT, "null weight pointer");
-    if (H % 32 || I % 32)
-        return fail(NNQ_ERR_INVALID_SHAPE, "MoE hidden (%lld) and intermediate (%lld) sizes must be multiples of 32",
-                    (long long)H, (long long)I);
+    if (int rc = moe_check_shape(E, H, I)) return rc;
     const size_t gnb = (size_t)E * H * 2 * I / 32, dnb = (size_t)E * I * H / 32;
     std::vector<uint8_t> gp(gnb * 16), gs(gnb), dp(dnb * 16), ds(dnb);
     ocp_split(gu_blocks, gnb, gp.data(), gs.data());

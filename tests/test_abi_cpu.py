@@ -96,6 +96,24 @@ def test_weight_create_validation_without_device(lib):
     assert lib.nnq_linear(None, None, 0, 1, 256, None, 0, None, 0, None) == _lib.ERR_NOT_QUANTIZED
 
 
+def test_moe_create_limits_without_device(lib):
+    """The MoE upload checks its shape before any device allocation: hidden / inter
+    multiples of 32 (InvalidShape), at most 4096 experts and 32768 hidden / inter
+    (Unsupported: the expert kernels address activation chunks with 32-bit offsets)."""
+    from nn_amd import _lib
+    h = ctypes.c_void_p()
+    dummy = np.zeros(64, np.uint8)
+    vp = dummy.ctypes.data_as(ctypes.c_void_p)
+    args = lambda E, H, I: (E, H, I, vp, vp, vp, vp, vp, vp, ctypes.byref(h))
+    assert lib.nnq_moe_create(*args(4, 40, 64)) == _lib.ERR_INVALID_SHAPE
+    assert lib.nnq_moe_create(*args(4097, 64, 64)) == _lib.ERR_UNSUPPORTED
+    assert lib.nnq_moe_create(*args(4, 32800, 64)) == _lib.ERR_UNSUPPORTED
+    assert "32768" in _lib.last_error()
+    assert lib.nnq_moe_create(*args(4, 64, 32800)) == _lib.ERR_UNSUPPORTED
+    assert lib.nnq_moe_create_ocp(4, 32800, 64, vp, vp, vp, vp, ctypes.byref(h)) == _lib.ERR_UNSUPPORTED
+    assert not h.value
+
+
 def test_python_mirror_validation_without_device():
     import nn_amd
     with pytest.raises(nn_amd.WeightRank):
