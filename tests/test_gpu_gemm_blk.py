@@ -110,6 +110,19 @@ def test_gemv_gemm_crossover_consistent(O, dev, fmt):
     check_close(ref[:8], y8.cpu().numpy(), f"{fmt} m=8")
 
 
+@pytest.mark.parametrize("fmt", ["q8_0", "q6_k"])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_gemm_blk_tall_tiles(O, dev, fmt, xdt):
+    """From 1024 rows on the tiles are 128 rows high (f32 input: two staged planes, the
+    largest LDS footprint); 1100 rows leave a ragged last tile."""
+    import nn_amd
+    n, k, m = 96, 512, 1100
+    b = quantized_weight_bytes(fmt, n, k, seed=29, O=O)
+    w = make_weight(fmt, b, n, k)
+    xf, y = run(w, nn_amd.synth_normal(m, 7, (m, k), 1.0), dev, xdt)
+    check_close(oracle_linear(O, fmt, b, n, k, xf), y.cpu().numpy(), f"{fmt} m={m} x={xdt}")
+
+
 @pytest.mark.parametrize("fmt,n,k,m", [("q8_0", 4096, 4096, 128), ("q6_k", 4096, 12288, 64)])
 def test_gemm_blk_baseline_shapes(O, dev, fmt, n, k, m):
     """A Qwen3-8B-sized Q8_0 projection and the Q6_K ffn_down of Q4_K_M-style models."""

@@ -146,7 +146,8 @@ def test_moe_many_experts_vs_oracle(O, dev, E, H, I, T, k, xdt):
 # Routing on batches across the 1024-token permutation chunk and small to medium
 # expert counts, with special rows: a +inf logit, half the experts at -inf, exact ties
 # that go to the lowest index, the last expert first.
-@pytest.mark.parametrize("E,T,k", [(32, 1024, 4), (32, 1025, 4), (20, 7, 3), (33, 300, 4), (32, 1, 8), (2, 600, 2)])
+@pytest.mark.parametrize("E,T,k", [(32, 512, 4), (32, 513, 4), (32, 1024, 4), (32, 1025, 4), (20, 7, 3), (33, 300, 4),
+                                   (32, 1, 8), (2, 600, 2), (2, 200, 2)])
 def test_moe_routing_special_rows(O, dev, E, T, k):
     import nn_amd
     H, I = 64, 32
