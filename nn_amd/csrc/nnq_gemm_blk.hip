@@ -16,10 +16,11 @@
 //         (|sc * (q' & ~1)| = 2 |sc| |q' >> 1| needs at most 11 bits), two MFMAs per 32 k;
 //         a super-block's MFMAs accumulate from zero and d_n * partial is added at its end.
 //
-// Tiling: a workgroup computes BM x 64 outputs with 4 waves (2 x 2), wave tile
-// BM/2 x 32 (MT x 2 MFMA tiles).  K advances 256 per stage: the stage's activation rows,
-// the raw weight bytes of its 4 column tiles and their headers go to LDS; the next stage
-// is prefetched into registers during the current one's compute.  Split-K (KS > 1, when
+// Tiling: a workgroup computes BM x BN outputs (BN 64, or 128 for Q6_K from 256 rows)
+// with 4 waves (2 x 2), wave tile BM/2 x BN/2 (MT x NT MFMA tiles).  K advances 256 per
+// stage: the stage's activation rows, the raw weight bytes of its BN / 16 column tiles
+// and their headers go to LDS; the next stage is prefetched into registers during the
+// current one's compute.  Split-K (KS > 1, when
 // the output tiles alone would leave CUs idle): workgroup (tile, ks) covers stages
 // [ks * S / KS, (ks + 1) * S / KS) and stores its f32 partial in slab ks of the scratch;
 // gemm_blk_finalize_kernel sums the slabs in order (deterministic), adds the bias and
@@ -34,10 +35,10 @@ namespace {
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
-template <int FMT, int BM, int P>
+template <int FMT, int BM, int P, int BN_>
 struct BlkCfg {
-    static constexpr int NTH = 256, BN = 64, NTILE = BN / 16;
-    static constexpr int WM = BM / 2, MT = WM / 16, NT = 2;
+    static constexpr int NTH = 256, BN = BN_, NTILE = BN / 16;
+    static constexpr int WM = BM / 2, MT = WM / 16, NT = NTILE / 2;
     static constexpr int AST = 264;  // LDS row stride of the staged activation (f16): 256 + 8 pad
     static constexpr int TB = FMT == NNQ_FMT_Q8_0 ? 4096 : 3072;  // raw bytes per column tile and stage
     static constexpr int HB = FMT == NNQ_FMT_Q8_0 ? 256 : 288;    // header bytes per column tile and stage
@@ -90,9 +91,9 @@ __device__ __forceinline__ void q6_b_operands(uint32_t W, uint32_t Cw, uint32_t 
 
 }  // namespace
 
-template <int FMT, int BM, int P>
+template <int FMT, int BM, int P, int BN>
 __global__ __launch_bounds__(256) void gemm_blk_kernel(GemmArgs a, GemmScratch sc) {
-    using C = BlkCfg<FMT, BM, P>;
+    using C = BlkCfg<FMT, BM, P, BN>;
     constexpr int NTH = C::NTH, MT = C::MT, NT = C::NT, AST = C::AST;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     uint16_t *As = reinterpret_cast<uint16_t *>(smem);
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(256) void gemm_blk_kernel(GemmArgs a, GemmScratch s
     float *slab = KS > 1 ? sc.ysplit + (int64_t)ks * M * a.n : nullptr;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        const int64_t col = n0 + wn * 32 + nt * 16 + l16;
+        const int64_t col = n0 + wn * (NT * 16) + nt * 16 + l16;
         if (col >= a.n) continue;
         const float bcol = (a.bias && KS == 1) ? a.bias[col] : 0.0f;
 #pragma unroll
@@ -309,12 +310,12 @@ __global__ __launch_bounds__(256) void gemm_blk_finalize_kernel(const float *ys,
         reinterpret_cast<float *>(y)[i] = v;
 }
 
-template <int FMT, int BM, int P>
+template <int FMT, int BM, int P, int BN>
 static int launch_blk_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    using C = BlkCfg<FMT, BM, P>;
+    using C = BlkCfg<FMT, BM, P, BN>;
     static bool attr_set = false;  // idempotent attribute write; races only repeat it
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_blk_kernel<FMT, BM, P>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_blk_kernel<FMT, BM, P, BN>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
@@ -322,7 +323,7 @@ static int launch_blk_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t 
     const dim3 grid((unsigned)((a.ntile * 16 + C::BN - 1) / C::BN), (unsigned)((a.m + BM - 1) / BM),
                     (unsigned)sc.ksplit);
     constexpr size_t lds = C::LDS;
-    hipLaunchKernelGGL((gemm_blk_kernel<FMT, BM, P>), grid, dim3(C::NTH), lds, st, a, sc);
+    hipLaunchKernelGGL((gemm_blk_kernel<FMT, BM, P, BN>), grid, dim3(C::NTH), lds, st, a, sc);
     int e = (int)hipGetLastError();
     if (e || sc.ksplit == 1) return e;
     const int64_t cnt = a.m * a.n;
@@ -331,26 +332,32 @@ static int launch_blk_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t 
     return (int)hipGetLastError();
 }
 
-// Tile height and K split: 128-row tiles from 1024 rows on, else 64; the K split doubles
-// (up to 16, at least one stage each) while the tiles alone fill fewer than 512
+// Tile shape and K split.  Q8_0: 64 x 64 tiles, 128 x 64 from 1024 rows on.  Q6_K with
+// bf16 input: 128 x 128 tiles from 256 rows on (its operand conversion per MFMA halves;
+// measured 7% faster at 512 rows, where Q8_0 measured slower), else as Q8_0.  The K split
+// doubles (up to 16, at least one stage each) while the tiles alone fill fewer than 512
 // workgroups (two per CU).
-int gemm_blk_plan(const GemmArgs &a, int *bm) {
+int gemm_blk_plan(const GemmArgs &a, int *bm, int *bn) {
     const int64_t nstage = a.blk == NNQ_FMT_Q8_0 ? a.nblk / 8 : a.nblk;
-    const int b = a.m >= 1024 ? 128 : 64;
-    const int64_t tiles = ((a.ntile * 16 + 63) / 64) * ((a.m + b - 1) / b);
+    const bool wide = a.blk == NNQ_FMT_Q6_K && a.x_bf16 && a.m >= 256;
+    const int b = (wide || a.m >= 1024) ? 128 : 64, c = wide ? 128 : 64;
+    const int64_t tiles = ((a.ntile * 16 + c - 1) / c) * ((a.m + b - 1) / b);
     int ks = 1;
     while (tiles * ks < 512 && ks * 2 <= 16 && ks * 2 <= nstage) ks *= 2;
     if (bm) *bm = b;
+    if (bn) *bn = c;
     return ks;
 }
 
 template <int FMT, int P>
 static int launch_blk_p(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    int bm = 64;
-    const int ks = gemm_blk_plan(a, &bm);
+    int bm = 64, bn = 64;
+    const int ks = gemm_blk_plan(a, &bm, &bn);
     if (ks != sc.ksplit || (ks > 1 && !sc.ysplit)) return (int)hipErrorInvalidValue;
-    if (bm == 128) return launch_blk_cfg<FMT, 128, P>(a, sc, st);
-    return launch_blk_cfg<FMT, 64, P>(a, sc, st);
+    if constexpr (FMT == NNQ_FMT_Q6_K && P == 1)
+        if (bn == 128) return launch_blk_cfg<FMT, 128, P, 128>(a, sc, st);
+    if (bm == 128) return launch_blk_cfg<FMT, 128, P, 64>(a, sc, st);
+    return launch_blk_cfg<FMT, 64, P, 64>(a, sc, st);
 }
 
 int launch_gemm_blk(const GemmArgs &a, void *stream) {

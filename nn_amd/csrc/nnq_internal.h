@@ -131,8 +131,8 @@ struct GemmArgs {
 int launch_gemm_q4k(const GemmArgs &a, void *stream);
 // Q8_0 / Q6_K prefill GEMM (M > 8): the activation staging below, then one kernel
 int launch_gemm_blk(const GemmArgs &a, void *stream);
-// its K split (and tile height, when bm is given)
-int gemm_blk_plan(const GemmArgs &a, int *bm);
+// its K split (and tile height and width, when bm / bn are given)
+int gemm_blk_plan(const GemmArgs &a, int *bm, int *bn = nullptr);
 size_t gemm_scratch_bytes(const GemmArgs &a);
 // staged activation (gemm_prep_kernel): P = 1 (bf16 x) or 2 (f32 x, hi + lo planes)
 struct GemmScratch {
