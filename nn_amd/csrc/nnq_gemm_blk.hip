@@ -16,7 +16,7 @@
 //         (|sc * (q' & ~1)| = 2 |sc| |q' >> 1| needs at most 11 bits), two MFMAs per 32 k;
 //         a super-block's MFMAs accumulate from zero and d_n * partial is added at its end.
 //
-// Tiling: a workgroup computes BM x BN outputs (BN 64, or 128 for Q6_K from 256 rows)
+// Tiling: a workgroup computes BM x BN outputs (BN 64, or 128 for large bf16 batches)
 // with 4 waves (2 x 2), wave tile BM/2 x BN/2 (MT x NT MFMA tiles).  K advances 256 per
 // stage: the stage's activation rows, the raw weight bytes of its BN / 16 column tiles
 // and their headers go to LDS; the next stage is prefetched into registers during the
@@ -332,14 +332,14 @@ static int launch_blk_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t 
     return (int)hipGetLastError();
 }
 
-// Tile shape and K split.  Q8_0: 64 x 64 tiles, 128 x 64 from 1024 rows on.  Q6_K with
-// bf16 input: 128 x 128 tiles from 256 rows on (its operand conversion per MFMA halves;
-// measured 7% faster at 512 rows, where Q8_0 measured slower), else as Q8_0.  The K split
-// doubles (up to 16, at least one stage each) while the tiles alone fill fewer than 512
-// workgroups (two per CU).
+// Tile shape and K split: 64 x 64 tiles, 128 x 64 from 1024 rows on; with bf16 input
+// 128 x 128 tiles from 256 rows on for Q6_K and from 1024 for Q8_0 (the operand work per
+// MFMA halves: Q6_K measured 7% faster at 512 rows, Q8_0 11% at 2048 and slower at 512).
+// The K split doubles (up to 16, at least one stage each) while the tiles alone fill
+// fewer than 512 workgroups (two per CU).
 int gemm_blk_plan(const GemmArgs &a, int *bm, int *bn) {
     const int64_t nstage = a.blk == NNQ_FMT_Q8_0 ? a.nblk / 8 : a.nblk;
-    const bool wide = a.blk == NNQ_FMT_Q6_K && a.x_bf16 && a.m >= 256;
+    const bool wide = a.x_bf16 && a.m >= (a.blk == NNQ_FMT_Q6_K ? 256 : 1024);
     const int b = (wide || a.m >= 1024) ? 128 : 64, c = wide ? 128 : 64;
     const int64_t tiles = ((a.ntile * 16 + c - 1) / c) * ((a.m + b - 1) / b);
     int ks = 1;
@@ -354,7 +354,7 @@ static int launch_blk_p(const GemmArgs &a, const GemmScratch &sc, hipStream_t st
     int bm = 64, bn = 64;
     const int ks = gemm_blk_plan(a, &bm, &bn);
     if (ks != sc.ksplit || (ks > 1 && !sc.ysplit)) return (int)hipErrorInvalidValue;
-    if constexpr (FMT == NNQ_FMT_Q6_K && P == 1)
+    if constexpr (P == 1)
         if (bn == 128) return launch_blk_cfg<FMT, 128, P, 128>(a, sc, st);
     if (bm == 128) return launch_blk_cfg<FMT, 128, P, 64>(a, sc, st);
     return launch_blk_cfg<FMT, 64, P, 64>(a, sc, st);

@@ -11,9 +11,9 @@ error <= 1e-3, per-row cosine >= 0.99999):
   * quantized N(0, 0.02) weights at the Qwen3-8B / GPT-OSS shapes;
   * Q8_0 rows whose block count is padded to groups of 8 (K = 2880, 4128);
   * f32 (hi + lo staging) and bf16 activations, f32 and bf16 outputs, bias, row counts
-    that leave partial tiles (m = 9, 33, 130, 320 and 1100: the 128-row and, for Q6_K
-    with bf16 input from 256 rows, 128-column tiles; n = 520 leaves a partial column
-    tile), and m = 8 / m = 9 consistency (GEMV vs GEMM).
+    that leave partial tiles (m = 9, 33, 130, 320 and 1100: the 128-row and, with bf16
+    input, 128-column tiles; n = 96 and 520 leave a partial column tile), and m = 8 /
+    m = 9 consistency (GEMV vs GEMM).
 """
 import numpy as np
 import pytest
