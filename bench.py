@@ -217,8 +217,10 @@ def achievable_f16_gemm(m, n, k):
 # workloads
 # ---------------------------------------------------------------------------------
 
-def bench_gemv(fmt, n, k, steps, warmup, seed, min_bytes=512 << 20, single=False):
-    """Decode GEMV y[1, n] = x[1, k] W^T, x f32 ~ N(0,1), W ~ N(0,0.02) quantized."""
+def bench_gemv(fmt, n, k, steps, warmup, seed, min_bytes=512 << 20, single=False, long_steps=0):
+    """Decode GEMV y[1, n] = x[1, k] W^T, x f32 ~ N(0,1), W ~ N(0,0.02) quantized.
+    long_steps > steps: also the same launches timed in graphs of long_steps launches (a
+    graph replay's fixed start-up cost, ~8-9 us, spread over more launches)."""
     import torch
 
     import nn_amd
@@ -244,6 +246,9 @@ def bench_gemv(fmt, n, k, steps, warmup, seed, min_bytes=512 << 20, single=False
     if single:  # cache-resident figure (one copy replayed), labelled as such
         st1 = time_windows(fns[:1], steps, warmup, windows_for(steps, 6e-6))
         out["gbs_single"] = algo / st1["median"] / 1e9
+    if long_steps > steps:
+        out["st_long"] = time_windows(fns, long_steps, 0, 5)
+        out["long_steps"] = long_steps
     return out
 
 
@@ -547,9 +552,12 @@ def main():
     r = None
     if want("headline"):
         log(f"bench: Q4_K GEMV 4096x12288 (rotating copies), {K} steps per window")
-        r = bench_gemv("q4_k", 4096, 12288, K, W, seed=2, single=not args.no_single)
+        r = bench_gemv("q4_k", 4096, 12288, K, W, seed=2, single=not args.no_single,
+                       long_steps=0 if args.no_single else 2000)
         log(f"  {r['st']['median'] * 1e6:.3f} us/step (p10 {r['st']['p10'] * 1e6:.3f}, p90 {r['st']['p90'] * 1e6:.3f})"
             f"  {r['gbs']:.1f} GB/s")
+        if "st_long" in r:
+            log(f"  {r['st_long']['median'] * 1e6:.3f} us/step in graphs of {r['long_steps']} launches")
     floor = None
     if want("floor") or (full and r is not None):
         log("bench: floors (28 MB streaming read, empty launch)")
@@ -666,7 +674,13 @@ def main():
                              f"stream; median of {r['st']['windows']} windows",
                    "us_per_step_p10": round(r["st"]["p10"] * 1e6, 3),
                    "us_per_step_p90": round(r["st"]["p90"] * 1e6, 3),
-                   **({"cache_resident_single_copy_GBps": round(r["gbs_single"], 1)} if "gbs_single" in r else {})},
+                   **({"cache_resident_single_copy_GBps": round(r["gbs_single"], 1)} if "gbs_single" in r else {}),
+                   **({"long_graph": {"steps_per_window": r["long_steps"], **ms3(r["st_long"]),
+                                      "GBps": round(r["algo_bytes"] / r["st_long"]["median"] / 1e9, 1),
+                                      "frac_hbm": round(r["algo_bytes"] / r["st_long"]["median"] / 1e9 / HBM_PEAK_GBS, 4),
+                                      "note": "the same launches in graphs of this many launches: the fixed start-up "
+                                              "cost of each graph replay spread over more launches"}}
+                      if "st_long" in r else {})},
         "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": tr["traffic_bytes_per_launch"] if tr else None},
