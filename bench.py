@@ -6,12 +6,14 @@ x f32 [1x12288]) in GB/s of algorithmic bytes (quantized weight + x + y).  A "st
 one GEMV launch over one weight copy; the weight rotates over enough distinct copies
 (>= 512 MB, twice the Infinity Cache) that every launch streams it from HBM.
 
-Timing: the steps are captured into one HIP graph of exactly `--steps` launches.  One
-timed window is one replay of that graph on torch's current stream, bracketed by HIP
-events recorded on the same stream, with a device-side sleep queued ahead of it so the
-replay's launch has been submitted before the start event fires; windows are repeated
-and the JSON carries the median window (p10 / p90 beside it).  Inputs are resident in
-HBM before timing starts.
+Timing: one timed window is exactly `--steps` launches on torch's current stream,
+bracketed by HIP events recorded on the same stream, with a device-side sleep queued
+ahead of it.  Up to 256 steps the launches are eager, and the sleep is long enough that
+all of them are queued before the start event fires (checked per window); beyond that
+the steps are one HIP graph of exactly `--steps` launches, replayed once per window (a
+graph replay carries a fixed start-up cost of several microseconds, which a short
+window would spread over few launches).  Windows are repeated and the JSON carries the
+median window (p10 / p90 beside it).  Inputs are resident in HBM before timing starts.
 
 The same JSON line carries the roofline of the headline kernel (achieved, peak, its
 measured traffic, and `floor_frac`: a pure 16-byte streaming read of the same bytes at
@@ -85,15 +87,73 @@ def stats(per_step):
             "mean": float(a.mean()), "windows": int(a.size)}
 
 
+EAGER_MAX_STEPS = 256  # windows of up to this many calls are timed as eager launches
+
+
+def _sleep_rate():
+    """Device seconds per cycle of torch.cuda._sleep, measured once."""
+    import torch
+    global _SLEEP_S_PER_CYCLE
+    if _SLEEP_S_PER_CYCLE is None:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(100_000)
+        a.record()
+        torch.cuda._sleep(2_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        _SLEEP_S_PER_CYCLE = a.elapsed_time(b) / 1e3 / 2_000_000
+    return _SLEEP_S_PER_CYCLE
+
+
+_SLEEP_S_PER_CYCLE = None
+
+
 def time_windows(fn_list, steps, warmup, windows):
-    """Capture exactly `steps` calls (cycling through fn_list) into one HIP graph and
-    time `windows` replays of it, each bracketed by HIP events on the replay stream
-    after a device-side sleep (so the replay is already queued when its start event
-    fires).  Returns the per-call time statistics over the windows, in seconds."""
+    """Time `windows` windows of exactly `steps` calls (cycling through fn_list), each
+    bracketed by HIP events on the current stream; returns the per-call time statistics
+    over the windows, in seconds.
+
+    Up to EAGER_MAX_STEPS calls per window: eager launches, enqueued behind a device-side
+    sleep long enough that every launch of the window is queued before the start event
+    fires (checked on the host for each window: a window whose enqueue outlasted its
+    sleep is timed again with a longer one), so the window times the device's back-to-back
+    execution, not the host's launch rate.  More calls: one HIP graph of exactly `steps`
+    calls, replayed once per window after a device-side sleep.  (A graph replay carries a
+    fixed start-up cost of several microseconds, which short windows would spread over
+    few calls.)"""
+    import time
+
     import torch
     for i in range(warmup):
         fn_list[i % len(fn_list)]()
     torch.cuda.synchronize()
+    if steps <= EAGER_MAX_STEPS:
+        spc = _sleep_rate()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            fn_list[i % len(fn_list)]()
+        enq = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        per = []
+        for w in range(windows):
+            sleep_s = max(1e-4, 4 * enq)
+            for _attempt in range(4):
+                st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda._sleep(int(sleep_s / spc))
+                t0 = time.perf_counter()
+                st.record()
+                for i in range(steps):
+                    fn_list[i % len(fn_list)]()
+                en.record()
+                enq_w = time.perf_counter() - t0
+                torch.cuda.synchronize()
+                if enq_w < 0.8 * sleep_s:
+                    per.append(st.elapsed_time(en) / 1e3 / steps)
+                    break
+                sleep_s *= 4
+            else:
+                raise RuntimeError("could not enqueue a window ahead of the device")
+        return stats(per)
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -670,8 +730,10 @@ def main():
         "config": {"workload": "Q4_K decode GEMV 4096x12288 (Qwen3-8B down_proj), x f32 [1x12288], y f32",
                    "n": r["n"], "k": r["k"], "weight_copies": r["copies"],
                    "algorithmic_bytes_per_step": r["algo_bytes"],
-                   "timing": f"HIP graph of exactly {K} launches, one replay per window, HIP events on the replay "
-                             f"stream; median of {r['st']['windows']} windows",
+                   "timing": (f"exactly {K} launches per window, " +
+                              ("eager, all queued behind a device-side sleep before the start event"
+                               if K <= EAGER_MAX_STEPS else "one HIP graph replay") +
+                              f"; HIP events on the launch stream; median of {r['st']['windows']} windows"),
                    "us_per_step_p10": round(r["st"]["p10"] * 1e6, 3),
                    "us_per_step_p90": round(r["st"]["p90"] * 1e6, 3),
                    **({"cache_resident_single_copy_GBps": round(r["gbs_single"], 1)} if "gbs_single" in r else {}),
@@ -693,7 +755,7 @@ def main():
             "floor_us": round(fr * 1e6, 3), "floor_GBps": round(r["algo_bytes"] / fr / 1e9, 1),
             "floor_frac": round(fr / r["st"]["median"], 4),
             "floor": f"pure 16-byte streaming read of {floor['bytes']} B per launch ({floor['workgroups']} workgroups, "
-                     f"rotating buffers), same graph cadence; empty-kernel launch "
+                     f"rotating buffers), timed as the headline; empty-kernel launch "
                      f"{floor['empty']['median'] * 1e6:.3f} us"})
     if achievable:
         line["achievable"] = achievable
