@@ -827,7 +827,7 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
 // y[t] = ((0 + w_a * y_a) + w_b * y_b) + ... over the token's experts a < b < ...
 // A NaN or infinite output sets *status (when given) to NNQ_ERR_NON_FINITE, the
 // check_output_finite of moe_forward (crates/nn-core/src/layers/nan_check.rs:113-140).
-template <int k>
+template <int k, bool V4>
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeScratch sc, int64_t H, float *y, int32_t *status) {
     const int64_t t = blockIdx.x;
     uint32_t ex[k];
@@ -855,12 +855,31 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeScratch sc, int64_t
             ws[q + 1] = sw ? w0 : w1;
         }
     bool bad = false;
-    for (int64_t c = threadIdx.x; c < H; c += 256) {
-        float acc = 0.0f;
+    if (V4) {
+        // four consecutive columns per thread (H % 4 == 0, y 16-byte aligned): the same
+        // per-element arithmetic on 16-byte loads and stores
+        const int64_t H4 = H / 4;
+#pragma unroll 3
+        for (int64_t c = threadIdx.x; c < H4; c += 256) {
+            floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < k; s++) acc = acc + sc.yb[(int64_t)ps[s] * H + c] * ws[s];
-        y[t * H + c] = acc;
-        bad |= !(fabsf(acc) <= 3.402823466e38f);
+            for (int s = 0; s < k; s++) {
+                const floatx4 v = *reinterpret_cast<const floatx4 *>(sc.yb + (int64_t)ps[s] * H + 4 * c);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = acc[i] + v[i] * ws[s];
+            }
+            *reinterpret_cast<floatx4 *>(y + t * H + 4 * c) = acc;
+#pragma unroll
+            for (int i = 0; i < 4; i++) bad |= !(fabsf(acc[i]) <= 3.402823466e38f);
+        }
+    } else {
+        for (int64_t c = threadIdx.x; c < H; c += 256) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int s = 0; s < k; s++) acc = acc + sc.yb[(int64_t)ps[s] * H + c] * ws[s];
+            y[t * H + c] = acc;
+            bad |= !(fabsf(acc) <= 3.402823466e38f);
+        }
     }
     if (status && __any(bad) && (threadIdx.x & 63) == 0) *status = NNQ_ERR_NON_FINITE;
 }
@@ -1002,10 +1021,14 @@ int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const floa
     if (e) return e;
     e = launch_stream<2, false>(d, sc, run, st);
     if (e) return e;
+    const bool v4 = d.H % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
     switch (k) {
-#define NNQ_COMB(K)                                                                                  \
-    case K:                                                                                          \
-        hipLaunchKernelGGL(moe_combine_kernel<K>, dim3((unsigned)T), dim3(256), 0, st, sc, d.H, y, status); \
+#define NNQ_COMB(K)                                                                                         \
+    case K:                                                                                                 \
+        if (v4)                                                                                             \
+            hipLaunchKernelGGL((moe_combine_kernel<K, true>), dim3((unsigned)T), dim3(256), 0, st, sc, d.H, y, status); \
+        else                                                                                                \
+            hipLaunchKernelGGL((moe_combine_kernel<K, false>), dim3((unsigned)T), dim3(256), 0, st, sc, d.H, y, status); \
         break;
         NNQ_COMB(1) NNQ_COMB(2) NNQ_COMB(3) NNQ_COMB(4) NNQ_COMB(5) NNQ_COMB(6) NNQ_COMB(7) NNQ_COMB(8)
 #undef NNQ_COMB

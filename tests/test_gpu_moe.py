@@ -403,7 +403,8 @@ def test_moe_long_batch_chunks(O, dev, xdt):
 
 def test_moe_misaligned_x(O, dev):
     """A token batch at an address that is not 16-byte aligned (a narrowed view) gives the
-    same routing and outputs as the aligned batch, through the router and the experts."""
+    same routing and outputs as the aligned batch, through the router and the experts; so
+    does an output at such an address."""
     import nn_amd
     E, H, I, T, k = 8, 96, 64, 20, 2
     L = make_layer(E, H, I, seed=51)
@@ -420,3 +421,16 @@ def test_moe_misaligned_x(O, dev):
         assert torch.equal(moe.forward(xv, logits, top_k=k), moe.forward(x, logits, top_k=k))
         assert torch.equal(moe.block_forward(xv, top_k=k), moe.block_forward(x, top_k=k))
         assert torch.equal(moe.router_logits(xv), moe.router_logits(x))
+    # an output at a 4-byte (not 16-byte) aligned address takes the combine's per-element
+    # form: bit-identical to the 16-byte form the aligned output takes
+    from nn_amd import _lib
+    from nn_amd.quantized import _DTYPE, _ptr, _stream
+    x = torch.from_numpy(nn_amd.synth_normal(54, 5, (T, H), 1.0)).to(dev)
+    logits = torch.from_numpy(nn_amd.synth_normal(54, 6, (T, E), 1.0)).to(dev)
+    ybig = torch.full((T * H + 4,), float("nan"), dtype=torch.float32, device=dev)
+    yv = ybig[1:1 + T * H].view(T, H)
+    assert yv.data_ptr() % 16 != 0
+    rc = _lib.load().nnq_moe_forward(moe._h, _ptr(x), _DTYPE[x.dtype], T, _ptr(logits), k, 7.0, _ptr(yv), None, None, _stream(x))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(yv, moe.forward(x, logits, top_k=k))
