@@ -6,13 +6,14 @@ x f32 [1x12288]) in GB/s of algorithmic bytes (quantized weight + x + y).  A "st
 one GEMV launch over one weight copy; the weight rotates over enough distinct copies
 (>= 512 MB, twice the Infinity Cache) that every launch streams it from HBM.
 
-Timing: one timed window is exactly `--steps` launches on torch's current stream,
+Timing: one timed window is exactly `--steps` calls on torch's current stream,
 bracketed by HIP events recorded on the same stream, with a device-side sleep queued
-ahead of it.  Up to 256 steps the launches are eager, and the sleep is long enough that
-all of them are queued before the start event fires (checked per window); beyond that
-the steps are one HIP graph of exactly `--steps` launches, replayed once per window (a
-graph replay carries a fixed start-up cost of several microseconds, which a short
-window would spread over few launches).  Windows are repeated and the JSON carries the
+ahead of it.  Short windows (up to 256 calls and about 0.3 ms of device time, as the
+headline at the driver's --steps 20) are eager launches, with a sleep long enough that
+all of them are queued before the start event fires (checked per window); longer ones
+are one HIP graph of exactly `--steps` calls, replayed once per window (a graph replay
+carries a fixed start-up cost of several microseconds, which a short window would spread
+over few calls; eager launches carry dispatch gaps per kernel).  Windows are repeated and the JSON carries the
 median window (p10 / p90 beside it).  Inputs are resident in HBM before timing starts.
 
 The same JSON line carries the roofline of the headline kernel (achieved, peak, its
@@ -87,7 +88,8 @@ def stats(per_step):
             "mean": float(a.mean()), "windows": int(a.size)}
 
 
-EAGER_MAX_STEPS = 256  # windows of up to this many calls are timed as eager launches
+EAGER_MAX_STEPS = 256  # short windows (calls, estimated device time) are timed as eager launches
+EAGER_MAX_WINDOW_S = 3e-4
 
 
 def _sleep_rate():
@@ -108,26 +110,28 @@ def _sleep_rate():
 _SLEEP_S_PER_CYCLE = None
 
 
-def time_windows(fn_list, steps, warmup, windows):
+def time_windows(fn_list, steps, warmup, windows, per_call_s=None):
     """Time `windows` windows of exactly `steps` calls (cycling through fn_list), each
     bracketed by HIP events on the current stream; returns the per-call time statistics
     over the windows, in seconds.
 
-    Up to EAGER_MAX_STEPS calls per window: eager launches, enqueued behind a device-side
-    sleep long enough that every launch of the window is queued before the start event
-    fires (checked on the host for each window: a window whose enqueue outlasted its
-    sleep is timed again with a longer one), so the window times the device's back-to-back
-    execution, not the host's launch rate.  More calls: one HIP graph of exactly `steps`
-    calls, replayed once per window after a device-side sleep.  (A graph replay carries a
-    fixed start-up cost of several microseconds, which short windows would spread over
-    few calls.)"""
+    Short windows (at most EAGER_MAX_STEPS calls and EAGER_MAX_WINDOW_S of estimated
+    device time, from `per_call_s`): eager launches, enqueued behind a device-side sleep
+    long enough that every launch of the window is queued before the start event fires
+    (checked on the host for each window: a window whose enqueue outlasted its sleep is
+    timed again with a longer one), so the window times the device's back-to-back
+    execution, not the host's launch rate.  Otherwise: one HIP graph of exactly `steps`
+    calls, replayed once per window after a device-side sleep.  A graph replay carries a
+    fixed start-up cost of several microseconds, which a short window would spread over
+    few calls; eager launches carry dispatch gaps per kernel, which add up over long
+    windows of multi-kernel calls."""
     import time
 
     import torch
     for i in range(warmup):
         fn_list[i % len(fn_list)]()
     torch.cuda.synchronize()
-    if steps <= EAGER_MAX_STEPS:
+    if per_call_s is not None and steps <= EAGER_MAX_STEPS and steps * per_call_s <= EAGER_MAX_WINDOW_S:
         spc = _sleep_rate()
         t0 = time.perf_counter()
         for i in range(steps):
@@ -153,7 +157,7 @@ def time_windows(fn_list, steps, warmup, windows):
                 sleep_s *= 4
             else:
                 raise RuntimeError("could not enqueue a window ahead of the device")
-        return stats(per)
+        return {**stats(per), "method": "eager"}
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -174,7 +178,7 @@ def time_windows(fn_list, steps, warmup, windows):
     torch.cuda.synchronize()
     per = [st.elapsed_time(en) / 1e3 / steps for st, en in ev]
     del g
-    return stats(per)
+    return {**stats(per), "method": "graph"}
 
 
 WINDOWS = None  # --windows: a fixed window count (profiler runs), else sized to a time budget
@@ -224,13 +228,13 @@ def bench_floor(nbytes, steps, warmup, min_bytes=512 << 20):
             def f():
                 check(P.probe_stream_read(ctypes.c_void_p(b.data_ptr()), nb, wg, vp(sink), cur_stream()))
             return f
-        st = time_windows([rd(b) for b in bufs], steps, warmup, windows_for(steps, 7e-6))
+        st = time_windows([rd(b) for b in bufs], steps, warmup, windows_for(steps, 7e-6), per_call_s=7e-6)
         if best is None or st["median"] < best[1]["median"]:
             best = (wg, st)
 
     def emp():
         check(P.probe_empty(cur_stream()))
-    est = time_windows([emp], steps, warmup, windows_for(steps, 2e-6))
+    est = time_windows([emp], steps, warmup, windows_for(steps, 2e-6), per_call_s=2e-6)
     del bufs
     return {"bytes": nb, "workgroups": best[0], "read": best[1], "empty": est}
 
@@ -299,12 +303,12 @@ def bench_gemv(fmt, n, k, steps, warmup, seed, min_bytes=512 << 20, single=False
         return f
 
     fns = [launcher(c, y) for c, y in zip(copies, ys)]
-    st = time_windows(fns, steps, warmup, windows_for(steps, 8e-6))
+    st = time_windows(fns, steps, warmup, windows_for(steps, 8e-6), per_call_s=8e-6)
     algo = len(wb) + k * 4 + n * 4
     out = dict(st=st, steps=steps, algo_bytes=algo, copies=len(copies), gbs=algo / st["median"] / 1e9, wbytes=wb,
                x=x, n=n, k=k)
     if single:  # cache-resident figure (one copy replayed), labelled as such
-        st1 = time_windows(fns[:1], steps, warmup, windows_for(steps, 6e-6))
+        st1 = time_windows(fns[:1], steps, warmup, windows_for(steps, 6e-6), per_call_s=6e-6)
         out["gbs_single"] = algo / st1["median"] / 1e9
     if long_steps > steps:
         out["st_long"] = time_windows(fns, long_steps, 0, 5)
@@ -335,7 +339,7 @@ def bench_lm_head(steps, warmup, seed=3):
                                       ctypes.c_void_p(stv.data_ptr() + 4 * i), cur_stream()))
         return f
 
-    st = time_windows([launcher(i) for i in range(len(copies))], steps, warmup, windows_for(steps, 9e-5))
+    st = time_windows([launcher(i) for i in range(len(copies))], steps, warmup, windows_for(steps, 9e-5), per_call_s=9e-5)
     # the same LM head followed by sampling (temperature 0.7, top-k 50, top-p 0.9, the
     # SamplingConfig defaults) over the 151936 logits, on the device
     from nn_amd import _lib as NL
@@ -347,7 +351,7 @@ def bench_lm_head(steps, warmup, seed=3):
                                       ctypes.c_void_p(idx.data_ptr() + 4 * i), cur_stream()))
         return f
 
-    st_s = time_windows([sampler(i) for i in range(len(copies))], steps, warmup, windows_for(steps, 1.1e-4))
+    st_s = time_windows([sampler(i) for i in range(len(copies))], steps, warmup, windows_for(steps, 1.1e-4), per_call_s=1.1e-4)
     algo = len(wb) + k * 4 + n * 4 + 4
     return dict(st=st, steps=steps, gbs=algo / st["median"] / 1e9, algo_bytes=algo, copies=len(copies), st_sample=st_s,
                 wbytes=wb, x=x)
@@ -377,7 +381,7 @@ def bench_gemm(m, n, k, steps, warmup, min_bytes=256 << 20, fmt="q4_k"):
             check(L.nnq_linear(wi.handle, vp(x), 2, m, k, None, 0, vp(yi), 2, cur_stream()))
         return f
 
-    st = time_windows([launcher(c, y) for c, y in zip(copies, ys)], steps, warmup, windows_for(steps, 1e-4))
+    st = time_windows([launcher(c, y) for c, y in zip(copies, ys)], steps, warmup, windows_for(steps, 1e-4), per_call_s=1e-4)
     flops = 2.0 * m * n * k
     algo = len(wb) + m * k * 2 + m * n * 2
     return dict(st=st, steps=steps, tflops=flops / st["median"] / 1e12, gbs=algo / st["median"] / 1e9,
@@ -407,7 +411,7 @@ def bench_mlp(steps, warmup, m=1, seed=8, min_bytes=512 << 20):
             check(L.nnq_mlp_forward(c._h, vp(x), 2, m, H, vp(y), 0, vp(stv), cur_stream()))
         return f
 
-    st = time_windows([launcher(c, y) for c, y in zip(copies, ys)], steps, warmup, windows_for(steps, 2e-5))
+    st = time_windows([launcher(c, y) for c, y in zip(copies, ys)], steps, warmup, windows_for(steps, 2e-5), per_call_s=2e-5)
     algo = per + m * H * 2 + m * H * 4 + 2 * (m * I * 4)  # weights, x, y, h written and read
     return dict(st=st, steps=steps, gbs=algo / st["median"] / 1e9, tokens_per_s=m / st["median"], copies=len(copies))
 
@@ -444,7 +448,7 @@ def bench_moe(steps, warmup, mi):
         check(L.nnq_moe_forward(moe._h, vp(x), 2, T, vp(logits), K, ctypes.c_float(7.0), vp(y), None, None,
                                 cur_stream()))
 
-    st = time_windows([f], steps, warmup, windows_for(steps, 2e-4))
+    st = time_windows([f], steps, warmup, windows_for(steps, 2e-4), per_call_s=2e-4)
     # the whole block: router Linear on the device, then the same layer
     rmoe = nn_amd.QuantizedMoE(E, H, I, mi["gp"], mi["gs"], mi["gb"], mi["dp"], mi["ds"], mi["db"],
                                router_weight=mi["rw"], router_bias=mi["rb"])
@@ -454,7 +458,7 @@ def bench_moe(steps, warmup, mi):
         check(L.nnq_moe_block_forward(rmoe._h, rmoe._router, vp(x), 2, T, K, ctypes.c_float(7.0), vp(y), None, None,
                                       vp(stv), cur_stream()))
 
-    st_b = time_windows([fb], steps, warmup, windows_for(steps, 2e-4))
+    st_b = time_windows([fb], steps, warmup, windows_for(steps, 2e-4), per_call_s=2e-4)
     del rmoe
     _, ti, _ = moe.forward(x, logits, top_k=K, return_routing=True)
     used = len(np.unique(ti.cpu().numpy()))
@@ -732,7 +736,7 @@ def main():
                    "algorithmic_bytes_per_step": r["algo_bytes"],
                    "timing": (f"exactly {K} launches per window, " +
                               ("eager, all queued behind a device-side sleep before the start event"
-                               if K <= EAGER_MAX_STEPS else "one HIP graph replay") +
+                               if r["st"]["method"] == "eager" else "one HIP graph replay") +
                               f"; HIP events on the launch stream; median of {r['st']['windows']} windows"),
                    "us_per_step_p10": round(r["st"]["p10"] * 1e6, 3),
                    "us_per_step_p90": round(r["st"]["p90"] * 1e6, 3),
