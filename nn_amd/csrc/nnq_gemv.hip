@@ -1291,6 +1291,200 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
 }
 
 // ---------------------------------------------------------------------------------
+// Q8_0 decode kernel (m <= 2).  gemv_q4k_decode_kernel's division of work over the
+// Q8_0 tile16 image (a unit is 8 blocks = 256 k of a 16-row tile: four 1024-byte
+// block pairs, lane 16p + r holding bytes 8p .. 8p + 7 of both blocks of row r, and
+// 16 bytes of row r's eight f16 d), arranged so that a wave waits once per unit:
+//  * staging lane l holds elements 4l .. 4l + 3 of the unit (block l / 8); each
+//    block's power-of-two scale and sum of x are reduced over its 8 lanes with DPP
+//    and read out as wave-uniform scalars, so no statistics go through LDS;
+//  * the A operand of block j is one 16-byte LDS read per lane (rows 2t / 2t + 1 =
+//    hi / lo of token t; the other rows read a zero pad, without branches); the
+//    eight reads of a unit are issued together and its eight MFMAs are independent;
+//  * codes enter as f16 subnormals (q ^ 0x80) * 2^-24 = (q + 128) * 2^-24, exact,
+//    and the block's 128 * sum(x) offset is subtracted with its d in f32.
+// Lanes 0 .. 15 of a wave end with the partial of rows 0 .. 15 for each token.
+// ---------------------------------------------------------------------------------
+template <bool XB>
+__device__ __forceinline__ void stage_q80(const u32x4 &raw, bool in, uint16_t *hi_plane, uint16_t *lo_plane,
+                                          float &back, float &sum) {
+    const int lane = threadIdx.x & 63;
+    float v0, v1, v2, v3;
+    if (XB) {
+        v0 = __uint_as_float(raw[0] << 16);
+        v1 = __uint_as_float(raw[0] & 0xFFFF0000u);
+        v2 = __uint_as_float(raw[1] << 16);
+        v3 = __uint_as_float(raw[1] & 0xFFFF0000u);
+    } else {
+        v0 = __uint_as_float(raw[0]);
+        v1 = __uint_as_float(raw[1]);
+        v2 = __uint_as_float(raw[2]);
+        v3 = __uint_as_float(raw[3]);
+    }
+    if (!in) v0 = v1 = v2 = v3 = 0.0f;  // k beyond K in the last (padded) unit
+    // max |x| of the lane's 32-element block (8 lanes), compared as bit patterns;
+    // s, back and the non-finite handling as in stage_q4k
+    uint32_t m = __float_as_uint(absmax4(v0, v1, v2, v3));
+    m = umax_dpp<0xB1>(m);
+    m = umax_dpp<0x4E>(m);
+    m = umax_dpp<0x141>(m);
+    const uint32_t sb = min(0x86000000u - (m & 0x7F800000u), 0x7E800000u);
+    const float s = __uint_as_float(sb);
+    const uint32_t h01 = mix_hi2(v0, v1, s), h23 = mix_hi2(v2, v3, s);
+    const uint32_t l01 = mix_lo2(v0, v1, s, h01), l23 = mix_lo2(v2, v3, s, h23);
+    *reinterpret_cast<u32x2 *>(hi_plane + 4 * lane) = u32x2{h01, h23};
+    *reinterpret_cast<u32x2 *>(lo_plane + 4 * lane) = u32x2{l01, l23};
+    float sm = (v0 + v1) + (v2 + v3);
+    sm = add_dpp<0xB1>(sm);
+    sm = add_dpp<0x4E>(sm);
+    sm = add_dpp<0x141>(sm);
+    back = __uint_as_float(0x7F000000u - sb);
+    sum = sm;
+}
+
+__device__ __forceinline__ float lane_value(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// XM: activation kind, 0 f32, 1 bf16, 2 f32 gate | up pairs (SwiGLU prologue)
+template <int WAVES, int UPW, int XM, int MT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q80_decode_kernel(GemvArgs a) {
+    constexpr bool XB = XM == 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = (int)blockIdx.x;
+    // per wave and unit of a pass: [token, hi / lo][256] f16, then 256 zero halves
+    constexpr int kBuf = MT * 512 + 256;
+    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][UPW][kBuf];
+    __shared__ float red[WAVES][MT][16];
+#pragma unroll
+    for (int j = 0; j < UPW; j++)  // the wave's own pads, read later only by lanes of this wave
+        if (lane < 32) *reinterpret_cast<u32x4 *>(&xbuf[wv][j][MT * 512 + 8 * lane]) = u32x4{0u, 0u, 0u, 0u};
+
+    // A-operand row of this lane: lane & 15 = 2t + part (token t, hi / lo part)
+    const int r16 = lane & 15, kg = lane >> 4;
+    const int aoff = (r16 >> 1) < MT ? r16 * 256 + 8 * kg : MT * 512 + 8 * kg;
+
+    const int units = (int)(a.nblk / 8), k = (int)a.k;
+    const uint8_t *qbase = a.qs + (size_t)tile * (size_t)(a.nblk / 2) * 1024 + 16 * lane;
+    const uint8_t *hbase = a.hdr + (size_t)tile * units * 256 + 16 * r16;
+    constexpr int xe = XB ? 2 : 4;
+    const int xrow = XM == 2 ? 2 * k : k;  // elements per token row of x
+    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x);
+    float acc1[MT], acc2[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc1[t] = acc2[t] = 0.f;
+    int ub0 = 0;
+    do {  // passes over K (units >= 1)
+        // activation slices first (L2 hits), then the weights of every unit of the pass
+        u32x4 xr[UPW][MT], xu[XM == 2 ? UPW : 1][MT];
+        bool xin[UPW];
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            const int u = min(ub0 + wv + j * WAVES, units - 1);
+            const int kk = u * 256 + 4 * lane;
+            xin[j] = kk < k;
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const uint8_t *p = xb + (size_t)(xin[j] ? t * xrow + kk : 0) * xe;  // out of range: x[0]
+                if (XB) {
+                    const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+                    xr[j][t] = u32x4{w2[0], w2[1], 0u, 0u};
+                } else {
+                    xr[j][t] = *reinterpret_cast<const u32x4 *>(p);
+                }
+                if constexpr (XM == 2) xu[j][t] = *reinterpret_cast<const u32x4 *>(p + (size_t)k * 4);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep this issue order
+        UnitQ80 w[UPW];
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            const uint32_t u = (uint32_t)min(ub0 + wv + j * WAVES, units - 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[j].q[i] = ldg128(qbase + (size_t)(u * 4u + i) * 1024u);
+            w[j].h = ldg128(hbase + (size_t)u * 256u);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // staging needs only the activation loads, so it runs while the weights stream in
+        float bk[UPW][MT], xs[UPW][MT];
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
+            uint16_t *buf = xbuf[wv][j];
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                u32x4 xv = xr[j][t];
+                if constexpr (XM == 2) xv = swiglu4(xv, xu[j][t]);
+                stage_q80<XB>(xv, xin[j], buf + 512 * t, buf + 512 * t + 256, bk[j][t], xs[j][t]);
+            }
+        }
+        // the wave's own LDS writes are read back by other lanes of the same wave
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
+            const uint16_t *ap = xbuf[wv][j] + aoff;
+            u32x4 av[8];
+#pragma unroll
+            for (int b = 0; b < 8; b++) av[b] = *reinterpret_cast<const u32x4 *>(ap + 32 * b);
+            floatx4 c[8];
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const uint32_t w0 = w[j].q[b >> 1][2 * (b & 1)] ^ 0x80808080u;
+                const uint32_t w1 = w[j].q[b >> 1][2 * (b & 1) + 1] ^ 0x80808080u;
+                const u32x4 bop = {w0 & 0x00FF00FFu, (w0 >> 8) & 0x00FF00FFu, w1 & 0x00FF00FFu,
+                                   (w1 >> 8) & 0x00FF00FFu};
+                c[b] = mfma16x16x32_f16(av[b], bop, floatx4{0.f, 0.f, 0.f, 0.f});
+            }
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const float d = f16_to_f32((w[j].h[b >> 1] >> (16 * (b & 1))) & 0xFFFFu);
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const float back = lane_value(bk[j][t], 8 * b), xsum = lane_value(xs[j][t], 8 * b);
+                    acc1[t] += (d * back) * (c[b][2 * t] + c[b][2 * t + 1]);
+                    acc2[t] += d * xsum;
+                }
+            }
+        }
+        ub0 += WAVES * UPW;
+    } while (ub0 < units);
+
+    // y = 2^24 * (code sums) - 128 * (offset terms), then summed over the waves
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+        if (lane < 16) red[wv][t][lane] = acc1[t] * 16777216.0f - 128.0f * acc2[t];
+    __syncthreads();
+    if (tid < MT * 16) {
+        const int t = tid >> 4, nn = tid & 15;
+        float y = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; w2++) y += red[w2][t][nn];
+        const int64_t row = (int64_t)tile * 16 + nn;
+        if (row < a.n) {
+            if (a.bias) y += a.bias[row];
+            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
+            if (a.y_bf16)
+                reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+            else
+                reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+        }
+        if (a.argmax_partial && t == 0) {
+            // first-index argmax of this tile's 16 logits (the 16 lanes hold one tile)
+            uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
+            for (int o = 8; o > 0; o >>= 1) {
+                uint64_t other = __shfl_xor(key, o, 16);
+                key = other > key ? other : key;
+            }
+            if (nn == 0) a.argmax_partial[tile] = key;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Q4_K streaming decode GEMV (m <= 2, K <= 16 units, many tiles: the fused gate | up
 // of an MLP).  gemv_q4k_decode_kernel's unit math inside gemv_stream_kernel's tile
 // loop: wave w owns unit w of every tile, stages its activation slice once, keeps the
@@ -1734,6 +1928,31 @@ static int launch_stream_t(const GemvArgs &a, int64_t units, int cus, void *stre
     return (int)hipGetLastError();
 }
 
+template <int WAVES, int UPW, int XM>
+static int launch_q80_decode_x(const GemvArgs &a, void *stream) {
+    if (a.m == 1)
+        hipLaunchKernelGGL((gemv_q80_decode_kernel<WAVES, UPW, XM, 1>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL((gemv_q80_decode_kernel<WAVES, UPW, XM, 2>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+template <int WAVES, int UPW>
+static int launch_q80_decode_t(const GemvArgs &a, void *stream) {
+    if (a.x_swiglu) return launch_q80_decode_x<WAVES, UPW, 2>(a, stream);
+    return a.x_bf16 ? launch_q80_decode_x<WAVES, UPW, 1>(a, stream) : launch_q80_decode_x<WAVES, UPW, 0>(a, stream);
+}
+// Q8_0 decode shapes: one wave per unit up to 16 units, then 16 waves of up to
+// three units (longer K loops over passes).
+static int launch_q80_decode(const GemvArgs &a, int64_t units, void *stream) {
+    if (units <= 4) return launch_q80_decode_t<4, 1>(a, stream);
+    if (units <= 8) return launch_q80_decode_t<8, 1>(a, stream);
+    if (units <= 16) return launch_q80_decode_t<16, 1>(a, stream);
+    if (units <= 32) return launch_q80_decode_t<16, 2>(a, stream);
+    return launch_q80_decode_t<16, 3>(a, stream);
+}
+
 template <int FMT>
 static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
     // many tiles per CU (the LM head): loop over tiles with the activation staged once
@@ -1757,22 +1976,26 @@ static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
             return launch_stream_t<FMT, 16, 1>(a, units, cus, stream);
         }
     }
-    constexpr int umax = FMT == FQ4K ? 6 : 4;
-    // up to two tiles per CU and K of 9-16 units: 16 waves of one unit hide more
-    // latency (Q8_0 4096x4096: 6.2 instead of 6.9 us); with many tiles per CU (the
-    // LM head) the 8-wave workgroups stay faster, and 16 waves of 2+ units spill
-    if (a.ntile <= 512 && units > 8 && units <= 16) return launch_wave_t<FMT, 16, 1>(a, stream);
-    if (units < 8) return launch_wave_t<FMT, 4, 2>(a, stream);
-    const int64_t need = (units + 7) / 8;
-    if (need <= 1) return launch_wave_t<FMT, 8, 1>(a, stream);
-    if (need <= 2) return launch_wave_t<FMT, 8, 2>(a, stream);
-    if (need <= 3) return launch_wave_t<FMT, 8, 3>(a, stream);
-    if (need <= 4 || umax == 4) return launch_wave_t<FMT, 8, 4>(a, stream);
-    if constexpr (umax > 4) {
-        if (need <= 5) return launch_wave_t<FMT, 8, 5>(a, stream);
-        return launch_wave_t<FMT, 8, 6>(a, stream);
+    if constexpr (FMT == FQ80) {
+        return launch_q80_decode(a, units, stream);
+    } else {
+        constexpr int umax = FMT == FQ4K ? 6 : 4;
+        // up to two tiles per CU and K of 9-16 units: 16 waves of one unit hide more
+        // latency; with many tiles per CU the 8-wave workgroups stay faster, and 16
+        // waves of 2+ units spill
+        if (a.ntile <= 512 && units > 8 && units <= 16) return launch_wave_t<FMT, 16, 1>(a, stream);
+        if (units < 8) return launch_wave_t<FMT, 4, 2>(a, stream);
+        const int64_t need = (units + 7) / 8;
+        if (need <= 1) return launch_wave_t<FMT, 8, 1>(a, stream);
+        if (need <= 2) return launch_wave_t<FMT, 8, 2>(a, stream);
+        if (need <= 3) return launch_wave_t<FMT, 8, 3>(a, stream);
+        if (need <= 4 || umax == 4) return launch_wave_t<FMT, 8, 4>(a, stream);
+        if constexpr (umax > 4) {
+            if (need <= 5) return launch_wave_t<FMT, 8, 5>(a, stream);
+            return launch_wave_t<FMT, 8, 6>(a, stream);
+        }
+        return (int)hipErrorInvalidValue;
     }
-    return (int)hipErrorInvalidValue;
 }
 
 template <int WAVES, int UPW, int R, int XM>

@@ -195,6 +195,24 @@ def test_q4k_decode_launch_shapes(O, dev, k, m, xdt):
     check_close(ref, y, f"q4_k decode n={n} k={k} m={m} x={xdt}")
 
 
+@pytest.mark.parametrize("k", [1024, 2048, 2080, 4096, 6144, 8192, 12288, 16416])
+@pytest.mark.parametrize("m,xdt", [(1, "f32"), (2, "f32"), (1, "bf16"), (2, "bf16")])
+def test_q80_decode_launch_shapes(O, dev, k, m, xdt):
+    """Every Q8_0 decode launch shape: K of 4, 8, 16, 24, 32 and 48 units, 2080 (9
+    units, the last one padded: 65 blocks) and 16416 (65 units: two passes, the second
+    partial and padded), a 37-row tail tile, f32 and bf16 x."""
+    import nn_amd
+    n = 37
+    b = quantized_weight_bytes("q8_0", n, k, seed=91 + k, O=O)
+    w = make_weight("q8_0", b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(13 + m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    y = nn_amd.quantized_linear(x, w).cpu().numpy()
+    ref = oracle_linear(O, "q8_0", b, n, k, x.float().cpu().numpy())
+    check_close(ref, y, f"q8_0 decode n={n} k={k} m={m} x={xdt}")
+
+
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k"])
 def test_linear_bf16_in_out_bias(O, dev, fmt):
     import nn_amd
@@ -253,15 +271,21 @@ def test_linear_known_values_q8_0(dev):
     assert np.allclose(y.cpu().numpy(), [[42.0, 52.0]], atol=1e-4)
 
 
-def test_nan_input_propagates(O, dev):
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0", "q6_k"])
+@pytest.mark.parametrize("m", [1, 2])
+def test_nan_input_propagates(O, dev, fmt, m):
+    """A NaN in one token's x makes every output of that token NaN, the other
+    token's outputs stay finite."""
     import nn_amd
     n, k = 32, 512
-    b = quantized_weight_bytes("q4_k", n, k, seed=3, O=O)
-    w = make_weight("q4_k", b, n, k)
-    x = torch.ones((1, k), device=dev)
+    b = quantized_weight_bytes(fmt, n, k, seed=3, O=O)
+    w = make_weight(fmt, b, n, k)
+    x = torch.ones((m, k), device=dev)
     x[0, 7] = float("nan")
     y = nn_amd.quantized_linear(x, w)
-    assert torch.isnan(y).all()
+    assert torch.isnan(y[0]).all()
+    if m == 2:
+        assert torch.isfinite(y[1]).all()
 
 
 # ---------------------------------------------------------------------------------
