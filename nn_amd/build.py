@@ -25,8 +25,10 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-u
 
 HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_gemm_blk.hip", "nnq_moe.hip",
                "nnq_sample.hip"]
-# per-file device flags (none at present)
-EXTRA_FLAGS = {}
+# per-file device flags: the block-scaled GEMM's MFMAs write their partials to VGPRs (the
+# FMAs that scale them read VGPRs only; with the default accumulator registers every
+# partial costs four extra register reads)
+EXTRA_FLAGS = {"nnq_gemm_blk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 HOST_SOURCES = ["nnq_abi.cpp", "nnq_repack.cpp", "nnq_host.cpp", "nnq_gguf.cpp"]
 # measurement probes for bench.py (streaming-read floor, empty launch), a library of their own
 PROBE_SOURCES = ["nnq_probe.hip"]

@@ -17,10 +17,13 @@
 //         a super-block's MFMAs accumulate from zero and d_n * partial is added at its end.
 //
 // Tiling: a workgroup computes BM x BN outputs (BN 64, or 128 for large bf16 batches)
-// with 4 waves (2 x 2), wave tile BM/2 x BN/2 (MT x NT MFMA tiles).  K advances 256 per
+// with 2 x WGN waves (4 waves of BM/2 x 32 for 64-wide tiles, 8 waves of 64 x 32 for
+// 128 x 128 tiles: two waves per SIMD), MT x NT MFMA tiles per wave.  K advances 256 per
 // stage: the stage's activation rows, the raw weight bytes of its BN / 16 column tiles
-// and their headers go to LDS; the next stage is prefetched into registers during the
-// current one's compute.  Split-K (KS > 1, when
+// and their headers go to LDS; the next stage is prefetched into registers (buffer loads
+// at a scalar per-stage offset) during the current one's compute.  The MFMA partials are
+// written to VGPRs (a per-file compiler option), so scaling them needs no register
+// moves; Q8_0 scales each block's partials one block after their MFMAs.  Split-K (KS > 1, when
 // the output tiles alone would leave CUs idle): workgroup (tile, ks) covers stages
 // [ks * S / KS, (ks + 1) * S / KS) and stores its f32 partial in slab ks of the scratch;
 // gemm_blk_finalize_kernel sums the slabs in order (deterministic), adds the bias and
@@ -35,10 +38,12 @@ namespace {
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
-template <int FMT, int BM, int P, int BN_>
+template <int FMT, int BM, int P, int BN_, int WGN>
 struct BlkCfg {
-    static constexpr int NTH = 256, BN = BN_, NTILE = BN / 16;
-    static constexpr int WM = BM / 2, MT = WM / 16, NT = NTILE / 2;
+    // waves: 2 (rows) x WGN (columns), wave tile WM x (BN / WGN)
+    static constexpr int NW = 2 * WGN, NTH = NW * 64, BN = BN_, NTILE = BN / 16;
+    static constexpr int WM = BM / 2, MT = WM / 16, NT = NTILE / WGN;
+    static_assert(NTILE % WGN == 0, "whole column tiles per wave");
     static constexpr int AST = 264;  // LDS row stride of the staged activation (f16): 256 + 8 pad
     static constexpr int TB = FMT == NNQ_FMT_Q8_0 ? 4096 : 3072;  // raw bytes per column tile and stage
     static constexpr int HB = FMT == NNQ_FMT_Q8_0 ? 256 : 288;    // header bytes per column tile and stage
@@ -61,14 +66,19 @@ __device__ __forceinline__ uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) * __builtin_bit_cast(half2v, b));
 }
 
-// Q8_0: the 8 codes of a lane (bytes in (e0, e2, e1, e3) order per word, so w & 0x00FF00FF
-// is the pair (e0, e1)) as the f16 B operand: (q + 128) | 0x6400 is the f16 1024 + q + 128,
-// exact, and 1152 is subtracted exactly.
+// Q8_0: the 8 codes of a lane (bytes in (e0, e2, e1, e3) order per word, so bytes 0 and 2
+// are the pair (e0, e1)) as the f16 B operand: the byte q + 128 under the high byte 0x64
+// (one byte permute per pair) is the f16 1024 + q + 128, exact, and 1152 is subtracted
+// exactly.
 __device__ __forceinline__ u32x4 q8_b_operand(u32x2 raw) {
     const half2v off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t k = 0x64646464u;
     const uint32_t t0 = raw[0] ^ 0x80808080u, t1 = raw[1] ^ 0x80808080u;
-    return u32x4{pk_add_f16((t0 & 0x00FF00FFu) | 0x64006400u, off), pk_add_f16(((t0 >> 8) & 0x00FF00FFu) | 0x64006400u, off),
-                 pk_add_f16((t1 & 0x00FF00FFu) | 0x64006400u, off), pk_add_f16(((t1 >> 8) & 0x00FF00FFu) | 0x64006400u, off)};
+    // selector bytes 0-3 take bytes of the second operand (t), 4 the first byte of k
+    return u32x4{pk_add_f16(__builtin_amdgcn_perm(k, t0, 0x04020400u), off),
+                 pk_add_f16(__builtin_amdgcn_perm(k, t0, 0x04030401u), off),
+                 pk_add_f16(__builtin_amdgcn_perm(k, t1, 0x04020400u), off),
+                 pk_add_f16(__builtin_amdgcn_perm(k, t1, 0x04030401u), off)};
 }
 
 // Q6_K: the 8 values of one 32-k step of a lane (pairs j = 4h .. 4h + 3: nibbles in word
@@ -91,9 +101,9 @@ __device__ __forceinline__ void q6_b_operands(uint32_t W, uint32_t Cw, uint32_t 
 
 }  // namespace
 
-template <int FMT, int BM, int P, int BN>
-__global__ __launch_bounds__(256) void gemm_blk_kernel(GemmArgs a, GemmScratch sc) {
-    using C = BlkCfg<FMT, BM, P, BN>;
+template <int FMT, int BM, int P, int BN, int WGN>
+__global__ __launch_bounds__(2 * WGN * 64) void gemm_blk_kernel(GemmArgs a, GemmScratch sc) {
+    using C = BlkCfg<FMT, BM, P, BN, WGN>;
     constexpr int NTH = C::NTH, MT = C::MT, NT = C::NT, AST = C::AST;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     uint16_t *As = reinterpret_cast<uint16_t *>(smem);
@@ -101,7 +111,7 @@ __global__ __launch_bounds__(256) void gemm_blk_kernel(GemmArgs a, GemmScratch s
     uint8_t *Hs = Bs + C::B_BYTES;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv >> 1, wn = wv & 1;
+    const int wm = wv / WGN, wn = wv % WGN;
     const int p = lane >> 4, l16 = lane & 15;
     const int64_t n0 = (int64_t)blockIdx.x * C::BN, m0 = (int64_t)blockIdx.y * BM;
     const int64_t t0 = n0 / 16;
@@ -116,47 +126,60 @@ __global__ __launch_bounds__(256) void gemm_blk_kernel(GemmArgs a, GemmScratch s
 #pragma unroll
         for (int j = 0; j < NT; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // byte offsets of (column tile t, stage s) in the tile16 image
-    auto wt_off = [&](int64_t t, int64_t s) -> int64_t {
-        return FMT == NNQ_FMT_Q8_0 ? (t * (a.nblk / 2) + 4 * s) * 1024 : (t * a.nblk + s) * 3072;
-    };
-    auto hd_off = [&](int64_t t, int64_t s) -> int64_t {
-        return FMT == NNQ_FMT_Q8_0 ? (t * (a.nblk / 8) + s) * 256 : (t * a.nblk + s) * 288;
-    };
-
     u32x4 ra[C::APT], rb[C::BPT], rh[C::HPT];
-    // global -> registers for stage s; activation columns past K (Q8_0 pads its blocks to
-    // groups of 8) and rows past M are zeros
+    // global -> registers for stage s: buffer loads from the workgroup's bases, a 32-bit
+    // lane offset fixed for the whole loop plus a scalar per-stage offset (no per-lane
+    // address arithmetic in the loop).  Rows past M read row M - 1 and column tiles past
+    // the weight read its last tile (their outputs are never stored); activation columns
+    // past K (Q8_0 pads its blocks to groups of 8) are zeroed in the last stage.  The
+    // ranges are exact, so an access outside them would read zeros.
+    constexpr bool Q8 = FMT == NNQ_FMT_Q8_0;
+    const int64_t tile_q = Q8 ? (a.nblk / 2) * 1024 : a.nblk * 3072;  // quant bytes per column tile
+    const int64_t tile_h = Q8 ? (a.nblk / 8) * 256 : a.nblk * 288;    // header bytes per column tile
+    const int mlast = (int)min((int64_t)BM - 1, M - 1 - m0);
+    const int tlast = (int)min((int64_t)C::NTILE - 1, a.ntile - 1 - t0);
+    auto range = [](int64_t bytes) { return (int)(uint32_t)min(bytes, (int64_t)0xFFFFFFFF); };
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(sc.xh + m0 * K), 0, range(((int64_t)P * M - m0) * K * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.qs + t0 * tile_q), 0, range((a.ntile - t0) * tile_q), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rhd = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.hdr + t0 * tile_h), 0, range((a.ntile - t0) * tile_h), 0x00020000);
+    const int plane = (int)(M * K * 2);  // bytes per activation plane (the host keeps P * M * K * 2 < 2^31)
+    int aof[C::APT], bof[C::BPT], hof[C::HPT], acol[C::APT];
+#pragma unroll
+    for (int i = 0; i < C::APT; i++) {
+        const int c = min(tid + i * NTH, C::ACH - 1), rem = c % (BM * 32);
+        acol[i] = (rem % 32) * 8;
+        aof[i] = (c / (BM * 32)) * plane + (min(rem / 32, mlast) * (int)K + acol[i]) * 2;
+    }
+#pragma unroll
+    for (int i = 0; i < C::BPT; i++) {
+        const int c = min(tid + i * NTH, C::BCH - 1);
+        bof[i] = (int)(min(c / (C::TB / 16), tlast) * tile_q + (c % (C::TB / 16)) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < C::HPT; i++) {
+        const int c = min(tid + i * NTH, C::HCH - 1);
+        hof[i] = (int)(min(c / (C::HB / 16), tlast) * tile_h + (c % (C::HB / 16)) * 16);
+    }
     auto gload = [&](int64_t s) {
+        const int sx = (int)s * 512, sq = (int)s * (Q8 ? 4096 : 3072), sh = (int)s * (Q8 ? 256 : 288);
 #pragma unroll
-        for (int i = 0; i < C::APT; i++) {
-            const int c = tid + i * NTH;
-            ra[i] = u32x4{0u, 0u, 0u, 0u};
-            if (c < C::ACH) {
-                const int pl = c / (BM * 32), rem = c % (BM * 32), row = rem / 32, c16 = rem % 32;
-                const int64_t k0 = s * 256 + c16 * 8;
-                if (m0 + row < M && k0 < K)
-                    ra[i] = *reinterpret_cast<const u32x4 *>(sc.xh + (int64_t)pl * M * K + (m0 + row) * K + k0);
-            }
+        for (int i = 0; i < C::APT; i++)
+            ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, aof[i], sx, 0));
+        if (Q8 && s * 256 + 256 > K) {  // workgroup-uniform: the last, padded stage
+#pragma unroll
+            for (int i = 0; i < C::APT; i++)
+                if (s * 256 + acol[i] >= K) ra[i] = u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int i = 0; i < C::BPT; i++) {
-            const int c = tid + i * NTH;
-            rb[i] = u32x4{0u, 0u, 0u, 0u};
-            if (c < C::BCH) {
-                const int tt = c / (C::TB / 16), w = c % (C::TB / 16);
-                if (t0 + tt < a.ntile) rb[i] = ldg128(a.qs + wt_off(t0 + tt, s) + w * 16);
-            }
-        }
+        for (int i = 0; i < C::BPT; i++)
+            rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, bof[i], sq, 0));
 #pragma unroll
-        for (int i = 0; i < C::HPT; i++) {
-            const int c = tid + i * NTH;
-            rh[i] = u32x4{0u, 0u, 0u, 0u};
-            if (c < C::HCH) {
-                const int tt = c / (C::HB / 16), w = c % (C::HB / 16);
-                if (t0 + tt < a.ntile) rh[i] = ldg128(a.hdr + hd_off(t0 + tt, s) + w * 16);
-            }
-        }
+        for (int i = 0; i < C::HPT; i++)
+            if (tid + i * NTH < C::HCH)
+                rh[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rhd, hof[i], sh, 0));
     };
     auto sstore = [&]() {
 #pragma unroll
@@ -196,25 +219,41 @@ __global__ __launch_bounds__(256) void gemm_blk_kernel(GemmArgs a, GemmScratch s
         __syncthreads();
         if (st + 1 < nstage) gload(s_begin + st + 1);
         if constexpr (FMT == NNQ_FMT_Q8_0) {
+            // each block's MT x NT partials go to their own registers, and d * partial is
+            // added to the totals one block later, so no MFMA result is waited on at once
+            floatx4 part[2][MT][NT];
+            float dcol[2][NT];
 #pragma unroll
-            for (int blk = 0; blk < 8; blk++) {
-                u32x4 af[P][MT];
-                afrag(32 * blk, af);
+            for (int blk = 0; blk <= 8; blk++) {
+                if (blk < 8) {
+                    u32x4 af[P][MT];
+                    afrag(32 * blk, af);
 #pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    const int tt = wn * NT + nt;  // column tile within the workgroup
-                    const u32x2 raw = *reinterpret_cast<const u32x2 *>(Bs + tt * 4096 + (blk >> 1) * 1024 +
-                                                                       16 * (16 * p + l16) + 8 * (blk & 1));
-                    const float d = f16_to_f32(*reinterpret_cast<const uint16_t *>(Hs + tt * 256 + 16 * l16 + 2 * blk));
-                    const u32x4 b = q8_b_operand(raw);
+                    for (int nt = 0; nt < NT; nt++) {
+                        const int tt = wn * NT + nt;  // column tile within the workgroup
+                        const u32x2 raw = *reinterpret_cast<const u32x2 *>(Bs + tt * 4096 + (blk >> 1) * 1024 +
+                                                                           16 * (16 * p + l16) + 8 * (blk & 1));
+                        dcol[blk & 1][nt] =
+                            f16_to_f32(*reinterpret_cast<const uint16_t *>(Hs + tt * 256 + 16 * l16 + 2 * blk));
+                        const u32x4 b = q8_b_operand(raw);
 #pragma unroll
-                    for (int mt = 0; mt < MT; mt++) {
-                        floatx4 part = mfma16x16x32_f16(af[0][mt], b, floatx4{0.f, 0.f, 0.f, 0.f});
-                        if constexpr (P == 2) part = mfma16x16x32_f16(af[1][mt], b, part);
-                        // the d of column l16 applies to all four rows this lane holds
-#pragma unroll
-                        for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(d, part[i], acc[mt][nt][i]);
+                        for (int mt = 0; mt < MT; mt++) {
+                            floatx4 pt = mfma16x16x32_f16(af[0][mt], b, floatx4{0.f, 0.f, 0.f, 0.f});
+                            if constexpr (P == 2) pt = mfma16x16x32_f16(af[1][mt], b, pt);
+                            part[blk & 1][mt][nt] = pt;
+                        }
                     }
+                }
+                if (blk > 0) {
+                    const int q = (blk - 1) & 1;
+                    // the d of column l16 applies to all four rows this lane holds
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                acc[mt][nt][i] = __builtin_fmaf(dcol[q][nt], part[q][mt][nt][i], acc[mt][nt][i]);
                 }
             }
         } else {
@@ -310,12 +349,12 @@ __global__ __launch_bounds__(256) void gemm_blk_finalize_kernel(const float *ys,
         reinterpret_cast<float *>(y)[i] = v;
 }
 
-template <int FMT, int BM, int P, int BN>
+template <int FMT, int BM, int P, int BN, int WGN = 2>
 static int launch_blk_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
-    using C = BlkCfg<FMT, BM, P, BN>;
+    using C = BlkCfg<FMT, BM, P, BN, WGN>;
     static bool attr_set = false;  // idempotent attribute write; races only repeat it
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_blk_kernel<FMT, BM, P, BN>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_blk_kernel<FMT, BM, P, BN, WGN>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
@@ -323,7 +362,7 @@ static int launch_blk_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t 
     const dim3 grid((unsigned)((a.ntile * 16 + C::BN - 1) / C::BN), (unsigned)((a.m + BM - 1) / BM),
                     (unsigned)sc.ksplit);
     constexpr size_t lds = C::LDS;
-    hipLaunchKernelGGL((gemm_blk_kernel<FMT, BM, P, BN>), grid, dim3(C::NTH), lds, st, a, sc);
+    hipLaunchKernelGGL((gemm_blk_kernel<FMT, BM, P, BN, WGN>), grid, dim3(C::NTH), lds, st, a, sc);
     int e = (int)hipGetLastError();
     if (e || sc.ksplit == 1) return e;
     const int64_t cnt = a.m * a.n;
@@ -333,8 +372,9 @@ static int launch_blk_cfg(const GemmArgs &a, const GemmScratch &sc, hipStream_t 
 }
 
 // Tile shape and K split: 64 x 64 tiles, 128 x 64 from 1024 rows on; with bf16 input
-// 128 x 128 tiles from 256 rows on for Q6_K and from 1024 for Q8_0 (the operand work per
-// MFMA halves: Q6_K measured 7% faster at 512 rows, Q8_0 11% at 2048 and slower at 512).
+// 128 x 128 tiles on eight waves from 256 rows on for Q6_K and from 1024 for Q8_0 (the
+// operand work per MFMA halves: Q6_K 512x4096x12288 150 us against 184 with 64-wide
+// tiles, Q8_0 2048x4096x4096 133 against 165; Q8_0 at 512 rows 60 against 50).
 // The K split doubles (up to 16, at least one stage each) while the tiles alone fill
 // fewer than 512 workgroups (two per CU).
 int gemm_blk_plan(const GemmArgs &a, int *bm, int *bn) {
@@ -355,7 +395,7 @@ static int launch_blk_p(const GemmArgs &a, const GemmScratch &sc, hipStream_t st
     const int ks = gemm_blk_plan(a, &bm, &bn);
     if (ks != sc.ksplit || (ks > 1 && !sc.ysplit)) return (int)hipErrorInvalidValue;
     if constexpr (P == 1)
-        if (bn == 128) return launch_blk_cfg<FMT, 128, P, 128>(a, sc, st);
+        if (bn == 128) return launch_blk_cfg<FMT, 128, P, 128, 4>(a, sc, st);
     if (bm == 128) return launch_blk_cfg<FMT, 128, P, 64>(a, sc, st);
     return launch_blk_cfg<FMT, 64, P, 64>(a, sc, st);
 }
