@@ -967,12 +967,16 @@ static int launch_stream_t(const MoeDev &d, const MoeScratch &sc, const MoeRun &
 }
 
 // Chunks of 3 k-blocks when K / 32 allows, scales staged in LDS when they fit beside
-// the ring (hidden / intermediate up to 5120 for gate_up with bf16 input).
+// the ring (hidden / intermediate up to 5120 for gate_up with bf16 input).  gate_up over
+// f32 input (two activation planes) takes chunks of one k-block: with three its weight
+// ring and operands exceed the registers of 12 waves (117 spilled; config 5 with f32 x
+// 184 against 168 us).
 template <int P, bool GU>
 static int launch_stream(const MoeDev &d, const MoeScratch &sc, const MoeRun &run, hipStream_t st) {
     const int64_t KB = (GU ? d.H : d.I) / 32;
-    if (KB % 3 == 0 && moe_lds<P, GU, 3, true>(KB) <= kMoeLdsMax)
-        return launch_stream_t<P, GU, 3, true>(d, sc, run, st, moe_lds<P, GU, 3, true>(KB));
+    if constexpr (!(P == 2 && GU))
+        if (KB % 3 == 0 && moe_lds<P, GU, 3, true>(KB) <= kMoeLdsMax)
+            return launch_stream_t<P, GU, 3, true>(d, sc, run, st, moe_lds<P, GU, 3, true>(KB));
     if (moe_lds<P, GU, 1, true>(KB) <= kMoeLdsMax)
         return launch_stream_t<P, GU, 1, true>(d, sc, run, st, moe_lds<P, GU, 1, true>(KB));
     return launch_stream_t<P, GU, 1, false>(d, sc, run, st, moe_lds<P, GU, 1, false>(KB));
