@@ -122,13 +122,54 @@ __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f};
 // ---------------------------------------------------------------------------------
 // routing: one wave per token, lane c holds logits c, c + 64, ... (E <= 256; more: moe_route_any_kernel)
 // ---------------------------------------------------------------------------------
+// Wave-wide reductions without LDS round trips: DPP steps inside each 16-lane row
+// (quad xor 1, xor 2, half-row mirror, row mirror), then the row swaps.  Every lane
+// ends with the result.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
+}
+__device__ __forceinline__ uint64_t swap_rows_max(uint64_t v, bool pair32) {
+    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    const auto l = pair32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                          : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h = pair32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                          : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return max_u64(((uint64_t)h[0] << 32) | l[0], ((uint64_t)h[1] << 32) | l[1]);
+}
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
+    v = max_u64(v, dpp_u64<0xB1>(v));
+    v = max_u64(v, dpp_u64<0x4E>(v));
+    v = max_u64(v, dpp_u64<0x141>(v));
+    v = max_u64(v, dpp_u64<0x140>(v));
+    v = swap_rows_max(v, false);
+    return swap_rows_max(v, true);
+}
+// fmaxf over the wave (a NaN lane is ignored unless every lane is NaN, in any order)
+__device__ __forceinline__ float wave_max_f32(float x) {
+    x = fmaxf(x, __uint_as_float(dpp_u32<0xB1>(__float_as_uint(x))));
+    x = fmaxf(x, __uint_as_float(dpp_u32<0x4E>(__float_as_uint(x))));
+    x = fmaxf(x, __uint_as_float(dpp_u32<0x141>(__float_as_uint(x))));
+    x = fmaxf(x, __uint_as_float(dpp_u32<0x140>(__float_as_uint(x))));
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+    v += (int)dpp_u32<0xB1>((uint32_t)v);
+    v += (int)dpp_u32<0x4E>((uint32_t)v);
+    v += (int)dpp_u32<0x141>((uint32_t)v);
+    v += (int)dpp_u32<0x140>((uint32_t)v);
+    const auto a = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = (int)(a[0] + a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return (int)(b[0] + b[1]);
 }
 
 // `logits` holds nsplit slabs [T][E] whose sum in slab order, plus `bias` when given,
@@ -157,9 +198,8 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *logits, int
         mx = fmaxf(mx, v[j]);
         ninf += (c < E && v[j] == INFINITY);
     }
-    mx = wave_max(mx);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ninf += __shfl_xor(ninf, o, 64);
+    mx = wave_max_f32(mx);
+    ninf = wave_sum_i32(ninf);
     // probs = softmax(logits) (DynTensor::softmax, crates/nn-core/src/dyn_tensor/softmax.rs:30-60,
     // called at crates/nn-gptoss/src/quantized_model.rs:140): exp(x - max) / sum, with the sum
     // accumulated in index order
@@ -217,7 +257,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *logits, int
             }
         }
         // broadcast the chosen probability from its lane
-        pv = __shfl(pv, (int)(c & 63), 64);
+        pv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), __builtin_amdgcn_readfirstlane((int)(c & 63))));
         idx[s] = c;
         val[s] = pv;
     }
@@ -266,9 +306,8 @@ __global__ __launch_bounds__(256) void moe_route_any_kernel(const float *logits,
         mx = fmaxf(mx, lv);
         ninf += lv == INFINITY;
     }
-    mx = wave_max(mx);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ninf += __shfl_xor(ninf, o, 64);
+    mx = wave_max_f32(mx);
+    ninf = wave_sum_i32(ninf);
     // probabilities (softmax with the sum in index order, as moe_route_kernel)
     if (mx == -INFINITY || mx == INFINITY) {
         for (int c = lane; c < E; c += 64) v[c] = (mx == INFINITY && v[c] == INFINITY) ? 1.0f / (float)ninf : 0.0f;
@@ -339,9 +378,13 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, i
     const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
     for (int e = tid; e < E; e += 1024) base[e] = 0;
     __syncthreads();
+    // with one chunk (T <= 1024) each thread keeps its token's experts and ranks in
+    // registers for the final scatter; longer batches pass the ranks through pos
+    const bool one_chunk = T <= 1024;
+    uint32_t ex[k];
+    int32_t myrank[k];
     for (int64_t t0 = 0; t0 < T; t0 += 1024) {
         const int64_t t = t0 + tid;
-        uint32_t ex[k];
 #pragma unroll
         for (int s = 0; s < k; s++) ex[s] = t < T ? ti[t * k + s] : 0xFFFFFFFFu;
         for (int g0 = 0; g0 < E; g0 += 256) {
@@ -349,7 +392,14 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, i
             int32_t rk[k];
 #pragma unroll
             for (int s = 0; s < k; s++) rk[s] = 0;
+            // waves past the batch only publish zero counts (a short batch leaves most of
+            // the 16 waves idle: 256 tokens use 4)
+            const bool live = t0 + (int64_t)wv * 64 < T;  // wave-uniform
             for (int e = 0; e < ge; e++) {
+                if (!live) {
+                    if (lane == 0) wcnt[wv][e] = 0;
+                    continue;
+                }
                 const uint32_t ee = (uint32_t)(g0 + e);
                 bool hit = false;
 #pragma unroll
@@ -380,8 +430,13 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, i
             if (t < T)
 #pragma unroll
                 for (int s = 0; s < k; s++)
-                    if (ex[s] >= (uint32_t)g0 && ex[s] < (uint32_t)(g0 + ge))
-                        pos[t * k + s] = wcnt[wv][ex[s] - g0] + rk[s];  // rank within the expert; offset below
+                    if (ex[s] >= (uint32_t)g0 && ex[s] < (uint32_t)(g0 + ge)) {
+                        const int32_t r = wcnt[wv][ex[s] - g0] + rk[s];  // rank within the expert; offset below
+                        if (one_chunk)
+                            myrank[s] = r;
+                        else
+                            pos[t * k + s] = r;
+                    }
             __syncthreads();  // wcnt is rewritten by the next group / chunk
         }
     }
@@ -419,6 +474,16 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, i
         if (tid == 0) off[E] = carry;  // the total
     }
     __syncthreads();
+    if (one_chunk) {
+        if (tid < T)
+#pragma unroll
+            for (int s = 0; s < k; s++) {
+                const int32_t p = myrank[s] + base[ex[s]];
+                pos[tid * k + s] = p;
+                stok[p] = tid;
+            }
+        return;
+    }
     for (int64_t i = tid; i < T * k; i += 1024) {
         const int32_t p = pos[i] + base[ti[i]];
         pos[i] = p;
