@@ -19,7 +19,8 @@ median window (p10 / p90 beside it).  Inputs are resident in HBM before timing s
 The same JSON line carries the roofline of the headline kernel (achieved, peak, its
 measured traffic, and `floor_frac`: a pure 16-byte streaming read of the same bytes at
 the same launch cadence against the kernel), measured achievable peaks (device copy,
-torch's f16 GEMM at the prefill shapes), the other BASELINE configs (Q8_0 GEMV, Q4_K
+torch's f16 GEMM at the prefill shapes), the other BASELINE configs (Q8_0 GEMV with its
+own streaming-read floor, Q4_K
 gate+up GEMV, MLP decode, the Q6_K LM head with argmax and sampling, the Q4_K prefill
 GEMMs at M = 16, 64, 128, 512, the MXFP4 MoE), and the CPU baseline: the reference's
 flow (oracle block decoders, numpy BLAS for the f32 products) on this host, one thread
@@ -633,6 +634,10 @@ def main():
         g = bench_gemv("q8_0", 4096, 4096, few, 20, seed=1)
         configs["q8_0_gemv_4096x4096"] = {**ms3(g["st"]), "GBps": round(g["gbs"], 1),
                                           "frac_hbm": round(g["gbs"] / HBM_PEAK_GBS, 4)}
+        if full:
+            # the same streaming-read floor as the headline's, for this launch's bytes
+            fq = bench_floor(g["algo_bytes"], few, 20)["read"]["median"]
+            configs["q8_0_gemv_4096x4096"].update(floor_us=round(fq * 1e6, 3), floor_frac=round(fq / g["st"]["median"], 4))
     if want("gateup"):
         log("bench: Q4_K GEMV 24576x4096 (fused gate+up)")
         g = bench_gemv("q4_k", 24576, 4096, few, 20, seed=5)

@@ -221,8 +221,15 @@ __global__ __launch_bounds__(2 * WGN * 64) void gemm_blk_kernel(GemmArgs a, Gemm
         if constexpr (FMT == NNQ_FMT_Q8_0) {
             // each block's MT x NT partials go to their own registers, and d * partial is
             // added to the totals one block later, so no MFMA result is waited on at once
+            // per column tile: the lane's row's eight d of the stage (one 16-byte read), and
+            // per pair of blocks its 16 code bytes of both (one 16-byte read: consecutive
+            // lanes read consecutive 16 bytes, no bank conflicts)
             floatx4 part[2][MT][NT];
             float dcol[2][NT];
+            u32x4 hd[NT], raw2[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+                hd[nt] = *reinterpret_cast<const u32x4 *>(Hs + (wn * NT + nt) * 256 + 16 * l16);
 #pragma unroll
             for (int blk = 0; blk <= 8; blk++) {
                 if (blk < 8) {
@@ -231,10 +238,11 @@ __global__ __launch_bounds__(2 * WGN * 64) void gemm_blk_kernel(GemmArgs a, Gemm
 #pragma unroll
                     for (int nt = 0; nt < NT; nt++) {
                         const int tt = wn * NT + nt;  // column tile within the workgroup
-                        const u32x2 raw = *reinterpret_cast<const u32x2 *>(Bs + tt * 4096 + (blk >> 1) * 1024 +
-                                                                           16 * (16 * p + l16) + 8 * (blk & 1));
-                        dcol[blk & 1][nt] =
-                            f16_to_f32(*reinterpret_cast<const uint16_t *>(Hs + tt * 256 + 16 * l16 + 2 * blk));
+                        if ((blk & 1) == 0)
+                            raw2[nt] = *reinterpret_cast<const u32x4 *>(Bs + tt * 4096 + (blk >> 1) * 1024 +
+                                                                        16 * (16 * p + l16));
+                        const u32x2 raw = {raw2[nt][2 * (blk & 1)], raw2[nt][2 * (blk & 1) + 1]};
+                        dcol[blk & 1][nt] = f16_to_f32((hd[nt][blk >> 1] >> (16 * (blk & 1))) & 0xFFFFu);
                         const u32x4 b = q8_b_operand(raw);
 #pragma unroll
                         for (int mt = 0; mt < MT; mt++) {
