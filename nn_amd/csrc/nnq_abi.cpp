@@ -373,7 +373,7 @@ static int check_linear(const nnq_weight *w, const void *x, nnq_dtype xd, int64_
 
 }  // extern "C"
 
-// One validated linear call: the prefill GEMM (Q4_K, m > 8) or GEMV passes of up to
+// One validated linear call: the MFMA GEMM (gemm_batch) or GEMV passes of up to
 // 8 tokens.  GEMV-only options: x_swiglu (x holds gate | up rows of 2k f32, the input
 // is silu(gate) * up; m <= 2 so one pass) and a status (mode 1 clears it in the
 // first pass, mode 2 flags non-finite outputs in every pass).
@@ -399,8 +399,19 @@ static GemmArgs gemm_args(const nnq_weight *w, const void *x, nnq_dtype x_dtype,
 }
 
 // scratch a linear call of m tokens needs (the prefill GEMM's staging and split-K slabs)
+// MFMA GEMM or GEMV passes (of up to 8 tokens, Q6_K 4), by the measured crossover on
+// MI355X: Q4_K from 5 tokens with bf16 activations (8 tokens at 4096x12288: 33.8 us as
+// GEMV passes, 20.9 as GEMM) and from 7 with f32 ones (33.0 against 28 at 8), Q6_K from 7
+// (41.1 against 35.2 at 8), Q8_0 from 9 (its GEMV stays faster through 8 tokens: 12.5
+// against 16.0 us at 4096x4096)
+static bool gemm_batch(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
+    if (w->L.fmt == NNQ_FMT_Q4_K) return m > (x_dtype == NNQ_BF16 ? 4 : 6);
+    if (w->L.fmt == NNQ_FMT_Q6_K) return m > 6;
+    return m > 8;
+}
+
 static size_t linear_scratch_bytes(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
-    if (m <= 8) return 0;
+    if (!gemm_batch(w, m, x_dtype)) return 0;
     return gemm_scratch_bytes(gemm_args(w, nullptr, x_dtype, m, nullptr, nullptr, NNQ_F32));
 }
 
@@ -413,7 +424,7 @@ static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype
     const Layout &L = w->L;
     const int64_t k = L.k;
     const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, ye = y_dtype == NNQ_BF16 ? 2 : 4;
-    if (m > 8 && !x_swiglu) {
+    if (gemm_batch(w, m, x_dtype) && !x_swiglu) {
         // prefill: MFMA GEMM (Q4_K: nnq_gemm*.hip; Q8_0 / Q6_K: nnq_gemm_blk.hip)
         GemmArgs g = gemm_args(w, x, x_dtype, m, bias, y, y_dtype);
         Scratch s;

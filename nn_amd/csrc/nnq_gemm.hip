@@ -56,10 +56,12 @@ GemmScratch gemm_carve(void *base, const GemmArgs &a, size_t *bytes) {
     s.rowback = reinterpret_cast<float *>(b + off);
     off += al256((size_t)a.m * 4);
     s.ksplit = a.blk ? gemm_blk_plan(a, nullptr) : (use_ring(a) ? gemm_ring_plan(a, nullptr) : 1);
+    // slabs: one per K part; the ring kernel runs f32 activations' two planes as two sets
+    const int nslab = s.ksplit * ((!a.blk && !a.x_bf16 && use_ring(a)) ? 2 : 1);
     s.ysplit = nullptr;
-    if (s.ksplit > 1) {
+    if (nslab > 1) {
         s.ysplit = reinterpret_cast<float *>(b + off);
-        off += al256((size_t)s.ksplit * a.m * a.n * 4);
+        off += al256((size_t)nslab * a.m * a.n * 4);
     }
     if (bytes) *bytes = off;
     return s;

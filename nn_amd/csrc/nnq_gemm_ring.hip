@@ -1,4 +1,4 @@
-// Prefill GEMM for Q4_K weights on gfx950, LDS-ring kernel (bf16 activations, M > 8):
+// Prefill GEMM for Q4_K weights on gfx950, LDS-ring kernel (the MFMA batches of the linear):
 // Y[m, n] = X[m, k] . W[n, k]^T (+ bias), the arithmetic of QLinear::forward with a batch
 // of tokens (crates/nn-core/src/layers/quantized/linear.rs:366-400).
 //
@@ -111,15 +111,19 @@ __global__ __launch_bounds__(NW * 64) void gemm_q4k_rk_kernel(GemmArgs a, GemmSc
     const int G = lane >> 4, c16 = lane & 15;
     const int K = (int)a.k, M = (int)a.m, nblk_all = (int)a.nblk, ntile = (int)a.ntile;
     const int KS = sc.ksplit;
+    // f32 activations: the staged hi and lo planes are two halves of the work, like two
+    // more K parts (slabs KS .. 2 KS - 1 hold the lo plane; the min term goes with hi)
+    const int NPL = a.x_bf16 ? 1 : 2, NS = KS * NPL;
     const int nsub = K / 32;
 
     // Tile order: workgroup ids go round-robin over the 8 XCDs, so when the count
     // allows, each XCD gets a contiguous run of tiles (same activation rows and K range,
     // L2-shared); column tiles vary fastest, then row tiles, then the K split.
     const int nct = (int)((a.ntile * 16 + BN - 1) / BN), nrt = (M + BM - 1) / BM;
-    const int total = nct * nrt * KS, bid = (int)blockIdx.x;
+    const int total = nct * nrt * NS, bid = (int)blockIdx.x;
     const int T = (total % 8 == 0) ? (bid % 8) * (total / 8) + bid / 8 : bid;
-    const int ks = T / (nct * nrt), Tt = T % (nct * nrt);
+    const int ksp = T / (nct * nrt), Tt = T % (nct * nrt);  // slab: plane ksp / KS, K part ksp % KS
+    const int plane = ksp / KS, ks = ksp % KS;
     const int m0 = (Tt / nct) * BM, t0 = (Tt % nct) * (BN / 16);
     const int nblk = nblk_all / KS, sb0 = ks * nblk;  // this workgroup's super-blocks
     const int nstage = nblk * 4;
@@ -145,7 +149,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_q4k_rk_kernel(GemmArgs a, GemmSc
         if (j * NTH < C::A_CH) {
             const int r = c >> 3, kc = (c & 7) ^ ((r >> 1) & 7);
             const int row = min(m0 + r, M - 1);
-            src[j] = reinterpret_cast<const uint8_t *>(sc.xh) + ((size_t)row * K + (size_t)sb0 * 256 + 8 * kc) * 2;
+            src[j] = reinterpret_cast<const uint8_t *>(sc.xh) +
+                     ((size_t)plane * M * K + (size_t)row * K + (size_t)sb0 * 256 + 8 * kc) * 2;
         } else {
             // granules past B_CH re-copy the last one into slots nobody reads
             const int cb = min(c - C::A_CH, C::B_CH - 1);
@@ -290,7 +295,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q4k_rk_kernel(GemmArgs a, GemmSc
                                                         (p == 0 && j == 0) ? floatx4{0.f, 0.f, 0.f, 0.f} : part[mt][nt]);
                 }
             }
-            if (p == 2) {
+            if (p == 2 && plane == 0) {  // workgroup-uniform
                 // min term of the super-block: one MFMA per tile whose 32 k are the four
                 // (x hi / lo) x (w hi / lo) cross products of its 8 sub-blocks: lane group G
                 // takes x part G & 1 (staged negated: the min term is subtracted) and w part G >> 1
@@ -325,7 +330,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q4k_rk_kernel(GemmArgs a, GemmSc
     // the staged sums carry 2^-8 and the min-term operands s_n.  The tile is assembled in
     // LDS (rows padded by 16 bytes, so the four row groups of a store land in distinct
     // banks) and written out as 16-byte row chunks.
-    const bool f32out = KS > 1 || !a.y_bf16;
+    const bool f32out = NS > 1 || !a.y_bf16;
     const int es = f32out ? 4 : 2, rs = BN * es + 16;
     unsigned char *stg = smem;
     // every factor is read before the first tile write (the compiler cannot tell the
@@ -342,7 +347,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q4k_rk_kernel(GemmArgs a, GemmSc
         const uint32_t eb = __float_as_uint(epi[BM + cl]) >> 23;
         f1[nt] = __uint_as_float((eb + 16u) << 23);
         f2[nt] = __uint_as_float((262u - eb) << 23);
-        bc[nt] = (a.bias && KS == 1) ? a.bias[(int64_t)t0 * 16 + cl] : 0.0f;
+        bc[nt] = (a.bias && NS == 1) ? a.bias[(int64_t)t0 * 16 + cl] : 0.0f;
     }
     float yv[MT][NT][4];
 #pragma unroll
@@ -375,7 +380,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_q4k_rk_kernel(GemmArgs a, GemmSc
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
     const int cpr = BN * es / 16;  // 16-byte chunks per row
-    unsigned char *ybase = KS > 1 ? reinterpret_cast<unsigned char *>(sc.ysplit + (int64_t)ks * M * a.n)
+    unsigned char *ybase = NS > 1 ? reinterpret_cast<unsigned char *>(sc.ysplit + (int64_t)ksp * M * a.n)
                                   : reinterpret_cast<unsigned char *>(a.y);
     for (int c = tid; c < BM * cpr; c += NTH) {
         const int rl = c / cpr, ch = c - rl * cpr;
@@ -412,19 +417,21 @@ int launch_rk(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
         attr_set = true;
     }
     const int nct = (int)((a.ntile * 16 + BN - 1) / BN), nrt = (int)((a.m + C::BM - 1) / C::BM);
-    hipLaunchKernelGGL((gemm_q4k_rk_kernel<BN, NBUF, WGN, BM, NW>), dim3((unsigned)(nct * nrt * sc.ksplit)), dim3(C::NTH), C::LDS,
+    const int ns = sc.ksplit * (a.x_bf16 ? 1 : 2);  // f32 activations: hi and lo plane slabs
+    hipLaunchKernelGGL((gemm_q4k_rk_kernel<BN, NBUF, WGN, BM, NW>), dim3((unsigned)(nct * nrt * ns)), dim3(C::NTH), C::LDS,
                        st, a, sc);
     int e = (int)hipGetLastError();
-    if (e || sc.ksplit == 1) return e;
+    if (e || ns == 1) return e;
     const int64_t cnt = a.m * a.n / 4;
-    hipLaunchKernelGGL(gemm_finalize_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, st, sc.ysplit, sc.ksplit,
-                       a.bias, a.y, a.y_bf16, a.m, a.n);
+    hipLaunchKernelGGL(gemm_finalize_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, st, sc.ysplit, ns, a.bias,
+                       a.y, a.y_bf16, a.m, a.n);
     return (int)hipGetLastError();
 }
 
 }  // namespace
 
-// Shapes the ring kernel takes (bf16 activations, N % 128 == 0, a 16-byte aligned output):
+// Shapes the ring kernel takes (N % 128 == 0, a 16-byte aligned output; f32 activations run
+// their staged hi and lo planes as two halves of the work, summed by the finalize):
 // BM x BN tiles, BM the smallest of 32, 64, 128 holding M (128 beyond), BN 192 or 128
 // (dividing N), K split 1, 2, 4, 8 or 16 ways (a divisor of the super-block count leaving
 // at least 4 super-blocks per workgroup, 2 with BM < 128).  Of these, the plan with the
@@ -435,7 +442,8 @@ int launch_rk(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
 // Returns the K split, or 0 when the shape does not fit.
 int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm) {
     // (the output tile is written in 16-byte chunks)
-    if (!a.x_bf16 || a.m < 1 || a.nblk < 1 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
+    if (a.m < 1 || a.nblk < 1 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
+    const int npl = a.x_bf16 ? 1 : 2;  // f32 activations: hi and lo planes, each a full pass
     const int rows = a.m <= 32 ? 32 : (a.m <= 64 ? 64 : 128);
     const int64_t ncols = a.ntile * 16, nrt = (a.m + rows - 1) / rows;
     const int min_sb = rows == 128 ? 4 : 2, per_cu = 1;
@@ -445,9 +453,10 @@ int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm) {
         if (ncols % cand) continue;
         for (int ks = 1; ks <= 16; ks *= 2) {
             if (a.nblk % ks || (ks > 1 && a.nblk / ks < min_sb)) continue;
-            const int64_t wgs = nrt * (ncols / cand) * ks;
+            const int64_t wgs = nrt * (ncols / cand) * ks * npl;
             const int64_t rounds = (wgs + 256 * per_cu - 1) / (256 * per_cu);
-            const double cost = (double)rounds * (double)(a.nblk / ks) * (cand == 192 ? 1.0 : 0.8) + (ks > 1 ? 1.0 : 0.0);
+            const double cost =
+                (double)rounds * (double)(a.nblk / ks) * (cand == 192 ? 1.0 : 0.8) + (ks * npl > 1 ? 1.0 : 0.0);
             if (best_bn == 0 || cost < best_cost) {
                 best_cost = cost;
                 best_bn = cand;
@@ -464,7 +473,8 @@ int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm) {
 int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     int bn = 0, bm = 0;
     const int ksplit = gemm_ring_plan(a, &bn, &bm);
-    if (ksplit == 0 || sc.ksplit != ksplit || (ksplit > 1 && !sc.ysplit)) return (int)hipErrorInvalidValue;
+    if (ksplit == 0 || sc.ksplit != ksplit || (ksplit * (a.x_bf16 ? 1 : 2) > 1 && !sc.ysplit))
+        return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     // four waves side by side (BM rows x BN / 4 columns each): measured 4-5% faster on
     // MI355X than 2 x 2 (BM / 2 x BN / 2), which halves the A reads from LDS but doubles

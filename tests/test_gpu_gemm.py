@@ -93,18 +93,21 @@ def test_gemm_bias_bf16_out_and_nan_row(O, dev):
     assert np.isnan(yn[5]).all() and np.isfinite(np.delete(yn, 5, axis=0)).all()
 
 
-@pytest.mark.parametrize("m", [16, 64, 128, 512])
+@pytest.mark.parametrize("m,xdt", [(16, "bf16"), (64, "bf16"), (128, "bf16"), (512, "bf16"), (64, "f32"), (5, "bf16")])
 @pytest.mark.parametrize("n,k", [(12288, 4096), (4096, 12288)])
-def test_gemm_baseline_shapes(O, dev, m, n, k):
+def test_gemm_baseline_shapes(O, dev, m, n, k, xdt):
     """Config 4: both Qwen3-8B MLP matrices at M = 16, 64, 128 (the GEMV-to-GEMM
-    crossover) and 512, bf16 activations, f32 and bf16 outputs."""
+    crossover) and 512, bf16 activations, f32 and bf16 outputs; also f32 activations
+    and a 5-token batch (the smallest that runs the GEMM)."""
     import nn_amd
     wb = q4k_bytes(n, k, seed=4000 + k)
     w = make_weight("q4_k", wb, n, k)
-    x = torch.from_numpy(nn_amd.synth_normal(4000 + m, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    x = torch.from_numpy(nn_amd.synth_normal(4000 + m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
     y = nn_amd.quantized_linear(x, w).cpu().numpy()
     ref = ref_f64(O, wb, n, k, x.float().cpu().numpy())
-    check_close(ref, y, f"gemm {m}x{n}x{k}")
+    check_close(ref, y, f"gemm {m}x{n}x{k} x={xdt}")
     yb = nn_amd.quantized_linear(x, w, out_dtype=torch.bfloat16).float().cpu().numpy()
     ref_b = torch.from_numpy(y).to(torch.bfloat16).float().numpy()
     assert np.array_equal(yb, ref_b), "bf16 output must be the f32 result rounded once"
@@ -114,10 +117,11 @@ def test_gemm_baseline_shapes(O, dev, m, n, k):
                                    (384, 1024, 4096), (128, 4096, 4096), (9, 128, 256), (17, 4096, 12288),
                                    (40, 384, 4096), (64, 192, 2048), (33, 768, 8192), (100, 1152, 1024),
                                    (20, 576, 2048), (50, 576, 4096), (24, 1536, 4096)])
-def test_gemm_ring_edges(O, dev, m, n, k):
-    """The LDS-ring kernel's edges (bf16 activations): 32-, 64- and 128-row tiles with a
-    ragged last row tile, 128- and 192-wide column tiles, a single super-block, K split
-    1 to 16 ways, with
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_gemm_ring_edges(O, dev, m, n, k, xdt):
+    """The LDS-ring kernel's edges: 32-, 64- and 128-row tiles with a ragged last row
+    tile, 128- and 192-wide column tiles, a single super-block, K split 1 to 16 ways,
+    bf16 activations and f32 ones (staged hi and lo planes as two sets of slabs), with
     random block bytes (arbitrary finite d / dmin / scales), d = 0 super-blocks, bias,
     f32 and bf16 outputs; the split-K sum is deterministic (two calls agree bit for bit)."""
     import nn_amd
@@ -125,13 +129,15 @@ def test_gemm_ring_edges(O, dev, m, n, k):
     b[::5, 0:2] = 0  # d = +0.0 for every fifth super-block
     b = b.ravel()
     w = make_weight("q4_k_legacy", b, n, k)
-    x = torch.from_numpy(nn_amd.synth_normal(m, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    x = torch.from_numpy(nn_amd.synth_normal(m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
     bias = torch.from_numpy(nn_amd.synth_normal(m, 3, (n,), 0.5)).to(dev)
     y = nn_amd.quantized_linear(x, w, bias)
     y2 = nn_amd.quantized_linear(x, w, bias)
     assert torch.equal(y, y2), "repeated calls must agree bit for bit"
     ref = ref_f64(O, b, n, k, x.float().cpu().numpy(), legacy=True) + bias.cpu().numpy()
-    check_close(ref, y.cpu().numpy(), f"gemm ring {m}x{n}x{k}")
+    check_close(ref, y.cpu().numpy(), f"gemm ring {m}x{n}x{k} x={xdt}")
     yb = nn_amd.quantized_linear(x, w, bias, out_dtype=torch.bfloat16).float().cpu().numpy()
     assert np.array_equal(yb, y.to(torch.bfloat16).float().cpu().numpy()), "bf16 output: the f32 result rounded once"
 

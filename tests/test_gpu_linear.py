@@ -195,6 +195,25 @@ def test_q4k_decode_launch_shapes(O, dev, k, m, xdt):
     check_close(ref, y, f"q4_k decode n={n} k={k} m={m} x={xdt}")
 
 
+@pytest.mark.parametrize("fmt,m,xdt", [("q4_k", 5, "bf16"), ("q4_k", 6, "bf16"), ("q4_k", 8, "bf16"), ("q4_k", 6, "f32"),
+                                       ("q4_k", 7, "f32"),
+                                       ("q6_k", 6, "f32"), ("q6_k", 7, "bf16"), ("q6_k", 8, "f32"), ("q8_0", 8, "bf16")])
+def test_linear_gemm_crossover(O, dev, fmt, m, xdt):
+    """Batches on both sides of each format's GEMV-to-GEMM crossover (Q4_K from 5 tokens
+    with bf16 activations and from 7 with f32 ones, Q6_K from 7, Q8_0 from 9), with a
+    ragged tile."""
+    import nn_amd
+    n, k = 200, 1024
+    b = quantized_weight_bytes(fmt, n, k, seed=300 + m, O=O)
+    w = make_weight(fmt, b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(29 + m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    y = nn_amd.quantized_linear(x, w).cpu().numpy()
+    ref = oracle_linear(O, fmt, b, n, k, x.float().cpu().numpy())
+    check_close(ref, y, f"{fmt} crossover m={m} x={xdt}")
+
+
 @pytest.mark.parametrize("k", [1024, 2048, 2080, 4096, 6144, 8192, 12288, 16416])
 @pytest.mark.parametrize("m,xdt", [(1, "f32"), (2, "f32"), (1, "bf16"), (2, "bf16")])
 def test_q80_decode_launch_shapes(O, dev, k, m, xdt):
