@@ -438,7 +438,10 @@ static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype
         if (e) return hip_fail((hipError_t)e, "gemm launch");
         return NNQ_OK;
     }
-    const int64_t mmax = L.fmt == NNQ_FMT_Q6_K ? 4 : 8;
+    // tokens per GEMV pass: Q4_K runs passes of two through its decode kernel (4 tokens:
+    // 14.6 us at 4096x12288 against 18.5 in one pass of the block GEMV), Q6_K passes of
+    // four, Q8_0 one pass of up to 8
+    const int64_t mmax = L.fmt == NNQ_FMT_Q6_K ? 4 : (L.fmt == NNQ_FMT_Q4_K ? 2 : 8);
     const int64_t xrow = x_swiglu ? 2 * k : k;
     for (int64_t m0 = 0; m0 < m; m0 += mmax) {
         GemvArgs a{};
