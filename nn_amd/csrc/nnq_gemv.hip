@@ -509,194 +509,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// Decode kernel (m <= 2 tokens): every wave works on its own units from start to
-// end.  It issues the activation slices and the (non-temporal) weight loads of all
-// its units first, then per unit converts its activation slice into a wave-private
-// LDS buffer and runs the MFMAs on it, so units are consumed in arrival order and
-// there is no workgroup barrier before the final cross-wave reduction.
-// ---------------------------------------------------------------------------------
-constexpr int kUnitBufHalfs = 2 * 2 * 256;  // [token][hi/lo][256] f16
-struct UnitBuf {
-    uint16_t xs[kUnitBufHalfs];
-    float xsum[2 * 16];  // [token][256 / GRAN]
-    float backs[2 * 8];  // [token][8 blocks of 32]
-};
-
-// Lane l holds elements 4l .. 4l + 3 of the unit for one token.
-template <int GRAN, bool PADDED>
-__device__ __forceinline__ void stage_unit(const u32x4 &raw, bool x_bf16, bool in, int t, UnitBuf &ub) {
-    const int lane = threadIdx.x & 63;
-    float v[4];
-    if (x_bf16) {
-        v[0] = bf16_to_f32(raw[0] & 0xFFFFu);
-        v[1] = bf16_to_f32(raw[0] >> 16);
-        v[2] = bf16_to_f32(raw[1] & 0xFFFFu);
-        v[3] = bf16_to_f32(raw[1] >> 16);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = __uint_as_float(raw[i]);
-    }
-    if (PADDED) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = in ? v[i] : 0.0f;
-    }
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    const float sum = (v[0] + v[1]) + (v[2] + v[3]);
-    if (!(fabsf(sum) <= 3.0e38f)) amax = INFINITY;  // NaN / inf in this lane's values
-    // max over the 8 lanes of each 32-element block
-    amax = fmaxf(amax, dpp_xor1(amax));
-    amax = fmaxf(amax, dpp_xor2(amax));
-    amax = fmaxf(amax, dpp_half_mirror(amax));
-    float s, back;
-    f16_prescale(amax, s, back);
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) split_f16(v[i] * s, h[i], l[i]);
-    *reinterpret_cast<u32x2 *>(ub.xs + (t * 2 + 0) * 256 + 4 * lane) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-    *reinterpret_cast<u32x2 *>(ub.xs + (t * 2 + 1) * 256 + 4 * lane) = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
-    float tot = sum + dpp_xor1(sum);
-    tot += dpp_xor2(tot);
-    if (GRAN == 32) tot += dpp_half_mirror(tot);
-    if ((lane & (GRAN / 4 - 1)) == 0) ub.xsum[t * (256 / GRAN) + lane / (GRAN / 4)] = tot;
-    if ((lane & 7) == 0) ub.backs[t * 8 + lane / 8] = back;
-}
-
-// SW: x is f32 [m, 2k] gate | up pairs and the GEMV input is silu(gate) * up
-template <int FMT, int WAVES, int UPW, bool SW>
-__global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(GemvArgs a) {
-    using Unit = typename UnitOf<FMT>::T;
-    constexpr int GRAN = Fmt<FMT>::kSumGran;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int64_t tile = blockIdx.x;
-    const int mt = (int)a.m;  // 1 or 2
-    __shared__ __attribute__((aligned(16))) UnitBuf ubuf[WAVES][2];
-    __shared__ u32x4 zero_lds[8];
-    __shared__ float red[WAVES][2][2][16];  // [wave][acc1/acc2][token][row]
-    if (tid < 8) zero_lds[tid] = u32x4{0u, 0u, 0u, 0u};
-    __syncthreads();
-
-    const int64_t units = FMT == FQ80 ? a.nblk / 8 : a.nblk;
-    const size_t xe = (!SW && a.x_bf16) ? 2 : 4;
-    float acc1[4][2] = {}, acc2[4][2] = {};
-    for (int64_t ub0 = 0; ub0 < units; ub0 += WAVES * UPW) {
-        // activation slices first (their wait then does not cover the weight loads)
-        u32x4 xr[UPW][2], xu[SW ? UPW : 1][2];
-        bool xin[UPW];
-        int64_t uu[UPW];
-#pragma unroll
-        for (int i = 0; i < UPW; i++) {
-            const int64_t u = ub0 + wv + i * WAVES;
-            uu[i] = u < units ? u : units - 1;
-            const int64_t kk = uu[i] * 256 + 4 * lane;
-            xin[i] = kk < a.k;
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const int64_t off = xin[i] ? (int64_t)(t < mt ? t : 0) * (SW ? 2 * a.k : a.k) + kk : 0;
-                const uint8_t *p = reinterpret_cast<const uint8_t *>(a.x) + off * xe;
-                if (!SW && a.x_bf16) {
-                    const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
-                    xr[i][t] = u32x4{w2[0], w2[1], 0u, 0u};
-                } else {
-                    xr[i][t] = *reinterpret_cast<const u32x4 *>(p);
-                }
-                if constexpr (SW) xu[i][t] = *reinterpret_cast<const u32x4 *>(p + (size_t)a.k * 4);
-            }
-        }
-        Unit w[UPW];
-#pragma unroll
-        for (int i = 0; i < UPW; i++) load_unit(a, tile, uu[i], w[i]);
-#pragma unroll
-        for (int i = 0; i < UPW; i++) {
-            if (ub0 + wv + i * WAVES >= units) break;  // wave-uniform
-            UnitBuf &b = ubuf[wv][i & 1];
-            if constexpr (SW) {
-                stage_unit<GRAN, FMT == FQ80>(swiglu4(xr[i][0], xu[i][0]), 0, xin[i], 0, b);
-                if (mt > 1) stage_unit<GRAN, FMT == FQ80>(swiglu4(xr[i][1], xu[i][1]), 0, xin[i], 1, b);
-            } else {
-                stage_unit<GRAN, FMT == FQ80>(xr[i][0], a.x_bf16, xin[i], 0, b);
-                if (mt > 1) stage_unit<GRAN, FMT == FQ80>(xr[i][1], a.x_bf16, xin[i], 1, b);
-            }
-            // the wave's own LDS writes are read back by other lanes of the same wave
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if constexpr (FMT == FQ4K)
-                compute_q4k<1>(w[i], b.xs, b.xsum, reinterpret_cast<const uint16_t *>(zero_lds), 256, mt, 0, b.backs,
-                               acc1, acc2);
-            else
-                compute_unit(w[i], b.xs, b.xsum, 256, mt, 0, b.backs, acc1[0], acc2[0]);
-        }
-    }
-
-    // combine the waves (and, for Q4_K, the four lane groups)
-    const int g = lane >> 4, n = lane & 15;
-    float r1[2], r2[2];
-    if constexpr (FMT == FQ4K) {
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            float v1 = acc1[0][h], v2 = acc2[0][h];
-            v1 += __shfl_xor(v1, 16, 64);
-            v2 += __shfl_xor(v2, 16, 64);
-            v1 += __shfl_xor(v1, 32, 64);
-            v2 += __shfl_xor(v2, 32, 64);
-            r1[h] = v1;
-            r2[h] = v2;
-        }
-        if (g == 0) {
-            red[wv][0][0][n] = r1[0];
-            red[wv][0][1][n] = r1[1];
-            red[wv][1][0][n] = r2[0];
-            red[wv][1][1][n] = r2[1];
-        }
-    } else if constexpr (FMT == FQ6K) {
-        // lane group g holds token g
-        if (g < 2) {
-            red[wv][0][g][n] = acc1[0][0];
-            red[wv][1][g][n] = acc2[0][0];
-        }
-    } else {
-        // lane group 0 holds tokens 0 and 1
-        if (g == 0) {
-            red[wv][0][0][n] = acc1[0][0];
-            red[wv][0][1][n] = acc1[0][1];
-            red[wv][1][0][n] = acc2[0][0];
-            red[wv][1][1][n] = acc2[0][1];
-        }
-    }
-    __syncthreads();
-    if (tid < mt * 16) {
-        const int t = tid >> 4, nn = tid & 15;
-        float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-        for (int w2 = 0; w2 < WAVES; w2++) {
-            s1 += red[w2][0][t][nn];
-            s2 += red[w2][1][t][nn];
-        }
-        // s1 carries the f16-subnormal factor 2^-24 of the integer weight codes
-        const float bias_k = FMT == FQ4K ? 1.0f : (FMT == FQ80 ? 128.0f : 32.0f);
-        float y = s1 * 16777216.0f - bias_k * s2;
-        const int64_t row = tile * 16 + nn;
-        if (row < a.n) {
-            if (a.bias) y += a.bias[row];
-            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
-            if (a.y_bf16)
-                reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
-            else
-                reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
-        }
-        if (a.argmax_partial && t == 0) {
-            // first-index argmax of this tile's 16 logits (row-major order), NaN -> max key
-            uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
-            for (int o = 8; o > 0; o >>= 1) {
-                uint64_t other = __shfl_xor(key, o, 16);
-                key = other > key ? other : key;
-            }
-            if (nn == 0) a.argmax_partial[tile] = key;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------
 // Streaming decode GEMV over many tiles (m <= 2, Q8_0 / Q6_K; the LM head).  Each
 // workgroup loops over tiles blockIdx.x, + gridDim.x, ...  The activation (all of K)
 // is staged once per workgroup into LDS as in gemv_kernel, and every wave loads its
@@ -1013,10 +825,10 @@ __global__ __launch_bounds__(1024) void gemv_q6k_stream_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// Q4_K decode kernel (m <= 2).  Same division of work as gemv_wave_kernel (one
-// workgroup per 16-row tile, unit u of K to wave u % WAVES, all loads of a pass
-// issued up front), arranged so that almost nothing but the MFMA inputs goes
-// through LDS:
+// Q4_K decode kernel (m <= 2).  One workgroup per 16-row tile, unit u of K to wave
+// u % WAVES, every wave issuing the activation slices and the weight loads of all its
+// units of a pass up front and then working through its units without a workgroup
+// barrier, arranged so that almost nothing but the MFMA inputs goes through LDS:
 //  * staging lane 16G + j holds elements 64G + 4j .. 64G + 4j + 3 of the unit, so
 //    sub-blocks 2G and 2G + 1 live in the same 16-lane row that consumes them in
 //    the MFMA epilogue (compute lane 16G + n, row n of the tile).  The per
@@ -1485,6 +1297,194 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q80_decode_kernel(GemvArgs a)
 }
 
 // ---------------------------------------------------------------------------------
+// Q6_K decode kernel (m <= 2), gemv_q80_decode_kernel's organisation for the Q6_K tile16
+// image (a unit is one 256-k super-block of a 16-row tile: four 768-byte chunks of 64 k,
+// lane 16p + r holding 12 bytes of row r per chunk, then 16 int8 sub-block scales and the
+// f16 d per row):
+//  * staging lane l holds elements 4l .. 4l + 3 (32-block l / 8, 16-sub-block l / 4);
+//    the blocks' powers of two and the sub-blocks' sums of x come out of DPP steps and
+//    are read as wave-uniform scalars;
+//  * MFMA j covers k 32j .. 32j + 31 (sub-blocks 2j, 2j + 1): A rows 4t + 2h + part hold
+//    token t's hi / lo parts in the k-groups of half h only (the others read a zero pad),
+//    so lane group t ends with the two sub-blocks' partial dots of token t;
+//  * the 6-bit codes enter as f16 subnormals q * 2^-24 (exact), the -32 offset is
+//    subtracted with the sub-block sums of x, in f32.
+// ---------------------------------------------------------------------------------
+template <bool XB>
+__device__ __forceinline__ void stage_q6k(const u32x4 &raw, uint16_t *hi_plane, uint16_t *lo_plane, float &back,
+                                          float &sum16) {
+    const int lane = threadIdx.x & 63;
+    float v0, v1, v2, v3;
+    if (XB) {
+        v0 = __uint_as_float(raw[0] << 16);
+        v1 = __uint_as_float(raw[0] & 0xFFFF0000u);
+        v2 = __uint_as_float(raw[1] << 16);
+        v3 = __uint_as_float(raw[1] & 0xFFFF0000u);
+    } else {
+        v0 = __uint_as_float(raw[0]);
+        v1 = __uint_as_float(raw[1]);
+        v2 = __uint_as_float(raw[2]);
+        v3 = __uint_as_float(raw[3]);
+    }
+    // max |x| of the 32-block (8 lanes); s, back and non-finite handling as in stage_q4k
+    uint32_t m = __float_as_uint(absmax4(v0, v1, v2, v3));
+    m = umax_dpp<0xB1>(m);
+    m = umax_dpp<0x4E>(m);
+    m = umax_dpp<0x141>(m);
+    const uint32_t sb = min(0x86000000u - (m & 0x7F800000u), 0x7E800000u);
+    const float s = __uint_as_float(sb);
+    const uint32_t h01 = mix_hi2(v0, v1, s), h23 = mix_hi2(v2, v3, s);
+    const uint32_t l01 = mix_lo2(v0, v1, s, h01), l23 = mix_lo2(v2, v3, s, h23);
+    *reinterpret_cast<u32x2 *>(hi_plane + 4 * lane) = u32x2{h01, h23};
+    *reinterpret_cast<u32x2 *>(lo_plane + 4 * lane) = u32x2{l01, l23};
+    float sm = (v0 + v1) + (v2 + v3);
+    sm = add_dpp<0xB1>(sm);
+    sm = add_dpp<0x4E>(sm);  // the 16-sub-block's sum (4 lanes)
+    back = __uint_as_float(0x7F000000u - sb);
+    sum16 = sm;
+}
+
+// XM: activation kind, 0 f32, 1 bf16, 2 f32 gate | up pairs (SwiGLU prologue)
+template <int WAVES, int UPW, int XM, int MT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q6k_decode_kernel(GemvArgs a) {
+    constexpr bool XB = XM == 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = (int)blockIdx.x;
+    // per wave and unit of a pass: [token, hi / lo][256] f16, then 256 zero halves
+    constexpr int kBuf = MT * 512 + 256;
+    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][UPW][kBuf];
+    __shared__ float red[WAVES][MT][16];
+#pragma unroll
+    for (int j = 0; j < UPW; j++)  // the wave's own pads, read later only by lanes of this wave
+        if (lane < 32) *reinterpret_cast<u32x4 *>(&xbuf[wv][j][MT * 512 + 8 * lane]) = u32x4{0u, 0u, 0u, 0u};
+
+    // A-operand row of this lane: lane & 15 = 4t + 2h + part, non-zero in the k-groups of half h
+    const int r16 = lane & 15, kg = lane >> 4, g = lane >> 4;
+    const int at = r16 >> 2, ah = (r16 >> 1) & 1, apart = r16 & 1;
+    const bool own = at < MT && (kg >> 1) == ah;
+    const int aoff = own ? (at * 2 + apart) * 256 + 8 * kg : MT * 512 + 8 * kg;
+
+    const int units = (int)a.nblk, k = (int)a.k;
+    constexpr int xe = XB ? 2 : 4;
+    const int xrow = XM == 2 ? 2 * k : k;  // elements per token row of x
+    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x);
+    float acc1 = 0.f, acc2 = 0.f;  // lane group g < MT: token g
+    int ub0 = 0;
+    do {  // passes over K (units >= 1)
+        u32x4 xr[UPW][MT], xu[XM == 2 ? UPW : 1][MT];
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            const int u = min(ub0 + wv + j * WAVES, units - 1);
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const uint8_t *p = xb + (size_t)(t * xrow + u * 256 + 4 * lane) * xe;
+                if (XB) {
+                    const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+                    xr[j][t] = u32x4{w2[0], w2[1], 0u, 0u};
+                } else {
+                    xr[j][t] = *reinterpret_cast<const u32x4 *>(p);
+                }
+                if constexpr (XM == 2) xu[j][t] = *reinterpret_cast<const u32x4 *>(p + (size_t)k * 4);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep this issue order
+        UnitQ6K w[UPW];
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            load_unit(a, tile, min(ub0 + wv + j * WAVES, units - 1), w[j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float bk[UPW][MT], xs16[UPW][MT];
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
+            uint16_t *buf = xbuf[wv][j];
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                u32x4 xv = xr[j][t];
+                if constexpr (XM == 2) xv = swiglu4(xv, xu[j][t]);
+                stage_q6k<XB>(xv, buf + 512 * t, buf + 512 * t + 256, bk[j][t], xs16[j][t]);
+            }
+        }
+        // the wave's own LDS writes are read back by other lanes of the same wave
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int j = 0; j < UPW; j++) {
+            if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
+            const uint16_t *ap = xbuf[wv][j] + aoff;
+            u32x4 av[8];
+#pragma unroll
+            for (int b = 0; b < 8; b++) av[b] = *reinterpret_cast<const u32x4 *>(ap + 32 * b);
+            floatx4 c[8];
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const uint32_t A = w[j].q[cc][0], B = w[j].q[cc][1], C = w[j].q[cc][2];
+                const u32x4 ba = {(A & 0x000F000Fu) | ((C << 4) & 0x00300030u), ((A >> 4) & 0x000F000Fu) | ((C << 2) & 0x00300030u),
+                                  ((A >> 8) & 0x000F000Fu) | (C & 0x00300030u), ((A >> 12) & 0x000F000Fu) | ((C >> 2) & 0x00300030u)};
+                const u32x4 bb = {(B & 0x000F000Fu) | ((C >> 4) & 0x00300030u), ((B >> 4) & 0x000F000Fu) | ((C >> 6) & 0x00300030u),
+                                  ((B >> 8) & 0x000F000Fu) | ((C >> 8) & 0x00300030u),
+                                  ((B >> 12) & 0x000F000Fu) | ((C >> 10) & 0x00300030u)};
+                c[2 * cc] = mfma16x16x32_f16(av[2 * cc], ba, floatx4{0.f, 0.f, 0.f, 0.f});
+                c[2 * cc + 1] = mfma16x16x32_f16(av[2 * cc + 1], bb, floatx4{0.f, 0.f, 0.f, 0.f});
+            }
+            // sub-block scales of row r16 (int8), the d of the super-block
+            float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const uint32_t sw = w[j].s[b >> 1] >> (16 * (b & 1));
+                const float sa = (float)(int8_t)(sw & 0xFFu), sbv = (float)(int8_t)((sw >> 8) & 0xFFu);
+                float back = lane_value(bk[j][0], 8 * b), xa = lane_value(xs16[j][0], 8 * b),
+                      xbs = lane_value(xs16[j][0], 8 * b + 4);
+                if constexpr (MT > 1) {
+                    const float back1 = lane_value(bk[j][1], 8 * b), xa1 = lane_value(xs16[j][1], 8 * b),
+                                xb1 = lane_value(xs16[j][1], 8 * b + 4);
+                    back = g == 1 ? back1 : back;
+                    xa = g == 1 ? xa1 : xa;
+                    xbs = g == 1 ? xb1 : xbs;
+                }
+                t1 += back * (sa * (c[b][0] + c[b][1]) + sbv * (c[b][2] + c[b][3]));
+                t2 += sa * xa + sbv * xbs;
+            }
+            const float d = f16_to_f32(w[j].d & 0xFFFFu);
+            acc1 += d * t1;
+            acc2 += d * t2;
+        }
+        ub0 += WAVES * UPW;
+    } while (ub0 < units);
+
+    // y = 2^24 * (code sums) - 32 * (offset terms), then summed over the waves
+    if (g < MT) red[wv][g][r16] = acc1 * 16777216.0f - 32.0f * acc2;
+    __syncthreads();
+    if (tid < MT * 16) {
+        const int t = tid >> 4, nn = tid & 15;
+        float y = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; w2++) y += red[w2][t][nn];
+        const int64_t row = (int64_t)tile * 16 + nn;
+        if (row < a.n) {
+            if (a.bias) y += a.bias[row];
+            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
+            if (a.y_bf16)
+                reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+            else
+                reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+        }
+        if (a.argmax_partial && t == 0) {
+            // first-index argmax of this tile's 16 logits (the 16 lanes hold one tile)
+            uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
+            for (int o = 8; o > 0; o >>= 1) {
+                uint64_t other = __shfl_xor(key, o, 16);
+                key = other > key ? other : key;
+            }
+            if (nn == 0) a.argmax_partial[tile] = key;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Q4_K streaming decode GEMV (m <= 2, K <= 16 units, many tiles: the fused gate | up
 // of an MLP).  gemv_q4k_decode_kernel's unit math inside gemv_stream_kernel's tile
 // loop: wave w owns unit w of every tile, stages its activation slice once, keeps the
@@ -1889,17 +1889,6 @@ static int launch_gemv_w(const GemvArgs &a, int64_t units, void *stream) {
     return launch_gemv_u<FMT, 4, NTP>(a, units, stream);
 }
 
-template <int FMT, int WAVES, int UPW>
-static int launch_wave_t(const GemvArgs &a, void *stream) {
-    if (a.x_swiglu)
-        hipLaunchKernelGGL((gemv_wave_kernel<FMT, WAVES, UPW, true>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
-                           (hipStream_t)stream, a);
-    else
-        hipLaunchKernelGGL((gemv_wave_kernel<FMT, WAVES, UPW, false>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
-                           (hipStream_t)stream, a);
-    return (int)hipGetLastError();
-}
-
 // decode (m <= 2): 8 waves with just enough units each to cover K in one pass
 // (longer K loops over passes)
 // streaming kernel: workgroups = CUs (every one loops over tiles); dynamic LDS holds
@@ -1953,6 +1942,31 @@ static int launch_q80_decode(const GemvArgs &a, int64_t units, void *stream) {
     return launch_q80_decode_t<16, 3>(a, stream);
 }
 
+template <int WAVES, int UPW, int XM>
+static int launch_q6k_decode_x(const GemvArgs &a, void *stream) {
+    if (a.m == 1)
+        hipLaunchKernelGGL((gemv_q6k_decode_kernel<WAVES, UPW, XM, 1>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL((gemv_q6k_decode_kernel<WAVES, UPW, XM, 2>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+template <int WAVES, int UPW>
+static int launch_q6k_decode_t(const GemvArgs &a, void *stream) {
+    if (a.x_swiglu) return launch_q6k_decode_x<WAVES, UPW, 2>(a, stream);
+    return a.x_bf16 ? launch_q6k_decode_x<WAVES, UPW, 1>(a, stream) : launch_q6k_decode_x<WAVES, UPW, 0>(a, stream);
+}
+// Q6_K decode shapes: as Q8_0's, with 8 waves of two units for K of 9-16 units when the
+// grid has more than two tiles per CU
+static int launch_q6k_decode(const GemvArgs &a, int64_t units, void *stream) {
+    if (units <= 4) return launch_q6k_decode_t<4, 1>(a, stream);
+    if (units <= 8) return launch_q6k_decode_t<8, 1>(a, stream);
+    if (units <= 16) return a.ntile > 512 ? launch_q6k_decode_t<8, 2>(a, stream) : launch_q6k_decode_t<16, 1>(a, stream);
+    if (units <= 32) return launch_q6k_decode_t<16, 2>(a, stream);
+    return launch_q6k_decode_t<16, 3>(a, stream);
+}
+
 template <int FMT>
 static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
     // many tiles per CU (the LM head): loop over tiles with the activation staged once
@@ -1976,26 +1990,11 @@ static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
             return launch_stream_t<FMT, 16, 1>(a, units, cus, stream);
         }
     }
-    if constexpr (FMT == FQ80) {
+    static_assert(FMT == FQ80 || FMT == FQ6K, "Q4_K has its own decode launcher");
+    if constexpr (FMT == FQ80)
         return launch_q80_decode(a, units, stream);
-    } else {
-        constexpr int umax = FMT == FQ4K ? 6 : 4;
-        // up to two tiles per CU and K of 9-16 units: 16 waves of one unit hide more
-        // latency; with many tiles per CU the 8-wave workgroups stay faster, and 16
-        // waves of 2+ units spill
-        if (a.ntile <= 512 && units > 8 && units <= 16) return launch_wave_t<FMT, 16, 1>(a, stream);
-        if (units < 8) return launch_wave_t<FMT, 4, 2>(a, stream);
-        const int64_t need = (units + 7) / 8;
-        if (need <= 1) return launch_wave_t<FMT, 8, 1>(a, stream);
-        if (need <= 2) return launch_wave_t<FMT, 8, 2>(a, stream);
-        if (need <= 3) return launch_wave_t<FMT, 8, 3>(a, stream);
-        if (need <= 4 || umax == 4) return launch_wave_t<FMT, 8, 4>(a, stream);
-        if constexpr (umax > 4) {
-            if (need <= 5) return launch_wave_t<FMT, 8, 5>(a, stream);
-            return launch_wave_t<FMT, 8, 6>(a, stream);
-        }
-        return (int)hipErrorInvalidValue;
-    }
+    else
+        return launch_q6k_decode(a, units, stream);
 }
 
 template <int WAVES, int UPW, int R, int XM>

@@ -214,6 +214,24 @@ def test_linear_gemm_crossover(O, dev, fmt, m, xdt):
     check_close(ref, y, f"{fmt} crossover m={m} x={xdt}")
 
 
+@pytest.mark.parametrize("k", [1024, 2048, 4096, 6144, 8192, 12288, 16384])
+@pytest.mark.parametrize("m,xdt", [(1, "f32"), (2, "f32"), (1, "bf16"), (2, "bf16")])
+def test_q6k_decode_launch_shapes(O, dev, k, m, xdt):
+    """Every Q6_K decode launch shape: K of 4, 8, 16, 24, 32, 48 and 64 units (one and
+    two passes), a 37-row tail tile, f32 and bf16 x, with a bias."""
+    import nn_amd
+    n = 37
+    b = quantized_weight_bytes("q6_k", n, k, seed=57 + k, O=O)
+    w = make_weight("q6_k", b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(19 + m, 2, (m, k), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    bias = nn_amd.synth_normal(7, 3, (n,), 0.5)
+    y = nn_amd.quantized_linear(x, w, torch.from_numpy(bias).to(dev)).cpu().numpy()
+    ref = oracle_linear(O, "q6_k", b, n, k, x.float().cpu().numpy()) + bias[None, :]
+    check_close(ref, y, f"q6_k decode n={n} k={k} m={m} x={xdt}")
+
+
 @pytest.mark.parametrize("k", [1024, 2048, 2080, 4096, 6144, 8192, 12288, 16416])
 @pytest.mark.parametrize("m,xdt", [(1, "f32"), (2, "f32"), (1, "bf16"), (2, "bf16")])
 def test_q80_decode_launch_shapes(O, dev, k, m, xdt):
