@@ -68,6 +68,18 @@ __device__ __forceinline__ void wave_sync() {
 // (then t is the kth largest key).  Each wave counts into its own histogram (hist holds
 // blockDim / 64 of them), so equal digits only contend within a wave.  Every thread of
 // the workgroup calls it.
+// inclusive prefix sum over the 64 lanes by DPP: shifts within each 16-lane row, then
+// the row totals broadcast into the following rows (row_bcast:15, row_bcast:31)
+__device__ __forceinline__ int wave_scan_incl(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+    return v;
+}
+
 template <int E, int NW>
 __device__ uint64_t radix_kth(const uint64_t (&e)[E], int k, int *hist, uint64_t *bcast) {
     uint64_t prefix = 0, mask = 0;
@@ -98,13 +110,7 @@ __device__ uint64_t radix_kth(const uint64_t (&e)[E], int k, int *hist, uint64_t
                 c[j] = col[255 - (4 * lane + j)];
                 sum += c[j];
             }
-            int before = sum;  // inclusive scan over lanes, then exclusive
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int v = __shfl_up(before, o, 64);
-                if (lane >= o) before += v;
-            }
-            before -= sum;
+            int before = wave_scan_incl(sum) - sum;  // exclusive scan over the lanes
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 if (before < rem && before + c[j] >= rem)
