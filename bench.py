@@ -19,7 +19,7 @@ median window (p10 / p90 beside it).  Inputs are resident in HBM before timing s
 The same JSON line carries the roofline of the headline kernel (achieved, peak, its
 measured traffic, and `floor_frac`: a pure 16-byte streaming read of the same bytes at
 the same launch cadence against the kernel), measured achievable peaks (device copy,
-torch's f16 GEMM at the prefill shapes), the other BASELINE configs (Q8_0 GEMV with its
+torch's f16 GEMM at the prefill shapes), the other benchmark configs (Q8_0 GEMV with its
 own streaming-read floor, Q4_K
 gate+up GEMV, MLP decode, the Q6_K LM head with argmax and sampling, the Q4_K prefill
 GEMMs at M = 16, 64, 128, 512, the MXFP4 MoE), and the CPU baseline: the reference's

@@ -4,7 +4,7 @@ The HIP GEMM runs through the C ABI (nn_amd -> libnnq.so) and is compared with t
 CPU oracle on the same bytes and activations (tolerances as in test_gpu_linear):
 normwise and elementwise max relative error <= 1e-3 (near-zero skip at 1% of the
 peak), per-row cosine >= 0.99999.  Small shapes use the oracle's own f32 path
-(QLinear::forward restated: full dequant + x @ W^T); the BASELINE shapes use the
+(QLinear::forward restated: full dequant + x @ W^T); the benchmark shapes use the
 oracle's bit-exact dequant followed by an f64 matmul (numpy), which is the exact
 product the f32 reference approximates.
 """

@@ -326,7 +326,7 @@ def test_nan_input_propagates(O, dev, fmt, m):
 
 
 # ---------------------------------------------------------------------------------
-# BASELINE shapes
+# benchmark shapes
 # ---------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("fmt,n,k", [("q8_0", 4096, 4096), ("q4_k", 4096, 12288), ("q4_k", 24576, 4096)])

@@ -7,7 +7,7 @@ QuantizedDecoderLayer::moe_forward (crates/nn-gptoss/src/quantized_model.rs:99-1
   * expert decode: bit-exact with Mxfp4Tensor::dequantize;
   * outputs: normwise and elementwise max relative error <= 1e-3 (near-zero skip at
     1% of the peak) and per-row cosine >= 0.99999.
-Small layers use the oracle's own f32 forward; the BASELINE layer (config 5) uses
+Small layers use the oracle's own f32 forward; the benchmark layer (config 5) uses
 the oracle's routing and bit-exact decode with the expert math in f64.
 """
 import numpy as np
