@@ -402,12 +402,13 @@ static GemmArgs gemm_args(const nnq_weight *w, const void *x, nnq_dtype x_dtype,
 // MFMA GEMM or GEMV passes (of up to 8 tokens, Q6_K 4), by the measured crossover on
 // MI355X: Q4_K from 5 tokens with bf16 activations (8 tokens at 4096x12288: 33.8 us as
 // GEMV passes, 20.9 as GEMM) and from 7 with f32 ones (33.0 against 28 at 8), Q6_K from 7
-// (41.1 against 35.2 at 8), Q8_0 from 9 (its GEMV stays faster through 8 tokens: 12.5
-// against 16.0 us at 4096x4096)
+// (41.1 against 35.2 at 8), Q8_0 from 9 with bf16 activations and from 17 with f32 ones
+// (8 tokens in one batched GEMV pass: 7.9 us at 4096x4096, 17.9 at 4096x12288; 9 f32
+// tokens as GEMM: 20.9 and 39.2 us)
 static bool gemm_batch(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
     if (w->L.fmt == NNQ_FMT_Q4_K) return m > (x_dtype == NNQ_BF16 ? 4 : 6);
     if (w->L.fmt == NNQ_FMT_Q6_K) return m > 6;
-    return m > 8;
+    return m > (x_dtype == NNQ_BF16 ? 8 : 16);
 }
 
 static size_t linear_scratch_bytes(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {

@@ -1297,6 +1297,127 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q80_decode_kernel(GemvArgs a)
 }
 
 // ---------------------------------------------------------------------------------
+// Q8_0 batched decode (3 <= m <= 8; MT = 4 or 8 token rows, the rows past m zero):
+// gemv_q80_decode_kernel's unit math with every A row in use (rows 2t + part), so lane
+// group g holds tokens 2g and 2g + 1.  The block statistics of every token go through a
+// per-wave LDS table (8 powers of two and 8 sums per token) that each lane group reads
+// for its two tokens with broadcast 16-byte reads.  One unit per wave and pass.
+// ---------------------------------------------------------------------------------
+template <int WAVES, int XM, int MT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q80_batch_kernel(GemvArgs a) {
+    constexpr bool XB = XM == 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = (int)blockIdx.x, mt = (int)a.m;
+    constexpr int kBuf = MT * 512 + 256;
+    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][kBuf];
+    __shared__ __attribute__((aligned(16))) float stats[WAVES][MT][16];  // [token][8 x 2^-s, 8 x sum]
+    __shared__ float red[WAVES][MT][16];
+    if (lane < 32) *reinterpret_cast<u32x4 *>(&xbuf[wv][MT * 512 + 8 * lane]) = u32x4{0u, 0u, 0u, 0u};
+
+    const int r16 = lane & 15, kg = lane >> 4, g = kg;
+    const int aoff = (r16 >> 1) < MT ? r16 * 256 + 8 * kg : MT * 512 + 8 * kg;
+    const int t0 = min(2 * g, MT - 1), t1 = min(2 * g + 1, MT - 1);  // this lane group's tokens
+
+    const int units = (int)(a.nblk / 8), k = (int)a.k;
+    const uint8_t *qbase = a.qs + (size_t)tile * (size_t)(a.nblk / 2) * 1024 + 16 * lane;
+    const uint8_t *hbase = a.hdr + (size_t)tile * units * 256 + 16 * r16;
+    constexpr int xe = XB ? 2 : 4;
+    const int xrow = XM == 2 ? 2 * k : k;
+    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x);
+    float acc1[2] = {0.f, 0.f}, acc2[2] = {0.f, 0.f};
+    for (int ub0 = 0; ub0 < units; ub0 += WAVES) {
+        const int u = min(ub0 + wv, units - 1);
+        const int kk = u * 256 + 4 * lane;
+        const bool xin = kk < k;
+        u32x4 xr[MT], xu[XM == 2 ? MT : 1];
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const bool tin = xin && t < mt;
+            const uint8_t *p = xb + (size_t)(tin ? t * xrow + kk : 0) * xe;  // out of range: x[0]
+            if (XB) {
+                const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+                xr[t] = u32x4{w2[0], w2[1], 0u, 0u};
+            } else {
+                xr[t] = *reinterpret_cast<const u32x4 *>(p);
+            }
+            if constexpr (XM == 2) xu[t] = *reinterpret_cast<const u32x4 *>(p + (size_t)k * 4);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep this issue order
+        UnitQ80 w;
+#pragma unroll
+        for (int i = 0; i < 4; i++) w.q[i] = ldg128(qbase + (size_t)(u * 4 + i) * 1024u);
+        w.h = ldg128(hbase + (size_t)u * 256u);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ub0 + wv >= units) break;  // wave-uniform: no unit left for this wave
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            u32x4 xv = xr[t];
+            if constexpr (XM == 2) xv = swiglu4(xv, xu[t]);
+            float bk, xs;
+            stage_q80<XB>(xv, xin && t < mt, xbuf[wv] + 512 * t, xbuf[wv] + 512 * t + 256, bk, xs);
+            if ((lane & 7) == 0) {
+                stats[wv][t][lane >> 3] = bk;
+                stats[wv][t][8 + (lane >> 3)] = xs;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint16_t *ap = xbuf[wv] + aoff;
+        u32x4 av[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) av[b] = *reinterpret_cast<const u32x4 *>(ap + 32 * b);
+        floatx4 s0[4], s1[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s0[i] = *reinterpret_cast<const floatx4 *>(&stats[wv][t0][4 * i]);
+            s1[i] = *reinterpret_cast<const floatx4 *>(&stats[wv][t1][4 * i]);
+        }
+        floatx4 c[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const uint32_t w0 = w.q[b >> 1][2 * (b & 1)] ^ 0x80808080u;
+            const uint32_t w1 = w.q[b >> 1][2 * (b & 1) + 1] ^ 0x80808080u;
+            const u32x4 bop = {w0 & 0x00FF00FFu, (w0 >> 8) & 0x00FF00FFu, w1 & 0x00FF00FFu, (w1 >> 8) & 0x00FF00FFu};
+            c[b] = mfma16x16x32_f16(av[b], bop, floatx4{0.f, 0.f, 0.f, 0.f});
+        }
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const float d = f16_to_f32((w.h[b >> 1] >> (16 * (b & 1))) & 0xFFFFu);
+            acc1[0] += (d * s0[b >> 2][b & 3]) * (c[b][0] + c[b][1]);
+            acc1[1] += (d * s1[b >> 2][b & 3]) * (c[b][2] + c[b][3]);
+            acc2[0] += d * s0[2 + (b >> 2)][b & 3];
+            acc2[1] += d * s1[2 + (b >> 2)][b & 3];
+        }
+        // the next pass rewrites this wave's buffers only after these reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // y = 2^24 * (code sums) - 128 * (offset terms), then summed over the waves
+    if (2 * g < MT) red[wv][2 * g][r16] = acc1[0] * 16777216.0f - 128.0f * acc2[0];
+    if (2 * g + 1 < MT) red[wv][2 * g + 1][r16] = acc1[1] * 16777216.0f - 128.0f * acc2[1];
+    __syncthreads();
+    if (tid < mt * 16) {
+        const int t = tid >> 4, nn = tid & 15;
+        float y = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; w2++) y += red[w2][t][nn];
+        const int64_t row = (int64_t)tile * 16 + nn;
+        if (row < a.n) {
+            if (a.bias) y += a.bias[row];
+            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
+            if (a.y_bf16)
+                reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+            else
+                reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Q6_K decode kernel (m <= 2), gemv_q80_decode_kernel's organisation for the Q6_K tile16
 // image (a unit is one 256-k super-block of a 16-row tile: four 768-byte chunks of 64 k,
 // lane 16p + r holding 12 bytes of row r per chunk, then 16 int8 sub-block scales and the
@@ -1932,6 +2053,31 @@ static int launch_q80_decode_t(const GemvArgs &a, void *stream) {
     if (a.x_swiglu) return launch_q80_decode_x<WAVES, UPW, 2>(a, stream);
     return a.x_bf16 ? launch_q80_decode_x<WAVES, UPW, 1>(a, stream) : launch_q80_decode_x<WAVES, UPW, 0>(a, stream);
 }
+template <int WAVES, int MT>
+static int launch_q80_batch_t(const GemvArgs &a, void *stream) {
+    if (a.x_swiglu)
+        hipLaunchKernelGGL((gemv_q80_batch_kernel<WAVES, 2, MT>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    else if (a.x_bf16)
+        hipLaunchKernelGGL((gemv_q80_batch_kernel<WAVES, 1, MT>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL((gemv_q80_batch_kernel<WAVES, 0, MT>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+// Q8_0 batches of 3-8 tokens: 4 or 8 token rows, waves of one unit per pass: 16 when
+// the grid has at most two tiles per CU and K is over 8 units, else 8 (4 for K of up
+// to 4 units).  4096x4096, 8 tokens: 7.9 us (12.5 in the block GEMV form).
+static int launch_q80_batch(const GemvArgs &a, int64_t units, void *stream) {
+    const bool w16 = a.ntile <= 512 && units > 8;
+    if (a.m <= 4)
+        return units <= 4 ? launch_q80_batch_t<4, 4>(a, stream)
+                          : (w16 ? launch_q80_batch_t<16, 4>(a, stream) : launch_q80_batch_t<8, 4>(a, stream));
+    return units <= 4 ? launch_q80_batch_t<4, 8>(a, stream)
+                      : (w16 ? launch_q80_batch_t<16, 8>(a, stream) : launch_q80_batch_t<8, 8>(a, stream));
+}
+
 // Q8_0 decode shapes: one wave per unit up to 16 units, then 16 waves of up to
 // three units (longer K loops over passes).
 static int launch_q80_decode(const GemvArgs &a, int64_t units, void *stream) {
@@ -2067,7 +2213,7 @@ int launch_gemv(int fmt, const GemvArgs &a, void *stream) {
         if (a.m <= 4) return launch_gemv_w<FQ4K, 2>(a, units, stream);
         return launch_gemv_w<FQ4K, 4>(a, units, stream);
     case FQ80:
-        return launch_gemv_w<FQ80, 1>(a, units, stream);
+        return launch_q80_batch(a, units, stream);
     case FQ6K:
         return launch_gemv_w<FQ6K, 1>(a, units, stream);
     }
