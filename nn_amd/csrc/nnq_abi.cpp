@@ -401,13 +401,13 @@ static GemmArgs gemm_args(const nnq_weight *w, const void *x, nnq_dtype x_dtype,
 // scratch a linear call of m tokens needs (the prefill GEMM's staging and split-K slabs)
 // MFMA GEMM or GEMV passes (of up to 8 tokens, Q6_K 4), by the measured crossover on
 // MI355X: Q4_K from 5 tokens with bf16 activations (8 tokens at 4096x12288: 33.8 us as
-// GEMV passes, 20.9 as GEMM) and from 7 with f32 ones (33.0 against 28 at 8), Q6_K from 7
-// (41.1 against 35.2 at 8), Q8_0 from 9 with bf16 activations and from 17 with f32 ones
-// (8 tokens in one batched GEMV pass: 7.9 us at 4096x4096, 17.9 at 4096x12288; 9 f32
-// tokens as GEMM: 20.9 and 39.2 us)
+// GEMV passes, 20.9 as GEMM) and from 7 with f32 ones (33.0 against 28 at 8), Q6_K from 9
+// (8 tokens at 4096x12288: two batched passes 27 us, GEMM 36.8), Q8_0 from 9 with bf16
+// activations and from 17 with f32 ones (8 tokens in one batched GEMV pass: 7.9 us at
+// 4096x4096, 17.9 at 4096x12288; 9 f32 tokens as GEMM: 20.9 and 39.2 us)
 static bool gemm_batch(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
     if (w->L.fmt == NNQ_FMT_Q4_K) return m > (x_dtype == NNQ_BF16 ? 4 : 6);
-    if (w->L.fmt == NNQ_FMT_Q6_K) return m > 6;
+    if (w->L.fmt == NNQ_FMT_Q6_K) return m > 8;
     return m > (x_dtype == NNQ_BF16 ? 8 : 16);
 }
 
@@ -441,7 +441,7 @@ static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype
     }
     // tokens per GEMV pass: Q4_K runs passes of two through its decode kernel (4 tokens:
     // 14.6 us at 4096x12288 against 18.5 in one pass of the block GEMV), Q6_K passes of
-    // four, Q8_0 one pass of up to 8
+    // four through its batched kernel, Q8_0 passes of up to 8 through its batched kernel
     const int64_t mmax = L.fmt == NNQ_FMT_Q6_K ? 4 : (L.fmt == NNQ_FMT_Q4_K ? 2 : 8);
     const int64_t xrow = x_swiglu ? 2 * k : k;
     for (int64_t m0 = 0; m0 < m; m0 += mmax) {

@@ -1,19 +1,23 @@
-// Decode GEMV (m <= 8 tokens) for Q4_K / Q8_0 / Q6_K weights on gfx950.
+// Decode GEMV (up to 8 tokens per launch: Q4_K 2, Q6_K 4, Q8_0 8) for Q4_K / Q8_0 / Q6_K
+// weights on gfx950.
 //
-// One workgroup owns a tile of 16 weight rows and all of K.  Its waves split K
-// into 256-element units (unit u goes to wave u % WAVES) and issue the loads of
-// all their units up front, so a whole K chunk of the tile is in flight at once.
-// Per unit a wave's coalesced 16-byte loads are, lane by lane, the B operand of a
-// 16x16x32 f16 MFMA (the tile16 repack puts them there); nibbles / bytes become
-// packed f16 values with one mask per pair (the integer q is read as an f16
-// subnormal q * 2^-24, exact) and are multiplied against the activation.
-// The activation is staged once per workgroup in LDS as f16 hi + lo parts of
-// x * 2^s (s per token and 256-element unit, chosen so the unit's max|x| lands in
-// [2^14, 2^15)), so the f16 MFMA sees x to ~22 significant bits and every product
-// is exact in the f32 accumulator.  Per-sub-block scales and mins are applied to
-// the MFMA results in f32; waves are combined through LDS at the end.
+// One workgroup owns a tile of 16 weight rows.  Its waves split K into units (256
+// elements; 8 blocks for Q8_0) and issue the activation slices and the weight loads of
+// all their units of a pass up front, so a whole K pass of the tile is in flight at
+// once.  Per unit a wave's coalesced loads are, lane by lane, the B operand of a
+// 16x16x32 f16 MFMA (the tile16 repack puts them there); nibbles / bytes become packed
+// f16 values with one mask per pair (the integer q is read as an f16 subnormal
+// q * 2^-24, exact) and are multiplied against the activation.
+// The decode kernels stage each unit's activation slice in a wave-private LDS buffer as
+// f16 hi + lo parts of x * 2^s (s per token and 32-element block, chosen so the block's
+// max|x| lands in [2^14, 2^15)), so the f16 MFMA sees x to ~22 significant bits and every
+// product is exact in the f32 accumulator; the blocks' powers of two and sums of x stay
+// in registers (wave-uniform scalars) or, for batches, in a small per-wave LDS table.
+// Scales and mins are applied to the MFMA results in f32; waves meet in LDS at the end.
+// The streaming kernels (many tiles per CU: the LM head, the fused gate | up) stage the
+// activation once per workgroup and loop over tiles.
 //
-// A-operand rows: Q4_K / Q8_0 use rows (2t, 2t+1) = (hi, lo) of token t (8 tokens);
+// A-operand rows: Q4_K / Q8_0 use rows (2t, 2t+1) = (hi, lo) of token t;
 // Q6_K uses rows 4t..4t+3 = (hi, lo) x (first / second 16-value sub-block).
 #include <algorithm>
 
@@ -67,25 +71,19 @@ template <int FMT>
 struct Fmt;
 template <>
 struct Fmt<FQ4K> {
-    static constexpr int kMaxTok = 8, kSumGran = 32;
+    static constexpr int kSumGran = 32;
 };
 template <>
 struct Fmt<FQ80> {
-    static constexpr int kMaxTok = 8, kSumGran = 32;
+    static constexpr int kSumGran = 32;
 };
 template <>
 struct Fmt<FQ6K> {
-    static constexpr int kMaxTok = 4, kSumGran = 16;
+    static constexpr int kSumGran = 16;
 };
 
 // Largest number of 8-element activation groups one thread stages per chunk.
 constexpr int kXGroups = 3;
-
-static inline size_t lds_bytes_for(int mt, int kc, int gran, int waves) {
-    size_t stage = (size_t)mt * kc * 4 + (size_t)mt * (kc / gran) * 4;
-    size_t red = (size_t)waves * 8 * 16 * 2 * 4;
-    return (stage > red ? stage : red) + 64;
-}
 
 // ---------------------------------------------------------------------------------
 // Activation staging: x[t][k0 .. k0+kc) -> LDS hi/lo f16 planes of x * 2^s(t,b),
@@ -236,82 +234,6 @@ __device__ __forceinline__ u32x4 a_operand2(const uint16_t *xs, int kc, int mt, 
     if (t < mt) return *reinterpret_cast<const u32x4 *>(xs + ((size_t)t * 2 + part) * kc + kk + 8 * p);
     return u32x4{0u, 0u, 0u, 0u};
 }
-// A operand for Q6_K: row m -> token m>>2, half (m>>1)&1 selects which 16-k sub-block, part m&1
-__device__ __forceinline__ u32x4 a_operand4(const uint16_t *xs, int kc, int mt, int kk) {
-    const int lane = threadIdx.x & 63, m = lane & 15, p = lane >> 4, t = m >> 2, part = m & 1, half = (m >> 1) & 1;
-    if (t < mt && (p >> 1) == half)
-        return *reinterpret_cast<const u32x4 *>(xs + ((size_t)t * 2 + part) * kc + kk + 8 * p);
-    return u32x4{0u, 0u, 0u, 0u};
-}
-
-// Q4_K, sub-block-per-lane-group form.  Lane 16G + n holds row n's 32 bytes of
-// group G, i.e. sub-blocks 2G (low nibbles) and 2G + 1 (high nibbles).  MFMA r of
-// a set consumes bytes 8r .. 8r + 7, so every lane group contributes 8 k of ITS
-// sub-block; the A operand of row 4G + i is non-zero only in k-group G (lanes with
-// l / 16 == (l % 16) / 4 read the activation, the others read zeros), so output
-// rows 4G .. 4G + 3 of lane group G are partial dots over sub-block 2G (+1) alone,
-// for (token 2tp, hi), (2tp, lo), (2tp + 1, hi), (2tp + 1, lo).  Four chained MFMAs
-// finish a sub-block, and its 6-bit scale is applied once per lane.
-template <int NTP>
-__device__ __forceinline__ void compute_q4k(const UnitQ4K &u, const uint16_t *xs, const float *xsum,
-                                            const uint16_t *zero_lds, int kc, int mt, int ul, const float *backs,
-                                            float acc1[4][2], float acc2[4][2]) {
-    const int lane = threadIdx.x & 63, G = lane >> 4, m = lane & 15, i = m & 3;
-    const bool own = G == (m >> 2);
-    // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K packing,
-    // get_scale_min_k4, crates/nn-core/src/layers/quantized/linear.rs:166-176)
-    const float d = f16_to_f32(u.h[0] & 0xFFFFu), dmin = f16_to_f32(u.h[0] >> 16);
-    const uint32_t S1 = u.h[1], S2 = u.h[2], S3 = u.h[3];
-    const uint32_t sc03 = S1 & 0x3F3F3F3Fu, mn03 = S2 & 0x3F3F3F3Fu;
-    const uint32_t sc47 = (S3 & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
-    const uint32_t mn47 = ((S3 >> 4) & 0x0F0F0F0Fu) | ((S2 >> 2) & 0x30303030u);
-    const uint32_t hsel = 0u - (uint32_t)(G >> 1);  // all ones for sub-blocks 4..7
-    const uint32_t scw = (sc03 & ~hsel) | (sc47 & hsel), mnw = (mn03 & ~hsel) | (mn47 & hsel);
-    const uint32_t scp = scw >> (16 * (G & 1)), mnp = mnw >> (16 * (G & 1));
-    const float sc_lo = (float)(scp & 0xFFu), sc_hi = 0.0625f * (float)((scp >> 8) & 0xFFu);
-    const float mn_lo = (float)(mnp & 0xFFu), mn_hi = (float)((mnp >> 8) & 0xFFu);
-
-    floatx4 clo[NTP], chi[NTP];
-    const uint16_t *ap[NTP];
-#pragma unroll
-    for (int tp = 0; tp < NTP; tp++) {
-        clo[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
-        chi[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
-        const int t = 2 * tp + (i >> 1);
-        ap[tp] = (own && t < mt) ? xs + (size_t)(t * 2 + (i & 1)) * kc + ul * 256 + 64 * G : zero_lds;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const u32x4 q = r < 2 ? u.q0 : u.q1;
-        const uint32_t w0 = q[2 * (r & 1)], w1 = q[2 * (r & 1) + 1];
-        const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
-        const u32x4 blo = {w0 & 0x000F000Fu, w0s & 0x000F000Fu, w1 & 0x000F000Fu, w1s & 0x000F000Fu};
-        const u32x4 bhi = {w0 & 0x00F000F0u, w0s & 0x00F000F0u, w1 & 0x00F000F0u, w1s & 0x00F000F0u};
-#pragma unroll
-        for (int tp = 0; tp < NTP; tp++) {
-            clo[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 8 * r), blo, clo[tp]);
-            chi[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 32 + 8 * r), bhi, chi[tp]);
-        }
-    }
-#pragma unroll
-    for (int tp = 0; tp < NTP; tp++) {
-        {
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int t = 2 * tp + h;
-                if (t < mt) {
-                    const float *bk = backs + t * (kc / 32) + ul * 8 + 2 * G;
-                    const float T = (sc_lo * bk[0]) * (clo[tp][2 * h] + clo[tp][2 * h + 1]) +
-                                    (sc_hi * bk[1]) * (chi[tp][2 * h] + chi[tp][2 * h + 1]);
-                    acc1[tp][h] += d * T;
-                    const float *xsp = xsum + (size_t)t * (kc / 32) + ul * 8 + 2 * G;
-                    acc2[tp][h] += dmin * (mn_lo * xsp[0] + mn_hi * xsp[1]);
-                }
-            }
-        }
-    }
-}
-
 __device__ __forceinline__ void compute_unit(const UnitQ80 &u, const uint16_t *xs, const float *xsum, int kc, int mt,
                                              int kk, const float *bku, float acc1[2], float acc2[2]) {
     const int g = (threadIdx.x & 63) >> 4;
@@ -340,38 +262,6 @@ __device__ __forceinline__ void compute_unit(const UnitQ80 &u, const uint16_t *x
     acc1[1] += t1[1];
 }
 
-__device__ __forceinline__ void compute_unit(const UnitQ6K &u, const uint16_t *xs, const float *xsum, int kc, int mt,
-                                             int kk, const float *bku, float acc1[2], float acc2[2]) {
-    const int g = (threadIdx.x & 63) >> 4;  // token of this lane group
-    const bool tok = g < mt;
-    const float *xsg = xsum + (size_t)g * (kc / 16) + kk / 16;
-    const float d = f16_to_f32(u.d);
-    float t1 = 0.f, t2 = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t A = u.q[c][0], B = u.q[c][1], C = u.q[c][2];
-        const u32x4 ba = {((A)&0x000F000Fu) | ((C << 4) & 0x00300030u),
-                          ((A >> 4) & 0x000F000Fu) | ((C << 2) & 0x00300030u),
-                          ((A >> 8) & 0x000F000Fu) | ((C)&0x00300030u),
-                          ((A >> 12) & 0x000F000Fu) | ((C >> 2) & 0x00300030u)};
-        const u32x4 bb = {((B)&0x000F000Fu) | ((C >> 4) & 0x00300030u),
-                          ((B >> 4) & 0x000F000Fu) | ((C >> 6) & 0x00300030u),
-                          ((B >> 8) & 0x000F000Fu) | ((C >> 8) & 0x00300030u),
-                          ((B >> 12) & 0x000F000Fu) | ((C >> 10) & 0x00300030u)};
-        floatx4 ca = mfma16x16x32_f16(a_operand4(xs, kc, mt, kk + 64 * c), ba, floatx4{0.f, 0.f, 0.f, 0.f});
-        floatx4 cb = mfma16x16x32_f16(a_operand4(xs, kc, mt, kk + 64 * c + 32), bb, floatx4{0.f, 0.f, 0.f, 0.f});
-        // sub-blocks 4c .. 4c+3 of this 256-value block
-        const uint32_t sw = u.s[c];
-        const float s0 = (float)(int8_t)(sw & 0xFF), s1 = (float)(int8_t)((sw >> 8) & 0xFF);
-        const float s2 = (float)(int8_t)((sw >> 16) & 0xFF), s3 = (float)(int8_t)(sw >> 24);
-        const float xba = tok ? bku[g * (kc / 32) + 2 * c] : 0.f, xbb = tok ? bku[g * (kc / 32) + 2 * c + 1] : 0.f;
-        t1 += xba * (s0 * (ca[0] + ca[1]) + s1 * (ca[2] + ca[3])) + xbb * (s2 * (cb[0] + cb[1]) + s3 * (cb[2] + cb[3]));
-        if (tok) t2 += s0 * xsg[4 * c] + s1 * xsg[4 * c + 1] + s2 * xsg[4 * c + 2] + s3 * xsg[4 * c + 3];
-    }
-    acc1[0] += d * t1;
-    acc2[0] += d * t2;
-}
-
 template <int FMT>
 struct UnitOf;
 template <>
@@ -391,121 +281,6 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
     uint32_t b = __float_as_uint(v);
     uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - idx);
-}
-
-// One workgroup per 16-row tile.  Per K chunk: the raw activation loads are issued
-// first, then every wave issues the weight loads of all its units of the chunk
-// (unit u goes to wave u % WAVES), then the activation is converted into LDS while
-// the weight loads are in flight, and finally each wave runs its units on the MFMA.
-template <int FMT, int WAVES, int NTP, int UPW>
-__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    using Unit = typename UnitOf<FMT>::T;
-    constexpr int GRAN = Fmt<FMT>::kSumGran;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int64_t tile = blockIdx.x;
-    const int mt = (int)a.m;
-    const int kc = a.kc;
-    uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
-    float *xsum = reinterpret_cast<float *>(smem + (size_t)mt * kc * 4);
-    __shared__ float backs[kXGroups * WAVES * 64 * 8 / 32];  // one per staged 32-element block
-
-    const int64_t kpad = a.nblk * (FMT == FQ80 ? 32 : 256);  // K rounded up to whole 256-element units
-
-    __shared__ u32x4 zero_lds[8];  // A operand of lanes that carry no activation (Q4_K)
-    if (tid < 8) zero_lds[tid] = u32x4{0u, 0u, 0u, 0u};
-
-    // Q4_K: acc[tp][h] = token 2tp + h (partial over this lane group's sub-blocks);
-    // Q8_0 / Q6_K: acc[0][*] as in the per-token-row form
-    float acc1[4][2] = {}, acc2[4][2] = {};
-    for (int64_t k0 = 0; k0 < kpad; k0 += kc) {
-        const int kcur = (int)((kpad - k0) < kc ? (kpad - k0) : kc);
-        const int64_t u0 = k0 / 256;
-        const int ucnt = kcur / 256;
-        XRaw raw;
-        stage_x_load(a, mt, k0, kcur, 1.0f / (float)(kcur / 8), raw);
-        Unit buf[UPW];
-#pragma unroll
-        for (int i = 0; i < UPW; i++) {
-            const int ul = wv + i * WAVES;
-            load_unit(a, tile, u0 + (ul < ucnt ? ul : ucnt - 1), buf[i]);  // unconditional: see stage_x_load
-        }
-        if (k0 > 0) __syncthreads();  // the previous chunk's units have finished reading LDS
-        stage_x_store<GRAN, FMT == FQ80>(a, kc, raw, xs, xsum, backs);
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < UPW; i++) {
-            const int ul = wv + i * WAVES;
-            if (ul < ucnt) {
-                if constexpr (FMT == FQ4K)
-                    compute_q4k<NTP>(buf[i], xs, xsum, reinterpret_cast<const uint16_t *>(zero_lds), kc, mt, ul, backs,
-                                acc1, acc2);
-                else
-                    compute_unit(buf[i], xs, xsum, kc, mt, ul * 256, backs + ul * 8, acc1[0], acc2[0]);
-            }
-        }
-    }
-    __syncthreads();
-
-    // combine waves: red[w][slot][n], slot = token
-    float *red1 = reinterpret_cast<float *>(smem);
-    float *red2 = red1 + WAVES * 8 * 16;
-    const int g = lane >> 4, n = lane & 15;
-    if constexpr (FMT == FQ4K) {
-        // sum the four lane groups (sub-block partials), lane group 0 stores
-#pragma unroll
-        for (int tp = 0; tp < NTP; tp++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                float v1 = acc1[tp][h], v2 = acc2[tp][h];
-                v1 += __shfl_xor(v1, 16, 64);
-                v2 += __shfl_xor(v2, 16, 64);
-                v1 += __shfl_xor(v1, 32, 64);
-                v2 += __shfl_xor(v2, 32, 64);
-                if (g == 0) {
-                    red1[(wv * 8 + 2 * tp + h) * 16 + n] = v1;
-                    red2[(wv * 8 + 2 * tp + h) * 16 + n] = v2;
-                }
-            }
-    } else if constexpr (FMT == FQ6K) {
-        red1[(wv * 8 + g) * 16 + n] = acc1[0][0];
-        red2[(wv * 8 + g) * 16 + n] = acc2[0][0];
-    } else {
-        red1[(wv * 8 + 2 * g) * 16 + n] = acc1[0][0];
-        red1[(wv * 8 + 2 * g + 1) * 16 + n] = acc1[0][1];
-        red2[(wv * 8 + 2 * g) * 16 + n] = acc2[0][0];
-        red2[(wv * 8 + 2 * g + 1) * 16 + n] = acc2[0][1];
-    }
-    __syncthreads();
-    if (tid < mt * 16) {
-        const int t = tid >> 4, nn = tid & 15;
-        float s1 = 0.f, s2 = 0.f;
-        for (int w = 0; w < WAVES; w++) {
-            s1 += red1[(w * 8 + t) * 16 + nn];
-            s2 += red2[(w * 8 + t) * 16 + nn];
-        }
-        // s1 carries the f16-subnormal factor 2^-24 of the integer weight codes
-        const float bias_k = FMT == FQ4K ? 1.0f : (FMT == FQ80 ? 128.0f : 32.0f);
-        float y = s1 * 16777216.0f - bias_k * s2;
-        const int64_t row = tile * 16 + nn;
-        if (row < a.n) {
-            if (a.bias) y += a.bias[row];
-            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
-            if (a.y_bf16)
-                reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
-            else
-                reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
-        }
-        if (a.argmax_partial && t == 0) {
-            // first-index argmax of this tile's 16 logits (row-major order), NaN -> max key
-            uint64_t key = row < a.n ? (y != y ? ~0ull : argmax_key(y, (uint32_t)row)) : 0ull;
-            for (int o = 8; o > 0; o >>= 1) {
-                uint64_t other = __shfl_xor(key, o, 16);
-                key = other > key ? other : key;
-            }
-            if (nn == 0) a.argmax_partial[tile] = key;
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------------
@@ -634,7 +409,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(GemvArgs a) {
 //    an exact f16 built from the byte s ^ 0x80 under exponent 10), and enter the f32
 //    sums through mixed-precision FMAs;
 //  * weight pointers are scalar per wave and tile.
-// Q6_K codes q (6 bits) enter as f16 subnormals q * 2^-24, exact, as in compute_unit.
+// Q6_K codes q (6 bits) enter as f16 subnormals q * 2^-24, exact, as in the decode kernels.
 // ---------------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t i8pair_to_f16x2(uint32_t w, int hi) {
     // bytes (2 hi, 2 hi + 1) of w -> f16 (s0, s1): 0x64 | (b ^ 0x80) is 1152 + s exactly
@@ -1606,6 +1381,124 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_decode_kernel(GemvArgs a)
 }
 
 // ---------------------------------------------------------------------------------
+// Q6_K batched decode (3 <= m <= 4 tokens, the rows past m zero): gemv_q6k_decode_kernel's
+// unit math with all four token row groups in use (lane group t holds token t); each
+// token's block powers of two and sub-block sums go through a per-wave LDS table (8 + 16
+// floats) that its lane group reads with broadcast 16-byte loads.  One unit per wave
+// and pass.
+// ---------------------------------------------------------------------------------
+template <int WAVES, int XM>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q6k_batch_kernel(GemvArgs a) {
+    constexpr bool XB = XM == 1;
+    constexpr int MT = 4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = (int)blockIdx.x, mt = (int)a.m;
+    constexpr int kBuf = MT * 512 + 256;
+    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][kBuf];
+    __shared__ __attribute__((aligned(16))) float stats[WAVES][MT][24];  // [token][8 x 2^-s, 16 x sum]
+    __shared__ float red[WAVES][MT][16];
+    if (lane < 32) *reinterpret_cast<u32x4 *>(&xbuf[wv][MT * 512 + 8 * lane]) = u32x4{0u, 0u, 0u, 0u};
+
+    const int r16 = lane & 15, kg = lane >> 4, g = kg;
+    const int at = r16 >> 2, ah = (r16 >> 1) & 1, apart = r16 & 1;
+    const int aoff = (kg >> 1) == ah ? (at * 2 + apart) * 256 + 8 * kg : MT * 512 + 8 * kg;
+
+    const int units = (int)a.nblk, k = (int)a.k;
+    constexpr int xe = XB ? 2 : 4;
+    const int xrow = XM == 2 ? 2 * k : k;
+    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x);
+    float acc1 = 0.f, acc2 = 0.f;  // token g
+    for (int ub0 = 0; ub0 < units; ub0 += WAVES) {
+        const int u = min(ub0 + wv, units - 1);
+        u32x4 xr[MT], xu[XM == 2 ? MT : 1];
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const uint8_t *p = xb + (size_t)(t < mt ? t * xrow + u * 256 + 4 * lane : 0) * xe;  // past m: x[0]
+            if (XB) {
+                const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+                xr[t] = u32x4{w2[0], w2[1], 0u, 0u};
+            } else {
+                xr[t] = *reinterpret_cast<const u32x4 *>(p);
+            }
+            if constexpr (XM == 2) xu[t] = *reinterpret_cast<const u32x4 *>(p + (size_t)k * 4);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep this issue order
+        UnitQ6K w;
+        load_unit(a, tile, u, w);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ub0 + wv >= units) break;  // wave-uniform: no unit left for this wave
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            u32x4 xv = xr[t];
+            if constexpr (XM == 2) xv = swiglu4(xv, xu[t]);
+            if (t >= mt) xv = u32x4{0u, 0u, 0u, 0u};  // rows past the batch: zeros (bf16 or f32)
+            float bk, x16;
+            stage_q6k<XB>(xv, xbuf[wv] + 512 * t, xbuf[wv] + 512 * t + 256, bk, x16);
+            if ((lane & 7) == 0) stats[wv][t][lane >> 3] = bk;
+            if ((lane & 3) == 0) stats[wv][t][8 + (lane >> 2)] = x16;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint16_t *ap = xbuf[wv] + aoff;
+        u32x4 av[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) av[b] = *reinterpret_cast<const u32x4 *>(ap + 32 * b);
+        floatx4 st[6];
+#pragma unroll
+        for (int i = 0; i < 6; i++) st[i] = *reinterpret_cast<const floatx4 *>(&stats[wv][g][4 * i]);
+        floatx4 c[8];
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const uint32_t A = w.q[cc][0], B = w.q[cc][1], C = w.q[cc][2];
+            const u32x4 ba = {(A & 0x000F000Fu) | ((C << 4) & 0x00300030u), ((A >> 4) & 0x000F000Fu) | ((C << 2) & 0x00300030u),
+                              ((A >> 8) & 0x000F000Fu) | (C & 0x00300030u), ((A >> 12) & 0x000F000Fu) | ((C >> 2) & 0x00300030u)};
+            const u32x4 bb = {(B & 0x000F000Fu) | ((C >> 4) & 0x00300030u), ((B >> 4) & 0x000F000Fu) | ((C >> 6) & 0x00300030u),
+                              ((B >> 8) & 0x000F000Fu) | ((C >> 8) & 0x00300030u),
+                              ((B >> 12) & 0x000F000Fu) | ((C >> 10) & 0x00300030u)};
+            c[2 * cc] = mfma16x16x32_f16(av[2 * cc], ba, floatx4{0.f, 0.f, 0.f, 0.f});
+            c[2 * cc + 1] = mfma16x16x32_f16(av[2 * cc + 1], bb, floatx4{0.f, 0.f, 0.f, 0.f});
+        }
+        float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const uint32_t sw = w.s[b >> 1] >> (16 * (b & 1));
+            const float sa = (float)(int8_t)(sw & 0xFFu), sbv = (float)(int8_t)((sw >> 8) & 0xFFu);
+            const float back = st[b >> 2][b & 3];
+            const float xa = st[2 + (2 * b) / 4][(2 * b) & 3], xbs = st[2 + (2 * b + 1) / 4][(2 * b + 1) & 3];
+            t1 += back * (sa * (c[b][0] + c[b][1]) + sbv * (c[b][2] + c[b][3]));
+            t2 += sa * xa + sbv * xbs;
+        }
+        const float d = f16_to_f32(w.d & 0xFFFFu);
+        acc1 += d * t1;
+        acc2 += d * t2;
+        // the next pass rewrites this wave's buffers only after these reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    red[wv][g][r16] = acc1 * 16777216.0f - 32.0f * acc2;
+    __syncthreads();
+    if (tid < mt * 16) {
+        const int t = tid >> 4, nn = tid & 15;
+        float y = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; w2++) y += red[w2][t][nn];
+        const int64_t row = (int64_t)tile * 16 + nn;
+        if (row < a.n) {
+            if (a.bias) y += a.bias[row];
+            gemv_status(a, y, blockIdx.x == 0 && tid == 0);
+            if (a.y_bf16)
+                reinterpret_cast<uint16_t *>(a.y)[(int64_t)t * a.n + row] = (uint16_t)f32_to_bf16_bits(y);
+            else
+                reinterpret_cast<float *>(a.y)[(int64_t)t * a.n + row] = y;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Q4_K streaming decode GEMV (m <= 2, K <= 16 units, many tiles: the fused gate | up
 // of an MLP).  gemv_q4k_decode_kernel's unit math inside gemv_stream_kernel's tile
 // loop: wave w owns unit w of every tile, stages its activation slice once, keeps the
@@ -1964,52 +1857,6 @@ int launch_nonfinite_check(const void *y, int y_bf16, int64_t count, int32_t *st
 // ---------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------
-template <int FMT, int WAVES, int NTP, int UPW>
-static int launch_gemv_t(const GemvArgs &a0, void *stream) {
-    GemvArgs a = a0;
-    const int mt = (int)a.m;
-    constexpr int gran = Fmt<FMT>::kSumGran;
-    const int64_t kpad = a.nblk * (FMT == FQ80 ? 32 : 256);
-    // K chunk: bounded by LDS (60 KB of staging), by the activation groups the
-    // threads stage in registers, and by the units the waves hold in registers
-    int64_t kc = (int64_t)(61440.0 / (mt * (4.0 + 4.0 / gran)));
-    const int64_t kc_x = (int64_t)kXGroups * WAVES * 64 * 8 / mt;
-    const int64_t kc_u = (int64_t)WAVES * UPW * 256;
-    if (kc > kc_x) kc = kc_x;
-    if (kc > kc_u) kc = kc_u;
-    kc = kc / 256 * 256;
-    if (kc < 256) kc = 256;
-    if (kc > kpad) kc = kpad;
-    a.kc = (int)kc;
-    const size_t lds = lds_bytes_for(mt, a.kc, gran, WAVES);
-    hipLaunchKernelGGL((gemv_kernel<FMT, WAVES, NTP, UPW>), dim3((unsigned)a.ntile), dim3(WAVES * 64), lds,
-                       (hipStream_t)stream, a);
-    return (int)hipGetLastError();
-}
-
-// units per wave: just enough for one chunk to cover K (capped by registers)
-template <int FMT, int WAVES, int NTP>
-static int launch_gemv_u(const GemvArgs &a, int64_t units, void *stream) {
-    constexpr int umax = (FMT == FQ4K && NTP == 1) ? 6 : 3;
-    const int64_t need = (units + WAVES - 1) / WAVES;
-    if (need <= 1) return launch_gemv_t<FMT, WAVES, NTP, 1>(a, stream);
-    if (need <= 2) return launch_gemv_t<FMT, WAVES, NTP, 2>(a, stream);
-    if (need <= 3 || umax == 3) return launch_gemv_t<FMT, WAVES, NTP, 3>(a, stream);
-    if constexpr (umax > 3) {
-        if (need <= 4) return launch_gemv_t<FMT, WAVES, NTP, 4>(a, stream);
-        if (need <= 5) return launch_gemv_t<FMT, WAVES, NTP, 5>(a, stream);
-        return launch_gemv_t<FMT, WAVES, NTP, 6>(a, stream);
-    }
-    return (int)hipErrorInvalidValue;
-}
-
-template <int FMT, int NTP>
-static int launch_gemv_w(const GemvArgs &a, int64_t units, void *stream) {
-    // 8 waves (two per SIMD) unless K is too short to give each of them a unit
-    if (units >= 8) return launch_gemv_u<FMT, 8, NTP>(a, units, stream);
-    return launch_gemv_u<FMT, 4, NTP>(a, units, stream);
-}
-
 // decode (m <= 2): 8 waves with just enough units each to cover K in one pass
 // (longer K loops over passes)
 // streaming kernel: workgroups = CUs (every one loops over tiles); dynamic LDS holds
@@ -2113,6 +1960,25 @@ static int launch_q6k_decode(const GemvArgs &a, int64_t units, void *stream) {
     return launch_q6k_decode_t<16, 3>(a, stream);
 }
 
+template <int WAVES>
+static int launch_q6k_batch_t(const GemvArgs &a, void *stream) {
+    if (a.x_swiglu)
+        hipLaunchKernelGGL((gemv_q6k_batch_kernel<WAVES, 2>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    else if (a.x_bf16)
+        hipLaunchKernelGGL((gemv_q6k_batch_kernel<WAVES, 1>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL((gemv_q6k_batch_kernel<WAVES, 0>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                           (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+// Q6_K batches of 3-4 tokens: waves of one unit per pass, as the Q8_0 batched kernel
+static int launch_q6k_batch(const GemvArgs &a, int64_t units, void *stream) {
+    if (units <= 4) return launch_q6k_batch_t<4>(a, stream);
+    return a.ntile <= 512 && units > 8 ? launch_q6k_batch_t<16>(a, stream) : launch_q6k_batch_t<8>(a, stream);
+}
+
 template <int FMT>
 static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
     // many tiles per CU (the LM head): loop over tiles with the activation staged once
@@ -2132,8 +1998,9 @@ static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
                     hipLaunchKernelGGL((gemv_q6k_stream_kernel<2>), dim3((unsigned)grid), dim3(1024), lds,
                                        (hipStream_t)stream, a);
                 return (int)hipGetLastError();
+            } else {
+                return launch_stream_t<FMT, 16, 1>(a, units, cus, stream);
             }
-            return launch_stream_t<FMT, 16, 1>(a, units, cus, stream);
         }
     }
     static_assert(FMT == FQ80 || FMT == FQ6K, "Q4_K has its own decode launcher");
@@ -2197,25 +2064,15 @@ static int launch_q4k_decode(const GemvArgs &a, void *stream) {
     return launch_q4k_decode_t<16, 4, 1>(a, stream);
 }
 
+// tokens per launch: Q4_K up to 2, Q6_K up to 4, Q8_0 up to 8 (callers run passes)
 int launch_gemv(int fmt, const GemvArgs &a, void *stream) {
-    if (a.m < 1 || a.m > 8 || (fmt == FQ6K && a.m > 4)) return (int)hipErrorInvalidValue;
+    const int mmax = fmt == FQ4K ? 2 : (fmt == FQ6K ? 4 : 8);
+    if (a.m < 1 || a.m > mmax) return (int)hipErrorInvalidValue;
     const int64_t units = fmt == FQ80 ? a.nblk / 8 : a.nblk;
-    if (a.m <= 2) {
-        switch (fmt) {
-        case FQ4K: return launch_q4k_decode(a, stream);
-        case FQ80: return launch_wave<FQ80>(a, units, stream);
-        case FQ6K: return launch_wave<FQ6K>(a, units, stream);
-        }
-        return (int)hipErrorInvalidValue;
-    }
     switch (fmt) {
-    case FQ4K:
-        if (a.m <= 4) return launch_gemv_w<FQ4K, 2>(a, units, stream);
-        return launch_gemv_w<FQ4K, 4>(a, units, stream);
-    case FQ80:
-        return launch_q80_batch(a, units, stream);
-    case FQ6K:
-        return launch_gemv_w<FQ6K, 1>(a, units, stream);
+    case FQ4K: return launch_q4k_decode(a, stream);
+    case FQ80: return a.m <= 2 ? launch_wave<FQ80>(a, units, stream) : launch_q80_batch(a, units, stream);
+    case FQ6K: return a.m <= 2 ? launch_wave<FQ6K>(a, units, stream) : launch_q6k_batch(a, units, stream);
     }
     return (int)hipErrorInvalidValue;
 }
