@@ -399,14 +399,14 @@ static GemmArgs gemm_args(const nnq_weight *w, const void *x, nnq_dtype x_dtype,
 }
 
 // scratch a linear call of m tokens needs (the prefill GEMM's staging and split-K slabs)
-// MFMA GEMM or GEMV passes (of up to 8 tokens, Q6_K 4), by the measured crossover on
-// MI355X: Q4_K from 5 tokens with bf16 activations (8 tokens at 4096x12288: 33.8 us as
-// GEMV passes, 20.9 as GEMM) and from 7 with f32 ones (33.0 against 28 at 8), Q6_K from 9
-// (8 tokens at 4096x12288: two batched passes 27 us, GEMM 36.8), Q8_0 from 9 with bf16
-// activations and from 17 with f32 ones (8 tokens in one batched GEMV pass: 7.9 us at
-// 4096x4096, 17.9 at 4096x12288; 9 f32 tokens as GEMM: 20.9 and 39.2 us)
+// MFMA GEMM or GEMV passes (of up to 8 tokens for Q8_0, 4 otherwise), by the measured
+// crossover on MI355X: Q4_K from 5 tokens with bf16 activations (8 tokens at 4096x12288:
+// 23.6 us as two GEMV passes, 20.7 as GEMM) and from 9 with f32 ones (23.6 against 28.4
+// at 8), Q6_K from 9 (8 tokens at 4096x12288: two batched passes 27 us, GEMM 36.8), Q8_0
+// from 9 with bf16 activations and from 17 with f32 ones (8 tokens in one batched GEMV
+// pass: 7.9 us at 4096x4096, 17.9 at 4096x12288; 9 f32 tokens as GEMM: 20.9 and 39.2 us)
 static bool gemm_batch(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
-    if (w->L.fmt == NNQ_FMT_Q4_K) return m > (x_dtype == NNQ_BF16 ? 4 : 6);
+    if (w->L.fmt == NNQ_FMT_Q4_K) return m > (x_dtype == NNQ_BF16 ? 4 : 8);
     if (w->L.fmt == NNQ_FMT_Q6_K) return m > 8;
     return m > (x_dtype == NNQ_BF16 ? 8 : 16);
 }
@@ -439,10 +439,9 @@ static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype
         if (e) return hip_fail((hipError_t)e, "gemm launch");
         return NNQ_OK;
     }
-    // tokens per GEMV pass: Q4_K runs passes of two through its decode kernel (4 tokens:
-    // 14.6 us at 4096x12288 against 18.5 in one pass of the block GEMV), Q6_K passes of
-    // four through its batched kernel, Q8_0 passes of up to 8 through its batched kernel
-    const int64_t mmax = L.fmt == NNQ_FMT_Q6_K ? 4 : (L.fmt == NNQ_FMT_Q4_K ? 2 : 8);
+    // tokens per GEMV pass: Q4_K and Q6_K up to 4 (their decode kernels with four token
+    // rows), Q8_0 up to 8 (its batched kernel)
+    const int64_t mmax = L.fmt == NNQ_FMT_Q8_0 ? 8 : 4;
     const int64_t xrow = x_swiglu ? 2 * k : k;
     for (int64_t m0 = 0; m0 < m; m0 += mmax) {
         GemvArgs a{};

@@ -1,4 +1,4 @@
-// Decode GEMV (up to 8 tokens per launch: Q4_K 2, Q6_K 4, Q8_0 8) for Q4_K / Q8_0 / Q6_K
+// Decode GEMV (up to 8 tokens per launch: Q4_K and Q6_K 4, Q8_0 8) for Q4_K / Q8_0 / Q6_K
 // weights on gfx950.
 //
 // One workgroup owns a tile of 16 weight rows.  Its waves split K into units (256
@@ -720,11 +720,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
     if (lane < 8 * UPW)  // the wave's own pads, read later only by lanes of this wave
         *reinterpret_cast<u32x4 *>(&xbuf[wv][lane >> 3][MT * 512 + 8 * (lane & 7)]) = u32x4{0u, 0u, 0u, 0u};
 
-    // A-operand rows of lane group G: 4G + 2t + part (token t, hi / lo part) over the
-    // k-group of sub-block 2G (low nibbles) or 2G + 1 (high nibbles); other rows zero.
+    // A-operand rows of lane group G: 4G + 2t + part (token 2 tp + t of MFMA set tp, hi /
+    // lo part) over the k-group of sub-block 2G (low nibbles) or 2G + 1 (high nibbles);
+    // other rows zero.  Four tokens take two sets of MFMAs over the same B operands.
+    static_assert(MT == 1 || MT == 2 || MT == 4, "token rows");
+    constexpr int NTP = (MT + 1) / 2;
     const int G = lane >> 4, n = lane & 15, i = n & 3;
-    const bool own = G == (n >> 2) && (i >> 1) < MT;
-    const int aoff = own ? ((i >> 1) * 2 + (i & 1)) * 256 + 64 * G : MT * 512;
+    int aoff[NTP];
+#pragma unroll
+    for (int tp = 0; tp < NTP; tp++) {
+        const bool own = G == (n >> 2) && 2 * tp + (i >> 1) < MT;
+        aoff[tp] = own ? ((2 * tp + (i >> 1)) * 2 + (i & 1)) * 256 + 64 * G : MT * 512;
+    }
+    const int mt = (int)a.m;  // tokens of the call (MT = 4 holds 3 or 4; the rows past mt are zero)
 
     const int units = (int)a.nblk, k = (int)a.k, ntile = (int)a.ntile;
     const uint8_t *qbase[R], *hbase[R];
@@ -752,7 +760,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
             const uint32_t u = (uint32_t)min(ub0 + wv + j * WAVES, units - 1);
 #pragma unroll
             for (int t = 0; t < MT; t++) {
-                const uint8_t *p = xbase + (uint32_t)(t * xrow + (int)u * 256) * (uint32_t)xe;
+                const int tr = t < mt ? t : 0;  // rows past the batch read row 0, staged as zeros
+                const uint8_t *p = xbase + (uint32_t)(tr * xrow + (int)u * 256) * (uint32_t)xe;
                 if (XB) {
                     const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
                     xr[j][t] = u32x4{w2[0], w2[1], 0u, 0u};
@@ -785,6 +794,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
             for (int t = 0; t < MT; t++) {
                 u32x4 xv = xr[j][t];
                 if constexpr (XM == 2) xv = swiglu4(xv, xu[j][t]);
+                if (MT > 2 && t >= mt) xv = u32x4{0u, 0u, 0u, 0u};  // rows past the batch
                 stage_q4k<XB>(xv, buf + 512 * t, buf + 512 * t + 256, st_all[j][t]);
             }
         }
@@ -796,7 +806,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
         for (int j = 0; j < UPW; j++) {
             if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
             const XStat *st = st_all[j];
-            const uint16_t *ap = xbuf[wv][j] + aoff;
+            const uint16_t *ap[NTP];
+#pragma unroll
+            for (int tp = 0; tp < NTP; tp++) ap[tp] = xbuf[wv][j] + aoff[tp];
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K
@@ -813,7 +825,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
                 const float sc_lo = (float)(scp & 0xFFu), sc_hi = 0.0625f * (float)((scp >> 8) & 0xFFu);
                 const float mn_lo = (float)(mnp & 0xFFu), mn_hi = (float)((mnp >> 8) & 0xFFu);
 
-                floatx4 clo = {0.f, 0.f, 0.f, 0.f}, chi = {0.f, 0.f, 0.f, 0.f};
+                floatx4 clo[NTP], chi[NTP];
+#pragma unroll
+                for (int tp = 0; tp < NTP; tp++) clo[tp] = chi[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {
                     const u32x4 q = q4 < 2 ? w[j][r].q0 : w[j][r].q1;
@@ -821,15 +835,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
                     const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
                     const u32x4 blo = {w0 & 0x000F000Fu, w0s & 0x000F000Fu, w1 & 0x000F000Fu, w1s & 0x000F000Fu};
                     const u32x4 bhi = {w0 & 0x00F000F0u, w0s & 0x00F000F0u, w1 & 0x00F000F0u, w1s & 0x00F000F0u};
-                    clo = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap + 8 * q4), blo, clo);
-                    chi = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap + 32 + 8 * q4), bhi, chi);
+#pragma unroll
+                    for (int tp = 0; tp < NTP; tp++) {
+                        clo[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 8 * q4), blo, clo[tp]);
+                        chi[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 32 + 8 * q4), bhi, chi[tp]);
+                    }
                 }
                 // lane 16G + n now holds, for row n and sub-blocks 2G / 2G + 1, the
-                // (hi, lo) partial dot products of token 0 (entries 0, 1) and token 1 (2, 3)
+                // (hi, lo) partial dot products of token 2 tp (entries 0, 1 of set tp) and
+                // token 2 tp + 1 (entries 2, 3)
 #pragma unroll
                 for (int t = 0; t < MT; t++) {
-                    const float T = (sc_lo * st[t].b_lo) * (clo[2 * t] + clo[2 * t + 1]) +
-                                    (sc_hi * st[t].b_hi) * (chi[2 * t] + chi[2 * t + 1]);
+                    const floatx4 &cl = clo[t >> 1], &ch = chi[t >> 1];
+                    const int e = 2 * (t & 1);
+                    const float T = (sc_lo * st[t].b_lo) * (cl[e] + cl[e + 1]) + (sc_hi * st[t].b_hi) * (ch[e] + ch[e + 1]);
                     acc1[r][t] += d * T;
                     acc2[r][t] += dmin * (mn_lo * st[t].xs_lo + mn_hi * st[t].xs_hi);
                 }
@@ -857,7 +876,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
         if (a.swiglu_out) {
             // rows nn < 8 are gate rows, nn + 8 their up rows (full tiles: n = 2 * inter, inter % 8 == 0)
             store_swiglu_pair(a, y, t, tile, nn, blockIdx.x == 0 && tid == 0);
-        } else if (row < a.n) {
+        } else if (row < a.n && t < mt) {
             if (a.bias) y += a.bias[row];
             gemv_status(a, y, blockIdx.x == 0 && tid == 0);
             if (a.y_bf16)
@@ -2033,8 +2052,28 @@ static int launch_q4k_decode_t(const GemvArgs &a, void *stream) {
 // workgroup (two tiles per workgroup, sharing the staged activation, measured slower).
 static int device_cus();
 
+// batches of 3-4 tokens: four token rows (two MFMA sets over the same B operands), 8
+// waves of up to 3 units or 16 of 2 (the staging buffers of four tokens fill LDS sooner):
+// 4 tokens at 4096x12288 in 11.4 us (two passes of two: 15.0)
+template <int WAVES, int UPW>
+static int launch_q4k_batch_t(const GemvArgs &a, void *stream) {
+    const dim3 grid((unsigned)a.ntile);
+    if (a.x_bf16)
+        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, 1, 1, 4>), grid, dim3(WAVES * 64), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, 1, 0, 4>), grid, dim3(WAVES * 64), 0, (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+
 static int launch_q4k_decode(const GemvArgs &a, void *stream) {
     const int64_t units = a.nblk;
+    if (a.m > 2) {
+        if (a.x_swiglu || a.swiglu_out) return (int)hipErrorInvalidValue;
+        if (units <= 4) return launch_q4k_batch_t<4, 1>(a, stream);
+        if (units <= 8) return launch_q4k_batch_t<8, 1>(a, stream);
+        if (units <= 16) return launch_q4k_batch_t<8, 2>(a, stream);
+        return a.ntile <= 512 ? launch_q4k_batch_t<16, 2>(a, stream) : launch_q4k_batch_t<8, 3>(a, stream);
+    }
     // many tiles per CU and K <= 16 units: one workgroup per CU loops over tiles
     if (!a.x_swiglu && units <= 16) {
         const int cus = device_cus();
@@ -2064,9 +2103,9 @@ static int launch_q4k_decode(const GemvArgs &a, void *stream) {
     return launch_q4k_decode_t<16, 4, 1>(a, stream);
 }
 
-// tokens per launch: Q4_K up to 2, Q6_K up to 4, Q8_0 up to 8 (callers run passes)
+// tokens per launch: Q4_K and Q6_K up to 4, Q8_0 up to 8 (callers run passes)
 int launch_gemv(int fmt, const GemvArgs &a, void *stream) {
-    const int mmax = fmt == FQ4K ? 2 : (fmt == FQ6K ? 4 : 8);
+    const int mmax = fmt == FQ80 ? 8 : 4;
     if (a.m < 1 || a.m > mmax) return (int)hipErrorInvalidValue;
     const int64_t units = fmt == FQ80 ? a.nblk / 8 : a.nblk;
     switch (fmt) {

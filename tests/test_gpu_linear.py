@@ -178,11 +178,12 @@ def test_linear_streaming_many_tiles(O, dev, fmt, n, k, m, xdt):
         assert int(idx) == O.argmax(ref0)
 
 
-@pytest.mark.parametrize("k", [1536, 2560, 6144, 16384, 20480])
-@pytest.mark.parametrize("m,xdt", [(1, "f32"), (2, "f32"), (1, "bf16"), (2, "bf16")])
+@pytest.mark.parametrize("k", [768, 1536, 2560, 6144, 16384, 20480])
+@pytest.mark.parametrize("m,xdt", [(1, "f32"), (2, "f32"), (1, "bf16"), (2, "bf16"), (3, "f32"), (4, "bf16")])
 def test_q4k_decode_launch_shapes(O, dev, k, m, xdt):
-    """Every decode launch shape: K of 6, 10, 24, 64 and 80 units (one wave with a
-    partial second unit, one and two passes), a 37-row tail tile, f32 and bf16 x."""
+    """Every decode launch shape: K of 3, 6, 10, 24, 64 and 80 units (one wave with a
+    partial second unit, one and several passes), a 37-row tail tile, f32 and bf16 x,
+    one, two and (four token rows) three and four tokens."""
     import nn_amd
     n = 37
     b = quantized_weight_bytes("q4_k", n, k, seed=77 + k, O=O)
@@ -196,13 +197,13 @@ def test_q4k_decode_launch_shapes(O, dev, k, m, xdt):
 
 
 @pytest.mark.parametrize("fmt,m,xdt", [("q4_k", 5, "bf16"), ("q4_k", 6, "bf16"), ("q4_k", 8, "bf16"), ("q4_k", 6, "f32"),
-                                       ("q4_k", 7, "f32"),
+                                       ("q4_k", 7, "f32"), ("q4_k", 9, "f32"), ("q4_k", 4, "bf16"),
                                        ("q6_k", 6, "f32"), ("q6_k", 7, "bf16"), ("q6_k", 8, "f32"), ("q8_0", 8, "bf16"),
                                        ("q8_0", 12, "f32"), ("q8_0", 16, "f32"), ("q8_0", 17, "f32"), ("q8_0", 5, "bf16"),
                                        ("q6_k", 3, "bf16"), ("q6_k", 9, "bf16"), ("q6_k", 5, "f32")])
 def test_linear_gemm_crossover(O, dev, fmt, m, xdt):
     """Batches on both sides of each format's GEMV-to-GEMM crossover (Q4_K from 5 tokens
-    with bf16 activations and from 7 with f32 ones, Q6_K from 9, Q8_0 from 9 with bf16
+    with bf16 activations and from 9 with f32 ones, Q6_K from 9, Q8_0 from 9 with bf16
     and from 17 with f32 ones; smaller Q8_0 and Q6_K batches run the batched decode
     kernels in passes of 8 and 4 tokens), with a ragged tile."""
     import nn_amd
