@@ -61,13 +61,6 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// A threshold t with exactly k of the nonzero keys held E per thread at or above it (k <=
-// their number, all distinct; zero keys are padding and take no part): passes over 8-bit
-// digits, most significant first, until the digit bin that holds the kth largest is
-// needed whole (then t is the prefix so far with zeros below) or all 64 bits are fixed
-// (then t is the kth largest key).  Each wave counts into its own histogram (hist holds
-// blockDim / 64 of them), so equal digits only contend within a wave.  Every thread of
-// the workgroup calls it.
 // inclusive prefix sum over the 64 lanes by DPP: shifts within each 16-lane row, then
 // the row totals broadcast into the following rows (row_bcast:15, row_bcast:31)
 __device__ __forceinline__ int wave_scan_incl(int v) {
@@ -80,54 +73,172 @@ __device__ __forceinline__ int wave_scan_incl(int v) {
     return v;
 }
 
+// The value of lane (lane ^ S) for S a power of two below 64, without LDS: DPP within each
+// 16-lane row (quad permutes and mirrors), lane swaps between rows.  Every lane of the
+// wave must be active.
+template <int S>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    static_assert(S >= 1 && S <= 32 && (S & (S - 1)) == 0, "xor distance");
+    const int x = (int)v;
+    if constexpr (S == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (S == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (S == 4) {
+        // quad_perm [3,2,1,0] (l ^ 3), then row_half_mirror (l ^ 7)
+        const int t = __builtin_amdgcn_update_dpp(0, x, 0x1B, 0xF, 0xF, false);
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, t, 0x141, 0xF, 0xF, false);
+    } else if constexpr (S == 8) {
+        // row_half_mirror (l ^ 7), then row_mirror (l ^ 15)
+        const int t = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, t, 0x140, 0xF, 0xF, false);
+    } else if constexpr (S == 16) {
+        // the swap leaves this lane's value and its partner's in the pair
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return p[0] ^ p[1] ^ v;
+    } else {
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return p[0] ^ p[1] ^ v;
+    }
+}
+template <int S>
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
+    return ((uint64_t)lane_xor<S>((uint32_t)(v >> 32)) << 32) | lane_xor<S>((uint32_t)v);
+}
+
+// One compare-exchange step of a bitonic network over one key per lane (partner lane ^ S,
+// descending where lane & size is 0).
+template <int S>
+__device__ __forceinline__ uint64_t bitonic_lanes(uint64_t v, int lane, int size) {
+    const uint64_t o = lane_xor64<S>(v);
+    const bool desc = (lane & size) == 0, lower = (lane & S) == 0;
+    return (lower == desc) ? (o > v ? o : v) : (o < v ? o : v);
+}
+
+// Descending bitonic sort of one key per lane over the first n lanes (n a power of two up
+// to 64; lanes from n on hold keys no larger than any of them, e.g. 0), in registers.
+__device__ uint64_t sort_lanes_desc(uint64_t v, int n) {
+    const int lane = threadIdx.x & 63;
+    if (n >= 2) v = bitonic_lanes<1>(v, lane, 2);
+    if (n >= 4) {
+        v = bitonic_lanes<2>(v, lane, 4);
+        v = bitonic_lanes<1>(v, lane, 4);
+    }
+    if (n >= 8) {
+        v = bitonic_lanes<4>(v, lane, 8);
+        v = bitonic_lanes<2>(v, lane, 8);
+        v = bitonic_lanes<1>(v, lane, 8);
+    }
+    if (n >= 16) {
+        v = bitonic_lanes<8>(v, lane, 16);
+        v = bitonic_lanes<4>(v, lane, 16);
+        v = bitonic_lanes<2>(v, lane, 16);
+        v = bitonic_lanes<1>(v, lane, 16);
+    }
+    if (n >= 32) {
+        v = bitonic_lanes<16>(v, lane, 32);
+        v = bitonic_lanes<8>(v, lane, 32);
+        v = bitonic_lanes<4>(v, lane, 32);
+        v = bitonic_lanes<2>(v, lane, 32);
+        v = bitonic_lanes<1>(v, lane, 32);
+    }
+    if (n >= 64) {
+        v = bitonic_lanes<32>(v, lane, 64);
+        v = bitonic_lanes<16>(v, lane, 64);
+        v = bitonic_lanes<8>(v, lane, 64);
+        v = bitonic_lanes<4>(v, lane, 64);
+        v = bitonic_lanes<2>(v, lane, 64);
+        v = bitonic_lanes<1>(v, lane, 64);
+    }
+    return v;
+}
+
+// A threshold t with exactly k of the nonzero keys held E per thread at or above it (k <=
+// their number, all distinct; zero keys are padding and take no part): passes over 8-bit
+// digits, most significant first, until the digit bin that holds the kth largest is
+// needed whole (then t is the prefix so far with zeros below) or all 64 bits are fixed
+// (then t is the kth largest key).  Each wave counts into its own histogram, so equal
+// digits only contend within a wave, and every wave then reads all NW histograms and
+// finds the bin itself, so a pass needs one barrier: the histograms are double-buffered
+// and each wave clears its own histogram of the other buffer (read by every wave before
+// this pass's barrier) for the next pass.  hist holds 2 * NW * 256 ints.  Every thread of
+// the workgroup calls it; it returns without a closing barrier (hist may still be read).
 template <int E, int NW>
-__device__ uint64_t radix_kth(const uint64_t (&e)[E], int k, int *hist, uint64_t *bcast) {
+__device__ uint64_t radix_kth(const uint64_t (&e)[E], int k, int *hist) {
     uint64_t prefix = 0, mask = 0;
     int rem = k;
-    const int lane = threadIdx.x & 63;
-    int *my = hist + (threadIdx.x / 64) * 256;
-    int *col = hist + NW * 256;  // [256] digit counts summed over the waves
-    for (int shift = 56; shift >= 0; shift -= 8) {
-        for (int i = threadIdx.x; i < 256 * NW; i += NW * 64) hist[i] = 0;
-        __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < 2 * NW * 256; i += NW * 64) hist[i] = 0;
+    __syncthreads();
+    int buf = 0;
+    for (int shift = 56; shift >= 0; shift -= 8, buf ^= 1) {
+        int *H = hist + buf * (NW * 256);
+        int *my = H + wv * 256;
 #pragma unroll
         for (int r = 0; r < E; r++)
             if (e[r] != 0 && (e[r] & mask) == prefix) atomicAdd(&my[(e[r] >> shift) & 255], 1);
         __syncthreads();
-        // column sums: one digit per thread, the NW loads independent of each other
-        for (int d = threadIdx.x; d < 256; d += NW * 64) {
-            int cd = 0;
+        // lane l: the descending digits 255 - 4l - j (j = 0..3), i.e. the 16 bytes at digit
+        // 252 - 4l of every wave's histogram, summed over the waves
+        int c[4] = {0, 0, 0, 0};
 #pragma unroll
-            for (int w = 0; w < NW; w++) cd += hist[w * 256 + d];
-            col[d] = cd;
+        for (int w = 0; w < NW; w++) {
+            const int4 h = *reinterpret_cast<const int4 *>(H + w * 256 + 252 - 4 * lane);
+            c[0] += h.w;
+            c[1] += h.z;
+            c[2] += h.y;
+            c[3] += h.x;
         }
-        __syncthreads();
-        if (threadIdx.x < 64) {
-            // lane l holds digits 255 - 4l .. 252 - 4l (descending order)
-            int c[4], sum = 0;
+        int *other = hist + (buf ^ 1) * (NW * 256) + wv * 256;
+        reinterpret_cast<int4 *>(other)[lane] = int4{0, 0, 0, 0};
+        const int sum = c[0] + c[1] + c[2] + c[3];
+        int before = wave_scan_incl(sum) - sum;  // exclusive scan over the lanes
+        int hit = -1, hbefore = 0, hcount = 0;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                c[j] = col[255 - (4 * lane + j)];
-                sum += c[j];
+        for (int j = 0; j < 4; j++) {
+            if (before < rem && before + c[j] >= rem) {
+                hit = j;
+                hbefore = before;
+                hcount = c[j];
             }
-            int before = wave_scan_incl(sum) - sum;  // exclusive scan over the lanes
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (before < rem && before + c[j] >= rem)
-                    bcast[0] = ((uint64_t)(255 - (4 * lane + j)) << 48) | ((uint64_t)c[j] << 24) | (uint64_t)before;
-                before += c[j];
-            }
+            before += c[j];
         }
-        __syncthreads();
-        const uint64_t b = bcast[0];
-        const int above = (int)(b & 0xFFFFFF), inbin = (int)((b >> 24) & 0xFFFFFF);
+        // exactly one lane holds the bin (k does not exceed the keys that take part)
+        const uint64_t found = __ballot(hit >= 0);
+        if (found == 0) break;  // not reached: callers keep k within the keys that take part
+        const int src = (int)__builtin_ctzll(found);
+        const int digit = 255 - 4 * src - __builtin_amdgcn_readlane(hit, src);
+        const int above = __builtin_amdgcn_readlane(hbefore, src), inbin = __builtin_amdgcn_readlane(hcount, src);
         rem -= above;
-        prefix |= (b >> 48) << shift;
+        prefix |= (uint64_t)digit << shift;
         mask |= 0xFFull << shift;
-        __syncthreads();  // bcast and hist are rewritten by the next pass
         if (inbin == rem) break;  // the whole bin is taken (uniform)
     }
     return prefix;
+}
+
+// Appends the keys e[r] >= kth (nonzero) to out at slots taken from the LDS counter *n:
+// one counter atomic per wave, the slots within the wave by lane rank.  Every lane of the
+// calling wave must be active.
+template <int E>
+__device__ __forceinline__ void append_selected(const uint64_t (&e)[E], uint64_t kth, int *n, uint64_t *out) {
+    uint64_t bal[E];
+    int total = 0;
+#pragma unroll
+    for (int r = 0; r < E; r++) {
+        bal[r] = __ballot(e[r] >= kth && e[r] != 0);
+        total += __builtin_popcountll(bal[r]);
+    }
+    if (total == 0) return;  // uniform
+    int base = 0;
+    if ((threadIdx.x & 63) == 0) base = atomicAdd(n, total);
+    base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+    for (int r = 0; r < E; r++) {
+        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal[r] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal[r], 0));
+        if ((bal[r] >> (threadIdx.x & 63)) & 1) out[base + below] = e[r];
+        base += __builtin_popcountll(bal[r]);
+    }
 }
 
 // Bitonic sort, descending, of n keys in LDS (n a power of two <= 16384); all threads
@@ -136,16 +247,9 @@ __device__ uint64_t radix_kth(const uint64_t (&e)[E], int k, int *hist, uint64_t
 // publishes the result to the other waves.
 __device__ void sort_desc_lds(uint64_t *a, int n) {
     if (n <= 64) {
-        // one key per lane of wave 0, the network on registers (lane exchanges)
         if (threadIdx.x < 64) {
             const int lane = threadIdx.x;
-            uint64_t v = lane < n ? a[lane] : 0ull;
-            for (int size = 2; size <= n; size <<= 1)
-                for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                    const uint64_t o = __shfl_xor(v, stride, 64);
-                    const bool desc = (lane & size) == 0, lower = (lane & stride) == 0;
-                    v = (lower == desc) ? (o > v ? o : v) : (o < v ? o : v);
-                }
+            const uint64_t v = sort_lanes_desc(lane < n ? a[lane] : 0ull, n);
             if (lane < n) a[lane] = v;
         }
         __syncthreads();
@@ -223,8 +327,7 @@ __device__ void block_keys(const float *logits, int64_t n, const uint32_t *past,
 __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, int64_t n, const uint32_t *past,
                                                            int64_t n_past, SampleParams sp, int kk, uint64_t *cand) {
     __shared__ int cnt[kSampleBlock];
-    __shared__ int hist[5 * 256];
-    __shared__ uint64_t bcast[1];
+    __shared__ __attribute__((aligned(16))) int hist[2 * 4 * 256];
     __shared__ int nout;
     const int tid = threadIdx.x;
     const int64_t base = (int64_t)blockIdx.x * kSampleBlock;
@@ -235,11 +338,9 @@ __global__ __launch_bounds__(256) void sample_local_kernel(const float *logits, 
     // the block's real logits may be fewer than kk: keep them all, pad the slots with 0
     const int real = (int)std::min<int64_t>(kSampleBlock, n - base);
     const int kb = std::min(kk, real);
-    const uint64_t kth = radix_kth<E, 4>(e, kb, hist, bcast);
+    const uint64_t kth = radix_kth<E, 4>(e, kb, hist);  // (its first barrier orders nout)
     uint64_t *out = cand + (int64_t)blockIdx.x * kk;
-#pragma unroll
-    for (int r = 0; r < E; r++)
-        if (e[r] >= kth && e[r] != 0) out[atomicAdd(&nout, 1)] = e[r];
+    append_selected<E>(e, kth, &nout, out);
     for (int j = kb + tid; j < kk; j += 256) out[j] = 0;
 }
 
@@ -299,14 +400,129 @@ __device__ int walk_wave(const float *p, int n, F stop) {
     return n;
 }
 
+// ((0 + x_0) + x_1) + ... + x_{n-1} over lanes 0 .. n - 1 (n <= 64) in lane order, the
+// same value in every lane: one addition after another, the addends read by readlane.
+// x must be 0 in the lanes at or past n and no addend negative (adding +0 to a sum that
+// is not negative leaves it unchanged), so whole groups of 16 lanes are added.
+__device__ __forceinline__ float ordered_lane_sum(float x, int n) {
+    float s = 0.0f;
+    for (int j0 = 0; j0 < n; j0 += 16)
+#pragma unroll
+        for (int j = 0; j < 16; j++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j0 + j));
+    return s;
+}
+
+// the first lane i < n whose cumulative sum p_0 + ... + p_i (in lane order, p >= 0 and 0
+// at or past n) meets `stop`, n when none
+template <class F>
+__device__ __forceinline__ int walk_lanes(float p, int n, F stop) {
+    const int lane = threadIdx.x & 63;
+    float cum = 0.0f, mine = 0.0f;
+    for (int j0 = 0; j0 < n; j0 += 16)
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            cum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j0 + j));
+            mine = lane == j0 + j ? cum : mine;
+        }
+    const uint64_t hit = __ballot(lane < n && stop(mine));
+    return hit ? (int)__builtin_ctzll(hit) : n;
+}
+
+// softmax_candidates (sampling.rs:371-391) of the lane values v of lanes 0 .. n - 1
+// (n <= 64): this lane's probability, 0 at or past n.  The maximum is order-free, the
+// sum runs in candidate order.
+__device__ __forceinline__ float softmax_lanes(float v, int n) {
+    const int lane = threadIdx.x & 63;
+    const bool in = lane < n;
+    const float mx = wave_max(in ? v : -INFINITY);
+    if (!(fabsf(mx) <= 3.402823466e38f)) return in ? 1.0f / (float)n : 0.0f;
+    const float ex = in ? expf(v - mx) : 0.0f;
+    const float sum = ordered_lane_sum(ex, n);
+    if (!(fabsf(sum) <= 3.402823466e38f) || sum == 0.0f) return in ? 1.0f / (float)n : 0.0f;
+    return in ? ex / sum : 0.0f;
+}
+
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+    return ((uint64_t)(uint32_t)__shfl((int)(v >> 32), src, 64) << 32) | (uint32_t)__shfl((int)v, src, 64);
+}
+
+// argmax_slice (sampling.rs:394-400) of the original logits, by one thread: the running
+// maximum moves on unless it compares greater (ties and NaN move on)
+__device__ void argmax_slice_serial(const float *logits, int64_t n, uint32_t *token) {
+    int64_t best = 0;
+    float bv = logits[0];
+    for (int64_t j = 1; j < n; j++) {
+        const float v = logits[j];
+        if (!(bv > v)) {
+            best = j;
+            bv = v;
+        }
+    }
+    *token = (uint32_t)best;
+}
+
+// The reference's tail for top-k up to 64, by wave 0 with one candidate per lane: sel[0..k)
+// holds the top k keys (unordered).  They are sorted in registers; the candidates then
+// sit in lanes 0 .. nc - 1 in the reference's order (descending for top-p, else ascending
+// index), and the top-p cut, softmax and selector walk run on lane values.
+__device__ void tail_lanes(const float *logits, int64_t n, const uint64_t *sel, int k, const SampleParams &sp,
+                           uint32_t *token) {
+    const int lane = threadIdx.x & 63;
+    const bool keep_inf = sp.keep_inf != 0;
+    int Q = 1;
+    while (Q < k) Q <<= 1;
+    const uint64_t v = sort_lanes_desc(lane < k ? sel[lane] : 0ull, Q);  // ties: lower index first
+    uint64_t w;
+    int nc;
+    if (!sp.use_top_p && k > 1) {
+        // without top-p the reference walks the candidates in index order: sort again by
+        // (candidate first, ascending index), carrying each one's lane
+        uint64_t r = 0;
+        if (lane < k && key_cand(v, keep_inf))
+            r = 0x8000000000000000ull | ((uint64_t)(0xFFFFFFFFu - key_idx(v)) << 14) | (uint64_t)lane;
+        r = sort_lanes_desc(r, Q);
+        nc = __builtin_popcountll(__ballot(r >> 63));
+        w = shfl_u64(v, (int)(r & 63));
+    } else {
+        // descending order: +inf keys first, then the finite ones, then -inf and NaN; the
+        // candidates move to the front in order (the +inf keys are candidates, and stay in
+        // front, only when top_k is None)
+        nc = __builtin_popcountll(__ballot(lane < k && key_cand(v, keep_inf)));
+        const int a = __builtin_popcountll(__ballot(lane < k && !keep_inf && (uint32_t)(v >> 32) == kOrdPosInf));
+        w = shfl_u64(v, std::min(lane + a, 63));
+    }
+    const float val = key_val(w);  // lanes < nc: the candidates' values and indices
+    const int id = (int)key_idx(w);
+    if (sp.use_top_p && nc > 0) {
+        // apply_top_p_candidates: the smallest prefix (descending order) whose cumulative
+        // probability reaches top_p
+        const float tp = sp.top_p;
+        const int i = walk_lanes(softmax_lanes(val, nc), nc, [tp](float cum) { return cum >= tp; });
+        nc = i < nc ? i + 1 : nc;
+    }
+    if (nc == 0) {
+        if (lane == 0) argmax_slice_serial(logits, n, token);
+        return;
+    }
+    if (nc == 1) {
+        const int pick = __builtin_amdgcn_readlane(id, 0);
+        if (lane == 0) *token = (uint32_t)pick;
+        return;
+    }
+    const float selector = (float)(sp.seed % 10000ull) / 10000.0f;
+    const int i = walk_lanes(softmax_lanes(val, nc), nc, [selector](float cum) { return selector < cum; });
+    const int pick = __builtin_amdgcn_readlane(id, i < nc ? i : nc - 1);
+    if (lane == 0) *token = (uint32_t)pick;
+}
+
 template <int NTH>
 __global__ __launch_bounds__(NTH) void sample_final_kernel(const float *logits, int64_t n, const uint64_t *cand,
                                                             int ncand, SampleParams sp, float *work,
                                                             uint32_t *token) {
-    __shared__ uint64_t sel[kSampleMaxCand];
-    __shared__ int hist[(NTH / 64 + 1) * 256];
-    __shared__ uint64_t bcast[1];
+    __shared__ __attribute__((aligned(16))) uint64_t sel[kSampleMaxCand];
     __shared__ int nsel;
+    // the select's histograms borrow the top of sel (free until the selected keys go in)
+    int *hist = reinterpret_cast<int *>(sel + kSampleMaxCand) - 2 * (NTH / 64) * 256;
     constexpr int E = 16;  // keys per thread: NTH * 16 >= the candidates (host-checked)
     const int tid = threadIdx.x, k = (int)sp.k;
     // the tail's arrays: in the upper half of `sel` when k <= 2048, else global scratch
@@ -324,14 +540,17 @@ __global__ __launch_bounds__(NTH) void sample_final_kernel(const float *logits, 
             e[r] = j < ncand ? cand[j] : 0ull;
         }
         if (tid == 0) nsel = 0;
-        const uint64_t kth = radix_kth<E, NTH / 64>(e, k, hist, bcast);  // (its barriers order nsel)
+        const uint64_t kth = radix_kth<E, NTH / 64>(e, k, hist);  // (its first barrier orders nsel)
+        __syncthreads();  // every wave is done with hist before sel is written
         int Q = 1;
         while (Q < k) Q <<= 1;
         for (int j = k + tid; j < Q; j += NTH) sel[j] = 0;
-#pragma unroll
-        for (int r = 0; r < E; r++)
-            if (e[r] >= kth && e[r] != 0) sel[atomicAdd(&nsel, 1)] = e[r];
+        append_selected<E>(e, kth, &nsel, sel);
         __syncthreads();
+        if (k <= 64) {
+            if (tid < 64) tail_lanes(logits, n, sel, k, sp, token);
+            return;
+        }
         sort_desc_lds(sel, Q);  // sel[0..k): the top k, descending (ties: lower index first)
         if (!sp.use_top_p && k > 1) {
             // without top-p the reference walks the candidates in index order: re-sort by
@@ -396,20 +615,7 @@ __global__ __launch_bounds__(NTH) void sample_final_kernel(const float *logits, 
         nc = i < nc ? i + 1 : nc;
     }
     if (nc == 0) {
-        // argmax_slice of the original logits: the running maximum moves on unless it
-        // compares greater (ties and NaN move on)
-        if (tid == 0) {
-            int64_t best = 0;
-            float bv = logits[0];
-            for (int64_t j = 1; j < n; j++) {
-                const float v = logits[j];
-                if (!(bv > v)) {
-                    best = j;
-                    bv = v;
-                }
-            }
-            *token = (uint32_t)best;
-        }
+        if (tid == 0) argmax_slice_serial(logits, n, token);
         return;
     }
     if (nc == 1) {
@@ -650,18 +856,7 @@ __global__ __launch_bounds__(1024) void sample_large_final_kernel(const float *l
         nc = i < nc ? i + 1 : nc;
     }
     if (nc == 0) {
-        if (tid == 0) {  // argmax_slice of the original logits (sampling.rs:394-400)
-            int64_t best = 0;
-            float bv = logits[0];
-            for (int64_t j = 1; j < n; j++) {
-                const float v = logits[j];
-                if (!(bv > v)) {
-                    best = j;
-                    bv = v;
-                }
-            }
-            *token = (uint32_t)best;
-        }
+        if (tid == 0) argmax_slice_serial(logits, n, token);
         return;
     }
     if (nc == 1) {
