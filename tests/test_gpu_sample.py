@@ -73,6 +73,21 @@ def test_sample_vs_oracle(O, dev, n, ci):
         assert got == want, (n, cfg, seed)
 
 
+@pytest.mark.parametrize("top_p", [None, 0.8])
+def test_sample_ties_around_register_tail(O, dev, top_p):
+    """Top-k up to 64 is sorted and finished in registers, from 65 on in LDS: logits with
+    few distinct values (many exact ties, broken by the lower index) for k on both sides
+    of that boundary, against the oracle."""
+    import nn_amd
+    n = 5000
+    lg = np.round(nn_amd.synth_normal(77, 1, (n,), 1.5) * 2.0).astype(np.float32) / 2.0
+    t = torch.from_numpy(lg).to(dev)
+    for k in (2, 17, 33, 63, 64, 65, 128):
+        for seed in (0, 3333, 9999):
+            got = int(nn_amd.sample_token(t, temperature=1.0, top_k=k, top_p=top_p, seed=seed).item())
+            assert got == O.sample_token(lg, temperature=1.0, top_k=k, top_p=top_p, seed=seed), (k, top_p, seed)
+
+
 def test_sample_top_k_none_small_vocab(O, dev):
     import nn_amd
     n = 3000
