@@ -593,7 +593,18 @@ struct MoeRun {
     const uint16_t *xa[2];  // activation planes (bf16), rows of H
     int64_t A;              // assignments (T * k): rows of the sorted buffers
     float limit;
+    // gate_up finds its expert's rows itself (no permute launch) when perm is set:
+    // ti[T][k] the routed experts; the expert's group-0 workgroup writes off and pos
+    const uint32_t *ti;
+    int64_t T;
+    int k;
+    int perm;
 };
+
+// batches up to this many tokens skip the permute launch (the expert's token list, one
+// int per token, sits in LDS)
+constexpr int kMoeInPermT = 1024;
+constexpr size_t kMoePermLds = (size_t)kMoeInPermT * 4 + 64 * 4;
 
 // Column streams.  gate_up: stream s = the pair of 32-column blocks (gate s, up I/32 + s),
 // both owned by one wave, so the SwiGLU epilogue needs no exchange; down: stream s =
@@ -629,7 +640,7 @@ __host__ __device__ constexpr int64_t moe_kbp(int64_t KB) { return (KB + 31) / 3
 
 template <int P, bool GU, int CKB, bool SL>
 constexpr size_t moe_lds(int64_t KB) {
-    return MoeK<P, CKB>::RING + (SL ? (size_t)kMoeWaves * (GU ? 2 : 1) * moe_kbp(KB) * 32 : 0);
+    return MoeK<P, CKB>::RING + (SL ? (size_t)kMoeWaves * (GU ? 2 : 1) * moe_kbp(KB) * 32 : 0) + (GU ? kMoePermLds : 0);
 }
 
 // slot of the 16-byte granule kc of row r among the row's granules of a chunk: rows r
@@ -654,10 +665,67 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
     const int nwg = (int)gridDim.x, bid = (int)blockIdx.x;
     const int item = (nwg % 8 == 0) ? (bid % 8) * (nwg / 8) + bid / 8 : bid;
     const int64_t e = item / kMoeGroups, g = item % kMoeGroups;
-    const int32_t r0 = sc.off[e], ne = sc.off[e + 1] - r0;
-    if (ne == 0) return;  // workgroup-uniform
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // the expert's tokens in ascending order (in-kernel permutation only)
+    int32_t *tok_s = reinterpret_cast<int32_t *>(smem + C::RING + (SL ? (size_t)kMoeWaves * NBW * KBP * 32 : 0));
+    int32_t r0, ne;
+    if (GU && run.perm) {
+        // moe_permute_kernel's result for this expert: r0 = the assignments to lower
+        // experts, the rows = its tokens in ascending order (a token routes to an expert
+        // at most once), counted per wave and ordered by lane rank
+        int32_t *wc = tok_s + kMoeInPermT;  // [2][kMoeWaves]
+        const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+        int below = 0;
+        ne = 0;
+        for (int64_t t0 = 0; t0 < run.T; t0 += NTH) {
+            const int64_t t = t0 + tid;
+            bool hit = false;
+            if (t < run.T)
+                for (int q = 0; q < run.k; q++) {
+                    const uint32_t x = run.ti[t * run.k + q];
+                    below += x < (uint32_t)e ? 1 : 0;
+                    hit |= x == (uint32_t)e;
+                }
+            const uint64_t m = __ballot(hit);
+            if (lane == 0) wc[wv] = __popcll(m);
+            __syncthreads();
+            int before = ne, total = 0;
+            for (int w = 0; w < kMoeWaves; w++) {
+                const int c = wc[w];
+                before += w < wv ? c : 0;
+                total += c;
+            }
+            if (hit) tok_s[before + __popcll(m & lt)] = (int32_t)t;
+            ne += total;
+            __syncthreads();  // wc is rewritten by the next chunk
+        }
+        below = wave_sum_i32(below);
+        if (lane == 0) wc[kMoeWaves + wv] = below;
+        __syncthreads();  // also publishes tok_s
+        r0 = 0;
+        for (int w = 0; w < kMoeWaves; w++) r0 += wc[kMoeWaves + w];
+        // the same in every lane: scalar registers for the epilogue's uniform addressing
+        r0 = __builtin_amdgcn_readfirstlane(r0);
+        ne = __builtin_amdgcn_readfirstlane(ne);
+        if (g == 0) {
+            // for the down and combine launches: the expert's first row, the total, and
+            // each assignment's row
+            if (tid == 0) {
+                sc.off[e] = r0;
+                if (e == d.E - 1) sc.off[d.E] = (int32_t)run.A;
+            }
+            for (int i = tid; i < ne; i += NTH) {
+                const int64_t t = tok_s[i];
+                for (int q = 0; q < run.k; q++)
+                    if (run.ti[t * run.k + q] == (uint32_t)e) sc.pos[t * run.k + q] = r0 + i;
+            }
+        }
+    } else {
+        r0 = sc.off[e];
+        ne = sc.off[e + 1] - r0;
+    }
+    if (ne == 0) return;  // workgroup-uniform
     const int p = lane >> 4, l16 = lane & 15;
     const int s_lo = (int)(g * S / kMoeGroups), s_hi = (int)((g + 1) * S / kMoeGroups);
     const int nch = (int)(KB / CKB);  // K / 32 is a multiple of CKB (the host picks CKB)
@@ -679,7 +747,8 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
             const int r = rem / C::ROWG, slot = rem % C::ROWG;
             const int kc = moe_slot(slot, r);  // the row's 16-byte granule held at this slot
             const int32_t rr = r0 + m0 + min(r, ne - m0 - 1);  // rows past the expert repeat its last row
-            aoff[j] = (uint32_t)(2 * ((int64_t)pl * pstride + (GU ? (int64_t)sc.stok[rr] * H : (int64_t)rr * I) + 8 * kc));
+            const int64_t tok = GU ? (run.perm ? tok_s[rr - r0] : sc.stok[rr]) : 0;
+            aoff[j] = (uint32_t)(2 * ((int64_t)pl * pstride + (GU ? tok * H : (int64_t)rr * I) + 8 * kc));
         }
         auto issue = [&](int ch) {
             const int cv = min(ch, nch - 1);  // past the end: re-copy the last chunk
@@ -1056,13 +1125,17 @@ int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const floa
     MoeRun run;
     run.A = T * k;
     run.limit = limit;
+    run.ti = sc.ti;
+    run.T = T;
+    run.k = k;
+    run.perm = T <= kMoeInPermT ? 1 : 0;
     if (d.E <= 256)
         hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, nsplit, bias, T,
                            (int)d.E, k, sc.ti, sc.tw, topk_idx, topk_w);
     else
         hipLaunchKernelGGL(moe_route_any_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), (size_t)4 * d.E * 4, st,
                            logits, nsplit, bias, T, (int)d.E, k, sc.ti, sc.tw, topk_idx, topk_w);
-    switch (k) {
+    if (!run.perm) switch (k) {
 #define NNQ_PERM(K)                                                                                              \
     case K:                                                                                                      \
         hipLaunchKernelGGL(moe_permute_kernel<K>, dim3(1), dim3(1024), (size_t)d.E * 4, st, sc.ti, T, (int)d.E, sc.off, \
