@@ -6,7 +6,8 @@
 //            renormalisation (crates/nn-core/src/dyn_tensor/ops_ext/sorting.rs:22-104)
 //   permute  per-expert counts, offsets and a stable (token, slot) order of the
 //            assignments: expert e's rows are its tokens in ascending order, as the
-//            host grouping of moe_forward (:157-169) builds them
+//            host grouping of moe_forward (:157-169) builds them; a launch of its own
+//            only for batches over 1024 tokens, else done by gate_up per expert
 //   gate_up  grouped GEMM over experts: x rows of the expert x W_gu[e] (+ bias), with
 //            the SwiGLU epilogue clamp(silu(gate), -limit, limit) * up fused in
 //   down     grouped GEMM over experts: h x W_down[e] (+ bias)
