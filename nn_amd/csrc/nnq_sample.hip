@@ -493,12 +493,34 @@ __device__ void tail_lanes(const float *logits, int64_t n, const uint64_t *sel, 
     }
     const float val = key_val(w);  // lanes < nc: the candidates' values and indices
     const int id = (int)key_idx(w);
+    float p = 0.0f;  // the final softmax over lanes < nc, once known
+    bool have_p = false;
     if (sp.use_top_p && nc > 0) {
-        // apply_top_p_candidates: the smallest prefix (descending order) whose cumulative
-        // probability reaches top_p
+        // apply_top_p_candidates: softmax_candidates, then the smallest prefix (descending
+        // order) whose cumulative probability reaches top_p.  The softmax of that prefix
+        // needs no second pass: its maximum is the same (lane 0 holds the largest value),
+        // so are its exponentials, and its sum is the ordered sum's partial sum at the
+        // prefix's last lane, kept per lane here.
+        const bool in = lane < nc;
+        const float mx = wave_max(in ? val : -INFINITY);
+        const bool mx_ok = fabsf(mx) <= 3.402823466e38f;
+        const float ex = (in && mx_ok) ? expf(val - mx) : 0.0f;
+        float sum = 0.0f, upto = 0.0f;
+        for (int j0 = 0; j0 < nc; j0 += 16)
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), j0 + j));
+                upto = lane == j0 + j ? sum : upto;
+            }
+        const bool uni = !mx_ok || !(fabsf(sum) <= 3.402823466e38f) || sum == 0.0f;
+        const float p1 = in ? (uni ? 1.0f / (float)nc : ex / sum) : 0.0f;
         const float tp = sp.top_p;
-        const int i = walk_lanes(softmax_lanes(val, nc), nc, [tp](float cum) { return cum >= tp; });
+        const int i = walk_lanes(p1, nc, [tp](float cum) { return cum >= tp; });
         nc = i < nc ? i + 1 : nc;
+        const float sum2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(upto), nc - 1));
+        const bool uni2 = !mx_ok || !(fabsf(sum2) <= 3.402823466e38f) || sum2 == 0.0f;
+        p = lane < nc ? (uni2 ? 1.0f / (float)nc : ex / sum2) : 0.0f;
+        have_p = true;
     }
     if (nc == 0) {
         if (lane == 0) argmax_slice_serial(logits, n, token);
@@ -509,8 +531,9 @@ __device__ void tail_lanes(const float *logits, int64_t n, const uint64_t *sel, 
         if (lane == 0) *token = (uint32_t)pick;
         return;
     }
+    if (!have_p) p = softmax_lanes(val, nc);
     const float selector = (float)(sp.seed % 10000ull) / 10000.0f;
-    const int i = walk_lanes(softmax_lanes(val, nc), nc, [selector](float cum) { return selector < cum; });
+    const int i = walk_lanes(p, nc, [selector](float cum) { return selector < cum; });
     const int pick = __builtin_amdgcn_readlane(id, i < nc ? i : nc - 1);
     if (lane == 0) *token = (uint32_t)pick;
 }
