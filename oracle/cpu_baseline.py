@@ -1,13 +1,14 @@
 """CPU baseline of the quantized-linear path, as the reference runs it: block decode
-to f32, then an f32 sgemm (crates/nn-core/src/dyn_tensor/ops/matmul.rs:18-52).
+to f32, then an f32 product (crates/nn-core/src/layers/quantized/linear.rs:366-400 ->
+crates/nn-core/src/dyn_tensor/ops/matmul.rs:18-52).
 
 Benchmark infrastructure: bench.py's cpu_baseline leg and the tests that check it
-load this module; no product code does.  The decoders are the oracle's own, built at
--O3 (libcpu_baseline.so), run over block ranges on a pool of threads (ctypes releases
-the GIL, identical values); the f32 GEMM is numpy's BLAS (OpenBLAS), a faster stand-in
-for the reference's matrixmultiply, with its thread count set through threadpoolctl.
-Results agree with the oracle to f32 rounding only, so this is a speed baseline, never
-a parity reference.
+load this module; no product code does.  libcpu_baseline.so (cpu_baseline.c) holds the
+oracle's own decoders built at -O3 and run over block ranges under OpenMP, and a
+cache-blocked f32 product (x . W^T) with the columns split over OpenMP threads.  The
+MoE's products (x . W with W stored [in, out]) use numpy's BLAS, its thread count set
+through threadpoolctl.  Decoded values are bit-identical to the oracle's; products agree
+with it to f32 rounding only, so this is a speed baseline, never a parity reference.
 """
 from __future__ import annotations
 
@@ -25,6 +26,8 @@ _lib = None
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _sz = ctypes.c_size_t
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
 
 
 def lib():
@@ -33,28 +36,16 @@ def lib():
         if not os.path.exists(_LIB):
             subprocess.run(["make", "-s", "-C", HERE], check=True)
         L = ctypes.CDLL(_LIB)
-        for name in ("orc_dequant_q4_k_gguf", "orc_dequant_q6_k_legacy"):
-            getattr(L, name).argtypes = [_u8p, _sz, _sz, _f32p]
-            getattr(L, name).restype = _sz
-        L.orc_mxfp4_dequantize.argtypes = [_u8p, _u8p, _sz, _sz, _f32p]
+        for name in ("cb_dequant_q4k", "cb_dequant_q6k"):
+            getattr(L, name).argtypes = [_u8p, _sz, _f32p, _int]
+        L.cb_dequant_mxfp4.argtypes = [_u8p, _u8p, _sz, _f32p, _int]
+        L.cb_matmul_xwt.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _f32p, _int]
+        L.cb_q4k_qlinear.argtypes = [_u8p, _i64, _i64, _f32p, _i64, _f32p, _f32p, _int]
+        L.cb_argmax.argtypes = [_f32p, _i64]
+        L.cb_argmax.restype = _i64
+        L.cb_max_threads.restype = _int
         _lib = L
     return _lib
-
-
-_pools = {}
-
-
-def _parallel(nblocks, threads, fn):
-    """fn(b0, b1) over [0, nblocks) split into `threads` contiguous ranges."""
-    if threads <= 1 or nblocks < 2 * threads:
-        fn(0, nblocks)
-        return
-    from concurrent.futures import ThreadPoolExecutor
-    pool = _pools.get(threads)
-    if pool is None:
-        pool = _pools[threads] = ThreadPoolExecutor(max_workers=threads)
-    per = -(-nblocks // threads)
-    list(pool.map(lambda b0: fn(b0, min(nblocks, b0 + per)), range(0, nblocks, per)))
 
 
 def _p(a, t):
@@ -96,18 +87,14 @@ def blas_threads(n: int):
 def dequant_q4k(wb, count, threads=1, out=None):
     wb = np.ascontiguousarray(wb, np.uint8)
     out = np.empty(count, np.float32) if out is None else out
-    L = lib()
-    _parallel(count // 256, threads, lambda b0, b1: L.orc_dequant_q4_k_gguf(
-        _p(wb[b0 * 144:], _u8p), (b1 - b0) * 144, (b1 - b0) * 256, _p(out[b0 * 256:], _f32p)))
+    lib().cb_dequant_q4k(_p(wb, _u8p), count // 256, _p(out, _f32p), threads)
     return out
 
 
 def dequant_q6k(wb, count, threads=1, out=None):
     wb = np.ascontiguousarray(wb, np.uint8)
     out = np.empty(count, np.float32) if out is None else out
-    L = lib()
-    _parallel(count // 256, threads, lambda b0, b1: L.orc_dequant_q6_k_legacy(
-        _p(wb[b0 * 210:], _u8p), (b1 - b0) * 210, (b1 - b0) * 256, _p(out[b0 * 256:], _f32p)))
+    lib().cb_dequant_q6k(_p(wb, _u8p), count // 256, _p(out, _f32p), threads)
     return out
 
 
@@ -115,15 +102,30 @@ def dequant_mxfp4(packed, scales, count, threads=1, out=None):
     packed = np.ascontiguousarray(packed, np.uint8)
     scales = np.ascontiguousarray(scales, np.uint8)
     out = np.empty(count, np.float32) if out is None else out
-    L = lib()
-    _parallel(count // 32, threads, lambda b0, b1: L.orc_mxfp4_dequantize(
-        _p(packed[b0 * 16:], _u8p), _p(scales[b0:], _u8p), b1 - b0, (b1 - b0) * 32, _p(out[b0 * 32:], _f32p)))
+    lib().cb_dequant_mxfp4(_p(packed, _u8p), _p(scales, _u8p), count // 32, _p(out, _f32p), threads)
+    return out
+
+
+def matmul_xwt(x, w, threads=1, out=None):
+    """y = x . w^T in f32 (x [m, k], w [n, k], both C-contiguous f32)."""
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.float32) if out is None else out
+    lib().cb_matmul_xwt(_p(x, _f32p), m, _p(w, _f32p), n, k, _p(out, _f32p), threads)
+    return out
+
+
+def q4k_qlinear(wb, n, k, x, wbuf, out, threads=1):
+    """QLinear::forward with a Q4_K weight: decode all of W into wbuf (allocated once by
+    the caller), then out = x . W^T."""
+    lib().cb_q4k_qlinear(_p(wb, _u8p), n, k, _p(x, _f32p), x.shape[0], _p(wbuf, _f32p), _p(out, _f32p), threads)
     return out
 
 
 def argmax(v) -> int:
     """First index of the maximum (argreduce.rs:105-118; the inputs here are finite)."""
-    return int(np.argmax(v))
+    v = np.ascontiguousarray(v, np.float32).ravel()
+    return int(lib().cb_argmax(_p(v, _f32p), v.size))
 
 
 def moe_forward(x, logits, top_k, gp, gs, gb, dp, ds, db, inter, limit=7.0, faithful=False, expert_limit=0,

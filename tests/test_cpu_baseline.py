@@ -46,3 +46,27 @@ def test_moe_matches_oracle(O, faithful):
         _, ran1 = CB.moe_forward(x, lg, K, gp, gs, gb, dp, ds, db, I, faithful=faithful, expert_limit=1)
     assert ran >= 1 and ran1 == 1
     assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 37, 300), (5, 70, 1040), (8, 130, 2048)])
+def test_matmul_and_qlinear_match_oracle(O, m, n, k):
+    """The blocked f32 product (any m, n, k: register-block and vector tails) equals an f64
+    product to f32 rounding, at one and several threads; QLinear::forward's flow (decode,
+    then the product) matches the oracle's decode followed by the same product."""
+    rng = np.random.default_rng(m * 1000 + n)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    w = rng.standard_normal((n, k), dtype=np.float32)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    for th in (1, 3):
+        y = CB.matmul_xwt(x, w, th)
+        assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max() * np.sqrt(k)
+    if k % 256 == 0:
+        import nn_amd
+        wb = O.quantize_q4_k(nn_amd.synth_normal(7, 1, (n, k), 0.02))
+        wbuf = np.empty(n * k, np.float32)
+        y = np.empty((m, n), np.float32)
+        CB.q4k_qlinear(wb, n, k, x, wbuf, y, 2)
+        assert np.array_equal(wbuf.view(np.uint32), O.dequant_q4_k(wb, n * k).view(np.uint32))
+        ref = x.astype(np.float64) @ wbuf.reshape(n, k).astype(np.float64).T
+        assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max() * np.sqrt(k)
+        assert CB.argmax(y[0]) == int(np.argmax(y[0]))
