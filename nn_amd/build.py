@@ -23,8 +23,8 @@ ARCH = "gfx950"
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 
-HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_gemm_blk.hip", "nnq_moe.hip",
-               "nnq_sample.hip"]
+HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_gemm_wide.hip", "nnq_gemm_blk.hip",
+               "nnq_moe.hip", "nnq_sample.hip"]
 # per-file device flags: the block-scaled GEMM's MFMAs write their partials to VGPRs (the
 # FMAs that scale them read VGPRs only; with the default accumulator registers every
 # partial costs four extra register reads)

@@ -470,6 +470,14 @@ int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm) {
     return best_ks;
 }
 
+int launch_gemm_finalize(const float *ys, int ks, const float *bias, void *y, int y_bf16, int64_t m, int64_t n,
+                         void *stream) {
+    const int64_t cnt = m * n / 4;
+    hipLaunchKernelGGL(gemm_finalize_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, (hipStream_t)stream, ys,
+                       ks, bias, y, y_bf16, m, n);
+    return (int)hipGetLastError();
+}
+
 int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     int bn = 0, bm = 0;
     const int ksplit = gemm_ring_plan(a, &bn, &bm);

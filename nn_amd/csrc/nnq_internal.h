@@ -146,6 +146,16 @@ struct GemmScratch {
 // the kernel; bn and bm, when given, receive the tile width and height), and its launch
 int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm = nullptr);
 int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream);
+// wide-wave-tile kernel (nnq_gemm_wide.hip; bf16 activations, more than 128 rows): its
+// column tiles per workgroup (0: the shape does not fit) and K split, its scratch (the
+// fragment-major staged activation in xh, min-term operands in xs, rowback, split slabs;
+// s null: sizes only) and its launch (staging, kernel, and with a K split the slab sum)
+int gemm_wide_plan(const GemmArgs &a, int *ks);
+size_t gemm_wide_scratch(const GemmArgs &a, GemmScratch *s, uint8_t *base);
+int launch_gemm_wide(const GemmArgs &a, const GemmScratch &sc, void *stream);
+// split-K result: ks f32 slabs [m][n] summed in order, plus the bias, to f32 or bf16 (n % 4 == 0)
+int launch_gemm_finalize(const float *ys, int ks, const float *bias, void *y, int y_bf16, int64_t m, int64_t n,
+                         void *stream);
 // the staging scratch of a GEMM call (base null: sizes only) and the staging kernel
 GemmScratch gemm_carve(void *base, const GemmArgs &a, size_t *bytes);
 int launch_gemm_prep(const GemmArgs &a, const GemmScratch &sc, void *stream);
