@@ -342,29 +342,31 @@ __global__ __launch_bounds__(NTH, 1) void gemm_q4k_wide_kernel(WideArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// Activation staging for the wide kernel: one wave per row, the whole row loaded at once
-// into registers (NG groups of 8 per lane, K <= 512 NG), its max found by wave reductions,
-// then written as f16 of x * 2^s_row (exact for bf16 input) into the fragment-major plane:
-// fragment (row group g, step s) is 1 KB, row r's 64 bytes at 64 r, so that the 16 bytes of
-// MFMA lane 16 G + r, x[16 g + r][32 s + 8 G .. + 7], sit at 64 r + 16 G (a row's stores are
-// 64-byte segments).  The min-term operands: per (row group, super-block) one fragment in
+// Activation staging for the wide kernel: one workgroup of 512 threads per row, the row
+// loaded at once into registers (NG groups of 8 per thread, K <= 4096 NG), its max found by
+// wave reductions and one exchange through LDS, then written as f16 of x * 2^s_row (exact
+// for bf16 input) into the fragment-major plane: fragment (row group g, step s) is 1 KB, row
+// r's 64 bytes at 64 r, so that the 16 bytes of MFMA lane 16 G + r,
+// x[16 g + r][32 s + 8 G .. + 7], sit at 64 r + 16 G (four consecutive threads store one
+// 64-byte segment).  The min-term operands: per (row group, super-block) one fragment in
 // the same order whose lane 16 G + r holds the f16 hi (G even) or lo (G odd) parts of
 // -2^-8 * sum(x * 2^s_row) over the row's eight 32-element sub-blocks.  Rows past M
 // (padding to 16) are written as zeros.
 // ---------------------------------------------------------------------------------
 template <int NG>
-__global__ __launch_bounds__(64) void gemm_stage_wide_kernel(const uint16_t *x, int64_t m, int64_t k, u32x4 *xa,
-                                                             u32x4 *xs, float *rowback) {
+__global__ __launch_bounds__(512) void gemm_stage_wide_kernel(const uint16_t *x, int64_t m, int64_t k, u32x4 *xa,
+                                                              u32x4 *xs, float *rowback) {
     const int64_t row = blockIdx.x;
-    const int lane = threadIdx.x;
-    __shared__ float sums[NG * 16];  // the row's sub-block sums (k / 32 <= 16 NG)
+    const int tid = threadIdx.x, lane = tid & 63, wvi = tid >> 6;
+    __shared__ float wred[8];
+    __shared__ float sums[NG * 128];  // the row's sub-block sums (k / 32 <= 128 NG)
     const bool valid = row < m;
     const int64_t ng = k / 8, nks = k / 32;
     const int g = (int)(row >> 4), r = (int)(row & 15);
     u32x4 w[NG];
 #pragma unroll
     for (int j = 0; j < NG; j++) {
-        const int64_t c = lane + 64 * j;
+        const int64_t c = tid + 512 * j;
         w[j] = (valid && c < ng) ? *reinterpret_cast<const u32x4 *>(x + row * k + 8 * c) : u32x4{0u, 0u, 0u, 0u};
     }
     float amax = 0.0f;
@@ -374,13 +376,17 @@ __global__ __launch_bounds__(64) void gemm_stage_wide_kernel(const uint16_t *x, 
         for (int i = 0; i < 4; i++)
             amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(w[j][i] & 0xFFFFu)), fabsf(bf16_to_f32(w[j][i] >> 16))));
     amax = wave_max(amax);
+    if (lane == 0) wred[wvi] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, wred[i]);
     float s, back;
     f16_prescale(amax, s, back);
-    if (lane == 0) rowback[row] = valid ? back : 1.0f;
+    if (tid == 0) rowback[row] = valid ? back : 1.0f;
 #pragma unroll
     for (int j = 0; j < NG; j++) {
-        const int64_t c = lane + 64 * j;  // chunk of 8: step c / 4, lane group c % 4
-        if (j * 64 < ng) {                // wave-uniform: whole groups of 64 chunks (k % 512 == 0 or a tail)
+        const int64_t c = tid + 512 * j;  // chunk of 8: step c / 4, lane group c % 4
+        if (j * 512 < ng) {               // wave-uniform: whole groups of 64 chunks (k % 512 == 0)
             uint32_t h[4];
             float sum = 0.0f;
 #pragma unroll
@@ -401,7 +407,7 @@ __global__ __launch_bounds__(64) void gemm_stage_wide_kernel(const uint16_t *x, 
     __syncthreads();
     // min-term fragments: lane group G of super-block b: part G & 1 of -2^-8 * sum, 8 sub-blocks
     const int64_t nsb = k / 256;
-    for (int64_t i = lane; i < nsb * 4; i += 64) {
+    for (int64_t i = tid; i < nsb * 4; i += 512) {
         const int64_t b = i >> 2;
         const int G = (int)(i & 3);
         uint32_t h[4];
@@ -423,14 +429,14 @@ __global__ __launch_bounds__(64) void gemm_stage_wide_kernel(const uint16_t *x, 
 }  // namespace
 
 // The wide kernel's shape rules: bf16 activations, more than 128 rows (smaller batches are
-// HBM-bound and take the ring kernel), a 16-byte aligned output, K <= 512 * 24 (the staging
-// keeps the row in one wave's registers and its sub-block sums in LDS), and enough workgroups to fill
+// HBM-bound and take the ring kernel), a 16-byte aligned output, K <= 4096 * 3 (the staging
+// keeps the row in one workgroup's registers and its sub-block sums in LDS), and enough workgroups to fill
 // the CUs: 96-column tiles when they give at least 192 workgroups, else 64-column tiles
 // (an even super-block count) when they give 128 with the K range split in two below 256.
 // Returns the column tiles per workgroup (6 or 4; 0: the ring kernel takes the shape) and
 // the K split.
 int gemm_wide_plan(const GemmArgs &a, int *ks) {
-    if (a.blk || !a.x_bf16 || a.m <= 128 || a.k > 512 * 24 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
+    if (a.blk || !a.x_bf16 || a.m <= 128 || a.k > 4096 * 3 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
     const int64_t nrt = (a.m + BM - 1) / BM;
     if (a.ntile % 6 == 0 && nrt * (a.ntile / 6) >= 192) {
         if (ks) *ks = 1;
@@ -495,10 +501,10 @@ int launch_gemm_wide(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     auto xs = reinterpret_cast<u32x4 *>(sc.xs);
     auto xin = reinterpret_cast<const uint16_t *>(a.x);
     const dim3 sg((unsigned)(nrg * 16));
-    if (a.k <= 512 * 8)
-        hipLaunchKernelGGL(gemm_stage_wide_kernel<8>, sg, dim3(64), 0, st, xin, a.m, a.k, xa, xs, sc.rowback);
+    if (a.k <= 4096)
+        hipLaunchKernelGGL(gemm_stage_wide_kernel<1>, sg, dim3(512), 0, st, xin, a.m, a.k, xa, xs, sc.rowback);
     else
-        hipLaunchKernelGGL(gemm_stage_wide_kernel<24>, sg, dim3(64), 0, st, xin, a.m, a.k, xa, xs, sc.rowback);
+        hipLaunchKernelGGL(gemm_stage_wide_kernel<3>, sg, dim3(512), 0, st, xin, a.m, a.k, xa, xs, sc.rowback);
     int e = (int)hipGetLastError();
     if (e) return e;
     WideArgs w{};
