@@ -441,8 +441,8 @@ int launch_rk(const GemmArgs &a, const GemmScratch &sc, hipStream_t st) {
 // resident workgroups with shallower rings measured 5-25% slower at M = 16 to 64.)
 // Returns the K split, or 0 when the shape does not fit.
 int gemm_ring_plan(const GemmArgs &a, int *bn, int *bm) {
-    // (the output tile is written in 16-byte chunks)
-    if (a.m < 1 || a.nblk < 1 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
+    // (the output tile is written in 16-byte chunks of whole rows: no partial last tile)
+    if (a.m < 1 || a.nblk < 1 || a.n != a.ntile * 16 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
     const int npl = a.x_bf16 ? 1 : 2;  // f32 activations: hi and lo planes, each a full pass
     const int rows = a.m <= 32 ? 32 : (a.m <= 64 ? 64 : 128);
     const int64_t ncols = a.ntile * 16, nrt = (a.m + rows - 1) / rows;

@@ -342,6 +342,198 @@ __global__ __launch_bounds__(NTH, 1) void gemm_q4k_wide_kernel(WideArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
+// Skinny GEMM (5 .. 32 rows, bf16 activations): the weight is streamed once, like a decode
+// GEMV.  One workgroup per R consecutive weight tiles (16 columns each); its W waves split
+// K by units of 256 (unit u to wave u % W).  Each wave runs all MT row tiles of the batch
+// against its R tiles: it dequantizes its B fragments in registers straight from the tile16
+// bytes (the wide kernel's exact sc * q operands, here without any LDS or barrier in the
+// loop), shares every A fragment (the same staged activation planes) across the R tiles,
+// and keeps the d-scaled totals and the min term as the wide kernel does.  The raw bytes of
+// a wave's next D units are loaded while it computes the current one.  At the end the waves'
+// totals meet in LDS and the workgroup writes its M x 16 R outputs.
+// ---------------------------------------------------------------------------------
+template <int R, int MT, int W>
+struct Skinny {
+    static constexpr int LDS = W * R * MT * 1024;  // every wave's totals, f32
+};
+
+// D = 0: a wave's next unit's raw bytes load during the current one and each step loads its
+// A fragments; D = 1: the burst schedule (A fragments one unit ahead, raw bytes two)
+template <int R, int MT, int W, int D>
+__global__ __launch_bounds__(W * 64) void gemm_q4k_skinny_kernel(WideArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = lane >> 4, c16 = lane & 15;
+    const int nblk = a.nblk;
+    const int t0 = (int)blockIdx.x * R;  // the plan keeps ntile % R == 0
+
+    __amdgpu_buffer_rsrc_t ra[MT], rxs[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int rg = min(mt, a.nrg - 1);
+        ra[mt] = rsrc(a.xa + (size_t)rg * nblk * 8 * 64, (int64_t)nblk * 8 * 1024);
+        rxs[mt] = rsrc(a.xs + (size_t)rg * nblk * 64, (int64_t)nblk * 1024);
+    }
+    const int loff = (c16 * 4 + G) * 16;  // lane (G, r) of a fragment: row r's 16 bytes G
+    const __amdgpu_buffer_rsrc_t rq = rsrc(a.qs + (size_t)t0 * nblk * 2048, (int64_t)R * nblk * 2048);
+    const __amdgpu_buffer_rsrc_t rh = rsrc(a.hdr + (size_t)t0 * nblk * 256, (int64_t)R * nblk * 256);
+    const __amdgpu_buffer_rsrc_t rx = rsrc(a.aux + (size_t)t0 * nblk * 512, (int64_t)R * nblk * 512);
+    // consumer lane (G, r) of group p takes bytes 8G .. 8G + 7 of row r's group: plane G >> 1,
+    // chunk 16 p + r, half G & 1
+    const int qoff = (G >> 1) * 1024 + c16 * 16 + 8 * (G & 1), hoff = c16 * 16;
+    const int xoff = (lane >> 5) * 256 + c16 * 16;
+    const float *srow = reinterpret_cast<const float *>(a.aux + (size_t)a.ntile * nblk * 512);
+    float f1[R];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        f1[r] = __uint_as_float(((__float_as_uint(srow[(size_t)(t0 + r) * 16 + c16]) >> 23) + 16u) << 23);
+
+    struct Raw {
+        u32x2 q[R][4];
+        u32x4 h[R], x[R];
+    };
+    auto load_raw = [&](int u, Raw &w) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+#pragma unroll
+            for (int p = 0; p < 4; p++) w.q[r][p] = bload2(rq, qoff + 256 * p, (r * nblk + u) * 2048);
+            w.h[r] = bload4(rh, hoff, (r * nblk + u) * 256);
+            w.x[r] = bload4(rx, xoff, (r * nblk + u) * 512);
+        }
+    };
+
+    floatx4 tot[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) tot[r][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // the unit body: unit u from ring slot `cur`; with apre, its A fragments were loaded
+    // one unit ahead (ap[step][mt]), else each step loads its own
+    auto unit = [&](int u, const Raw &cur, const u32x4 (*apre)[MT]) {
+        u32x4 xsf[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) xsf[mt] = bload4(rxs[mt], loff, u * 1024);
+        // f16 (sc_j, sc_j+1 / 16) per tile and group
+        uint32_t sw[R][4];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const u32x4 h = cur.h[r];
+            const uint32_t sc03 = h[1] & 0x3F3F3F3Fu;
+            const uint32_t sc47 = (h[3] & 0x0F0F0F0Fu) | ((h[1] >> 2) & 0x30303030u);
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const uint32_t pair = ((p < 2 ? sc03 : sc47) >> (16 * (p & 1))) & 0xFFFFu;
+                const uint32_t biased = 0x64006400u | (pair & 0xFFu) | ((pair & 0xFF00u) << 8);
+                const half2v sh = (__builtin_bit_cast(half2v, biased) - half2v{(_Float16)1024.0f, (_Float16)1024.0f}) *
+                                  half2v{(_Float16)1.0f, (_Float16)0.0625f};
+                sw[r][p] = __builtin_bit_cast(uint32_t, sh);
+            }
+        }
+        floatx4 part[R][MT];
+        u32x4 af[MT];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int p = s >> 1;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) af[mt] = apre ? apre[s][mt] : bload4(ra[mt], loff, (u * 8 + s) * 1024);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t w0 = cur.q[r][p][0], w1 = cur.q[r][p][1], w0s = w0 >> 8, w1s = w1 >> 8;
+                u32x4 b;
+                if ((s & 1) == 0)
+                    b = u32x4{pk_mul_bcast<0>(w0 & 0x000F000Fu, sw[r][p]), pk_mul_bcast<0>(w0s & 0x000F000Fu, sw[r][p]),
+                              pk_mul_bcast<0>(w1 & 0x000F000Fu, sw[r][p]), pk_mul_bcast<0>(w1s & 0x000F000Fu, sw[r][p])};
+                else
+                    b = u32x4{pk_mul_bcast<1>(w0 & 0x00F000F0u, sw[r][p]), pk_mul_bcast<1>(w0s & 0x00F000F0u, sw[r][p]),
+                              pk_mul_bcast<1>(w1 & 0x00F000F0u, sw[r][p]), pk_mul_bcast<1>(w1s & 0x00F000F0u, sw[r][p])};
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    part[r][mt] = mfma16x16x32_f16(af[mt], b, s == 0 ? floatx4{0.f, 0.f, 0.f, 0.f} : part[r][mt]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float dn = f16_to_f32(cur.h[r][0] & 0xFFFFu) * f1[r];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) tot[r][mt][e] += dn * part[r][mt][e];
+                tot[r][mt] = mfma16x16x32_f16(xsf[mt], cur.x[r], tot[r][mt]);
+            }
+        }
+    };
+    // this wave's units wv, wv + W, ...
+    const int nu = nblk > wv ? (nblk - wv + W - 1) / W : 0;
+    if constexpr (D == 0) {
+        // one unit's raw bytes ahead, A fragments loaded by each step
+        Raw cur, nxt;
+        if (nu > 0) load_raw(wv, cur);
+        for (int i = 0; i < nu; i++) {
+            if (i + 1 < nu) load_raw(wv + (i + 1) * W, nxt);
+            unit(wv + i * W, cur, nullptr);
+            if (i + 1 < nu) cur = nxt;
+        }
+    } else {
+        // Loads in bursts, because the vector memory counter retires loads in issue order:
+        // at the start of unit i come all A fragments of unit i + 1, then the raw bytes of
+        // unit i + 2, so every wait inside unit i is on loads issued a unit or more before
+        // (the HBM-latency raw loads never hold up an A fragment needed soon).
+        Raw rw[3];
+        u32x4 ab[2][8][MT];
+        auto load_a = [&](int i, u32x4 (*dst)[MT]) {
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) dst[s][mt] = bload4(ra[mt], loff, ((wv + i * W) * 8 + s) * 1024);
+        };
+        if (nu > 0) load_raw(wv, rw[0]);
+        if (nu > 0) load_a(0, ab[0]);
+        if (nu > 1) load_raw(wv + W, rw[1]);
+        for (int i0 = 0; i0 < nu; i0 += 6) {
+#pragma unroll
+            for (int j = 0; j < 6; j++) {
+                const int i = i0 + j;
+                if (i >= nu) break;
+                if (i + 1 < nu) load_a(i + 1, ab[(j + 1) & 1]);
+                if (i + 2 < nu) load_raw(wv + (i + 2) * W, rw[(j + 2) % 3]);
+                unit(wv + i * W, rw[j % 3], ab[j & 1]);
+            }
+        }
+    }
+    // the waves' totals meet in LDS: [W][R][MT][64 lanes] floatx4
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            *reinterpret_cast<floatx4 *>(smem + ((((wv * R + r) * MT + mt) * 64) + lane) * 16) = tot[r][mt];
+    __syncthreads();
+    // thread (r, mt, lane) for the first R * MT * 64 threads: sum over the waves, epilogue
+    for (int i = tid; i < R * MT * 64; i += W * 64) {
+        const int l = i & 63, rm = i >> 6, r = rm / MT, mt = rm % MT;
+        floatx4 v = *reinterpret_cast<const floatx4 *>(smem + (rm * 64 + l) * 16);
+#pragma unroll
+        for (int w2 = 1; w2 < W; w2++) v += *reinterpret_cast<const floatx4 *>(smem + (((w2 * R * MT) + rm) * 64 + l) * 16);
+        const int lg = l >> 4, col = (t0 + r) * 16 + (l & 15);
+        if (col >= a.n) continue;  // the padded rows of a last, partial weight tile
+        const float f2 = __uint_as_float((262u - (__float_as_uint(srow[col]) >> 23)) << 23);
+        const float bc = a.bias ? a.bias[col] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int row = mt * 16 + 4 * lg + e;
+            if (row < a.m) {
+                const float y = v[e] * f2 * a.rowback[row] + bc;
+                if (a.y_bf16)
+                    reinterpret_cast<uint16_t *>(a.y)[(int64_t)row * a.n + col] = (uint16_t)f32_to_bf16_bits(y);
+                else
+                    reinterpret_cast<float *>(a.y)[(int64_t)row * a.n + col] = y;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Activation staging for the wide kernel: one workgroup of 512 threads per row, the row
 // loaded at once into registers (NG groups of 8 per thread, K <= 4096 NG), its max found by
 // wave reductions and one exchange through LDS, then written as f16 of x * 2^s_row (exact
@@ -429,14 +621,17 @@ __global__ __launch_bounds__(512) void gemm_stage_wide_kernel(const uint16_t *x,
 }  // namespace
 
 // The wide kernel's shape rules: bf16 activations, more than 128 rows (smaller batches are
-// HBM-bound and take the ring kernel), a 16-byte aligned output, K <= 4096 * 3 (the staging
+// HBM-bound and take the other kernels), whole 16-row weight tiles and a 16-byte aligned
+// output (the epilogue writes 16-byte row chunks), K <= 4096 * 3 (the staging
 // keeps the row in one workgroup's registers and its sub-block sums in LDS), and enough workgroups to fill
 // the CUs: 96-column tiles when they give at least 192 workgroups, else 64-column tiles
 // (an even super-block count) when they give 128 with the K range split in two below 256.
 // Returns the column tiles per workgroup (6 or 4; 0: the ring kernel takes the shape) and
 // the K split.
 int gemm_wide_plan(const GemmArgs &a, int *ks) {
-    if (a.blk || !a.x_bf16 || a.m <= 128 || a.k > 4096 * 3 || (reinterpret_cast<uintptr_t>(a.y) & 15)) return 0;
+    if (a.blk || !a.x_bf16 || a.m <= 128 || a.k > 4096 * 3 || a.n != a.ntile * 16 ||
+        (reinterpret_cast<uintptr_t>(a.y) & 15))
+        return 0;
     const int64_t nrt = (a.m + BM - 1) / BM;
     if (a.ntile % 6 == 0 && nrt * (a.ntile / 6) >= 192) {
         if (ks) *ks = 1;
@@ -453,11 +648,27 @@ int gemm_wide_plan(const GemmArgs &a, int *ks) {
     return 0;
 }
 
+// The skinny kernel's shape rules: bf16 activations, 5 to 32 rows, K <= 4096 * 3 (the
+// staging), whole groups of R tiles.  R = 3 tiles per workgroup when that gives at least
+// 192 workgroups, else 1; with one tile per workgroup only up to 16 rows (every workgroup
+// reads the whole staged activation: from 17 rows on, and at 48 and 64 rows for either R,
+// the ring kernel measured as fast or faster on MI355X).  W = 8 waves over K (measured
+// against 4).  Returns 1 when the kernel takes the shape.
+int gemm_skinny_plan(const GemmArgs &a, int *R, int *W) {
+    if (a.blk || !a.x_bf16 || a.m <= 4 || a.m > 32 || a.k > 4096 * 3) return 0;
+    const int mt = (int)((a.m + 15) / 16);
+    const int r = (a.ntile % 3 == 0 && a.ntile / 3 >= 192) ? 3 : 1;
+    if (mt == 2 && r == 1) return 0;  // 17 to 32 rows over one tile per workgroup: the ring kernel is as fast
+    if (R) *R = r;
+    if (W) *W = 8;
+    return 1;
+}
+
 size_t gemm_wide_scratch(const GemmArgs &a, GemmScratch *s, uint8_t *base) {
     auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
     const int64_t nrg = (a.m + 15) / 16;
     int ks = 1;
-    gemm_wide_plan(a, &ks);
+    if (!gemm_skinny_plan(a, nullptr, nullptr)) gemm_wide_plan(a, &ks);
     size_t off = 0;
     if (s) s->xh = reinterpret_cast<uint16_t *>(base + off);
     off += al((size_t)nrg * 16 * a.k * 2);
@@ -491,10 +702,38 @@ static int launch_wide_nt(const WideArgs &w, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
+template <int R, int MT, int W>
+static int launch_skinny_cfg(const WideArgs &w, hipStream_t st) {
+    using C = Skinny<R, MT, W>;
+    constexpr int D = (R == 1 && MT <= 2) ? 1 : 0;  // the burst schedule where the registers allow
+    static bool attr_set = false;  // idempotent attribute write; races only repeat it
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_skinny_kernel<R, MT, W, D>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
+        if (e != hipSuccess) return (int)e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((gemm_q4k_skinny_kernel<R, MT, W, D>), dim3((unsigned)(w.ntile / R)), dim3(W * 64), C::LDS, st,
+                       w);
+    return (int)hipGetLastError();
+}
+
+template <int R, int W>
+static int launch_skinny_r(const WideArgs &w, hipStream_t st) {
+    switch ((w.m + 15) / 16) {
+        case 1: return launch_skinny_cfg<R, 1, W>(w, st);
+        case 2: return launch_skinny_cfg<R, 2, W>(w, st);
+        case 3: if constexpr (R == 1) return launch_skinny_cfg<R, 3, W>(w, st); break;
+        case 4: if constexpr (R == 1) return launch_skinny_cfg<R, 4, W>(w, st); break;
+    }
+    return (int)hipErrorInvalidValue;
+}
+
 int launch_gemm_wide(const GemmArgs &a, const GemmScratch &sc, void *stream) {
-    int ks = 0;
-    const int nt = gemm_wide_plan(a, &ks);
-    if (!nt || sc.ksplit != ks || (ks > 1 && !sc.ysplit)) return (int)hipErrorInvalidValue;
+    int ks = 0, sr = 0, sw = 0;
+    const bool skinny = gemm_skinny_plan(a, &sr, &sw);
+    const int nt = skinny ? 0 : gemm_wide_plan(a, &ks);
+    if (!skinny && (!nt || sc.ksplit != ks || (ks > 1 && !sc.ysplit))) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const int64_t nrg = (a.m + 15) / 16;
     auto xa = reinterpret_cast<u32x4 *>(sc.xh);
@@ -522,8 +761,11 @@ int launch_gemm_wide(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     w.n = a.n;
     w.nblk = (int)a.nblk;
     w.ntile = (int)a.ntile;
-    w.ks = ks;
+    w.ks = skinny ? 1 : ks;
     w.nrg = (int)nrg;
+    if (skinny) {
+        return sr == 3 ? launch_skinny_r<3, 8>(w, st) : launch_skinny_r<1, 8>(w, st);
+    }
     e = nt == 6 ? launch_wide_nt<6>(w, st) : launch_wide_nt<4>(w, st);
     if (e || ks == 1) return e;
     return launch_gemm_finalize(sc.ysplit, ks, a.bias, a.y, a.y_bf16, a.m, a.n, stream);

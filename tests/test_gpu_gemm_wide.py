@@ -1,10 +1,11 @@
-"""GPU parity for the wide-wave-tile Q4_K prefill GEMM (bf16 activations, more than 128
-rows; nnq_gemm_wide.hip), against the oracle's bit-exact decode followed by an f64
-product (tolerances as in test_gpu_linear).  Shapes cover both column-tile widths (96
-columns, and 64 with the K range split in two), ragged row tiles (the last 256-row tile
-partly past M, a row group partly past M), random block bytes (arbitrary finite d / dmin
-/ scales, with d = 0 super-blocks), a single-row-tile batch, bias, f32 and bf16 outputs,
-and repeated calls agreeing bit for bit."""
+"""GPU parity for the Q4_K prefill GEMMs of nnq_gemm_wide.hip (bf16 activations): the
+wide-wave-tile kernel (more than 128 rows) and the skinny kernel (5 to 64 rows), against
+the oracle's bit-exact decode followed by an f64 product (tolerances as in
+test_gpu_linear).  Shapes cover both wide column-tile widths (96 columns, and 64 with the
+K range split in two), the skinny kernel's 1 and 3 tiles per workgroup, 4 and 8 waves
+over K and 1 to 4 row tiles, ragged row tiles (the last tile partly past M, a row group
+partly past M), random block bytes (arbitrary finite d / dmin / scales, with d = 0
+super-blocks), bias, f32 and bf16 outputs, and repeated calls agreeing bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -24,7 +25,8 @@ def dev():
 
 
 @pytest.mark.parametrize("m,n,k", [(300, 12288, 1024), (512, 12288, 512), (129, 4096, 2048), (700, 4096, 1536),
-                                   (257, 6144, 1024), (1000, 8192, 512)])
+                                   (257, 6144, 1024), (1000, 8192, 512), (5, 12288, 1024), (32, 12288, 512),
+                                   (48, 12288, 1024), (64, 4096, 8192), (17, 3072, 12288), (63, 768, 2048), (40, 1528, 1024), (300, 1528, 512)])
 @pytest.mark.parametrize("legacy", [False, True])
 def test_wide_random_blocks(O, dev, m, n, k, legacy):
     import nn_amd
