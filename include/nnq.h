@@ -21,7 +21,12 @@
  *    their capture sequence, so a graph may be replayed on any stream while eager
  *    calls run elsewhere.  Two replays of one graph that overlap in time share that
  *    graph's workspace and must be ordered by the caller.  A capture's workspace is
- *    kept until the process ends; nnq_release_workspace frees a stream's eager one.
+ *    kept until nnq_release_capture_workspaces; nnq_release_workspace frees a
+ *    stream's eager one.
+ *  - Several host threads may call on one stream: a call holds the stream's
+ *    workspace from its first scratch request until its last enqueue, so their
+ *    calls take it one at a time.  (nnq_linear_sample_noalloc's fixed scratch is
+ *    the exception; see there.)
  *  - Weights are row-major W[n, k] (out_features x in_features) with blocks
  *    along k, as QuantizedStorage / QuantizedWeight store them
  *    (crates/nn-core/src/dyn_tensor/quantized.rs:109-172,
@@ -115,6 +120,14 @@ const char *nnq_last_error(void);
  * reference (its CPU path allocates per call); the next call on the stream allocates
  * again. */
 int nnq_release_workspace(void *stream);
+
+/* Free the workspaces of every capture sequence on the current device (calls captured
+ * into HIP graphs keep theirs, since a graph reads it on every replay).  Call it once
+ * every graph that captured library calls on this device has been destroyed, or will
+ * never be replayed again; a replay after it reads freed memory.  Graphs captured
+ * afterwards allocate again.  No counterpart in the reference (it captures no graphs);
+ * it is for callers that capture graphs repeatedly, e.g. one per shape bucket. */
+int nnq_release_capture_workspaces(void);
 
 /* ---- weights ------------------------------------------------------------------ */
 

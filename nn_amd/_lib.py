@@ -62,6 +62,7 @@ SIGNATURES = {
     "nnq_dequant_mxfp4_ocp": (c_int, [c_void_p, c_i64, c_void_p, c_void_p]),
     "nnq_quantize_mxfp4_ocp": (c_int, [c_void_p, c_sz, c_void_p]),
     "nnq_release_workspace": (c_int, [c_void_p]),
+    "nnq_release_capture_workspaces": (c_int, []),
     "nnq_linear_sample_noalloc": (c_int, [c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_i64,
                                           c_void_p, c_void_p, c_void_p]),
     "nnq_gguf_open": (c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),

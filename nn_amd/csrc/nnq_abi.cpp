@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -92,36 +93,73 @@ size_t block_bytes(int fmt) {
 //    device, stream and capture id), allocated with the capture's ban on allocation calls
 //    relaxed for this thread, so the graph holds no allocation nodes.  A graph keeps
 //    reading that buffer whenever and on whatever stream it is replayed, so it is never
-//    shared with eager calls or other captures, and it is kept until the process ends
-//    (the library cannot know when the graph is destroyed).  A buffer outgrown within one
-//    capture is kept as well, since the calls captured before hold it.
+//    shared with eager calls or other captures, and it is kept until
+//    nnq_release_capture_workspaces (the library cannot see when the graph is destroyed).
+//    A buffer outgrown within one capture is kept as well, since the calls captured
+//    before hold it.
 // If the relaxed allocation is refused, the call takes a stream-ordered allocation that
 // becomes nodes of the graph (freed by the graph after the call's work).
-struct Workspace {
+//
+// Stream order alone does not keep two host threads that call on one stream apart: their
+// copies and kernels could interleave on the shared buffer, and a call that grows the
+// workspace would free the buffer that another thread's call holds but has not yet used.
+// So a call holds its stream's lock (recursive: a call may take scratch twice) from its
+// first workspace request until its last enqueue.
+//
+// hipStreamPerThread names a different stream in each host thread, so for that handle the
+// thread is part of the key.
+struct StreamKey {
     int dev;
     hipStream_t st;
+    std::thread::id owner;
+    bool operator==(const StreamKey &o) const { return dev == o.dev && st == o.st && owner == o.owner; }
+};
+struct Workspace {
+    StreamKey key;
     unsigned long long capture;  // 0: eager
     void *p;
     size_t n;
 };
+struct StreamLock {
+    StreamKey key;
+    std::recursive_mutex mu;
+};
+struct Retired {
+    int dev;
+    void *p;
+};
 std::mutex g_ws_mu;
 std::vector<Workspace> g_ws;
-std::vector<void *> g_capture_retired;
+std::vector<Retired> g_capture_retired;
+std::vector<std::unique_ptr<StreamLock>> g_stream_locks;  // never erased: held locks stay valid
 
-hipError_t stream_workspace(hipStream_t st, size_t n, void **out, bool *owned) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
+hipError_t stream_key(hipStream_t st, StreamKey *k) {
+    k->st = st;
+    k->owner = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+    return hipGetDevice(&k->dev);
+}
+
+std::recursive_mutex &stream_lock(const StreamKey &k) {
+    std::lock_guard<std::mutex> g(g_ws_mu);
+    for (auto &l : g_stream_locks)
+        if (l->key == k) return l->mu;
+    g_stream_locks.push_back(std::make_unique<StreamLock>());
+    g_stream_locks.back()->key = k;
+    return g_stream_locks.back()->mu;
+}
+
+hipError_t stream_workspace(const StreamKey &key, size_t n, void **out, bool *owned) {
+    const hipStream_t st = key.st;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     unsigned long long cid = 0;
-    e = hipStreamGetCaptureInfo(st, &cs, &cid);
+    hipError_t e = hipStreamGetCaptureInfo(st, &cs, &cid);
     if (e != hipSuccess) return e;
     const bool capturing = cs != hipStreamCaptureStatusNone;
     if (!capturing) cid = 0;
     std::lock_guard<std::mutex> g(g_ws_mu);
     Workspace *w = nullptr;
     for (auto &x : g_ws)
-        if (x.dev == dev && x.st == st && x.capture == cid) w = &x;
+        if (x.key == key && x.capture == cid) w = &x;
     if (w && w->n >= n) {
         *out = w->p;
         *owned = false;
@@ -140,7 +178,7 @@ hipError_t stream_workspace(hipStream_t st, size_t n, void **out, bool *owned) {
             *owned = true;
             return hipMallocAsync(out, n, st);
         }
-        if (w) g_capture_retired.push_back(w->p);
+        if (w) g_capture_retired.push_back(Retired{key.dev, w->p});
     } else {
         e = hipMallocAsync(&p, sz, st);
         if (e != hipSuccess) return e;
@@ -156,21 +194,23 @@ hipError_t stream_workspace(hipStream_t st, size_t n, void **out, bool *owned) {
         w->p = p;
         w->n = sz;
     } else {
-        g_ws.push_back(Workspace{dev, st, cid, p, sz});
+        g_ws.push_back(Workspace{key, cid, p, sz});
     }
     *out = p;
     *owned = false;
     return hipSuccess;
 }
 
-// frees the eager workspace of `st` on the current device (stream-ordered on st)
+// frees the eager workspace of `st` on the current device (stream-ordered on st), once no
+// call on the stream holds it
 hipError_t release_stream_workspace(hipStream_t st) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    StreamKey key;
+    hipError_t e = stream_key(st, &key);
     if (e != hipSuccess) return e;
+    std::lock_guard<std::recursive_mutex> call(stream_lock(key));
     std::lock_guard<std::mutex> g(g_ws_mu);
     for (size_t i = 0; i < g_ws.size(); i++)
-        if (g_ws[i].dev == dev && g_ws[i].st == st && g_ws[i].capture == 0) {
+        if (g_ws[i].key == key && g_ws[i].capture == 0) {
             e = hipFreeAsync(g_ws[i].p, st);
             g_ws.erase(g_ws.begin() + (ptrdiff_t)i);
             return e;
@@ -178,19 +218,62 @@ hipError_t release_stream_workspace(hipStream_t st) {
     return hipSuccess;
 }
 
+// frees every capture workspace on the current device; the caller guarantees that no
+// graph captured with library calls on this device runs or is replayed afterwards
+hipError_t release_capture_workspaces() {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::vector<void *> victims;
+    {
+        std::lock_guard<std::mutex> g(g_ws_mu);
+        for (size_t i = 0; i < g_ws.size();)
+            if (g_ws[i].key.dev == dev && g_ws[i].capture != 0) {
+                victims.push_back(g_ws[i].p);
+                g_ws.erase(g_ws.begin() + (ptrdiff_t)i);
+            } else {
+                i++;
+            }
+        for (size_t i = 0; i < g_capture_retired.size();)
+            if (g_capture_retired[i].dev == dev) {
+                victims.push_back(g_capture_retired[i].p);
+                g_capture_retired.erase(g_capture_retired.begin() + (ptrdiff_t)i);
+            } else {
+                i++;
+            }
+    }
+    // relaxed for this thread, so that a capture another thread runs is not invalidated
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    hipError_t first = hipSuccess;
+    for (void *p : victims) {
+        e = hipFree(p);
+        if (e != hipSuccess && first == hipSuccess) first = e;
+    }
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    return first;
+}
+
 // Scratch of one call: the stream's workspace (or, under capture when that is too
-// small, a stream-ordered allocation freed after the call's work).  Calls that overlap
-// on one stream cannot happen (stream order), so one call holds the workspace at a time.
+// small, a stream-ordered allocation freed after the call's work).  The first alloc takes
+// the stream's lock, which the Scratch holds until it is destroyed, i.e. after the call
+// has enqueued its work (every entry point declares its Scratch before its launches).
+// Calls from several threads on one stream therefore take the workspace one at a time.
 struct Scratch {
     void *p = nullptr;
     hipStream_t s = nullptr;
     bool owned = false;
+    std::unique_lock<std::recursive_mutex> call;  // released after the destructor's body
     ~Scratch() {
         if (owned && p) (void)hipFreeAsync(p, s);
     }
     hipError_t alloc(size_t n, hipStream_t st) {
         s = st;
-        return stream_workspace(st, n ? n : 16, &p, &owned);
+        StreamKey key;
+        hipError_t e = stream_key(st, &key);
+        if (e != hipSuccess) return e;
+        if (!call.owns_lock()) call = std::unique_lock<std::recursive_mutex>(stream_lock(key));
+        return stream_workspace(key, n ? n : 16, &p, &owned);
     }
 };
 
@@ -232,6 +315,12 @@ const char *nnq_last_error(void) { return g_err.c_str(); }
 int nnq_release_workspace(void *stream) {
     hipError_t e = release_stream_workspace((hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "release workspace");
+    return NNQ_OK;
+}
+
+int nnq_release_capture_workspaces(void) {
+    hipError_t e = release_capture_workspaces();
+    if (e != hipSuccess) return hip_fail(e, "release capture workspaces");
     return NNQ_OK;
 }
 
