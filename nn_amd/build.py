@@ -28,7 +28,12 @@ HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_gemm_wi
 # per-file device flags: the block-scaled GEMM's MFMAs write their partials to VGPRs (the
 # FMAs that scale them read VGPRs only; with the default accumulator registers every
 # partial costs four extra register reads)
-EXTRA_FLAGS = {"nnq_gemm_blk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# The decode GEMVs and the probes take their first arguments preloaded into SGPRs at wave
+# start (gfx950 kernel-argument preload), so a wave's first loads do not wait for the
+# kernel-argument fetch: at 4096x12288 the GEMV is launch- and latency-bound at ~7 us.
+PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
+EXTRA_FLAGS = {"nnq_gemm_blk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "nnq_gemv.hip": PRELOAD,
+               "nnq_probe.hip": PRELOAD}
 HOST_SOURCES = ["nnq_abi.cpp", "nnq_repack.cpp", "nnq_host.cpp", "nnq_gguf.cpp"]
 # measurement probes for bench.py (streaming-read floor, empty launch), a library of their own
 PROBE_SOURCES = ["nnq_probe.hip"]

@@ -705,84 +705,90 @@ __device__ __forceinline__ void stage_q4k(const u32x4 &raw, uint16_t *hi_plane, 
     st.xs_hi = first ? sum_o : sum;
 }
 
-// XM: activation kind, 0 f32, 1 bf16, 2 f32 gate | up pairs (SwiGLU prologue)
-template <int WAVES, int UPW, int R, int XM, int MT>
-__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a) {
+// Buffer resources over one tile's planes: SGPR bases, so a load's address is a lane
+// offset (VGPR) plus a unit offset (SGPR) with no per-load address arithmetic; reads
+// past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gv_rsrc(const void *p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)min(bytes, (int64_t)0x7FFFFFF0), 0x00020000);
+}
+// AUX 2: non-temporal (the weight stream); 0: default (activations, reused from L2)
+template <int AUX>
+__device__ __forceinline__ u32x4 gv_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
+}
+__device__ __forceinline__ u32x2 gv_load2(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+
+// XM: activation kind, 0 f32, 1 bf16, 2 f32 gate | up pairs (SwiGLU prologue).
+// The arguments the first loads need come first as scalars: the build preloads the
+// leading kernel arguments into SGPRs (-amdgpu-kernarg-preload-count), so a wave issues
+// its loads without waiting for the kernel-argument fetch; the rest (outputs, bias,
+// status, argmax) sit in GemvArgs and are fetched while the loads are in flight.
+// One workgroup per 16-row tile (grid = ntile).
+template <int WAVES, int UPW, int XM, int MT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(const uint8_t *qs, const uint8_t *hdr,
+                                                                    const void *x, int units, int mt, GemvArgs a) {
     constexpr bool XB = XM == 1;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tile0 = (int)blockIdx.x * R;  // this workgroup's tiles: tile0 .. tile0 + R - 1
-    // per wave: one buffer per unit of a pass [token, hi/lo][256] f16, each followed
-    // by 64 zero halves that the A operand of the rows without data reads
-    constexpr int kBuf = MT * 512 + 64;
-    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][UPW][kBuf];
-    __shared__ float red[WAVES][R * MT][16];
-    if (lane < 8 * UPW)  // the wave's own pads, read later only by lanes of this wave
-        *reinterpret_cast<u32x4 *>(&xbuf[wv][lane >> 3][MT * 512 + 8 * (lane & 7)]) = u32x4{0u, 0u, 0u, 0u};
+    const int tile = (int)blockIdx.x;
+    const int k = units * 256;             // the host checks k >= 256
+    const int xrow = XM == 2 ? 2 * k : k;  // elements per token row of x
+    constexpr int xe = XB ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t rq = gv_rsrc(qs + (size_t)tile * units * 2048, (int64_t)units * 2048);
+    const __amdgpu_buffer_rsrc_t rh = gv_rsrc(hdr + (size_t)tile * units * 256, (int64_t)units * 256);
+    const __amdgpu_buffer_rsrc_t rx = gv_rsrc(x, (int64_t)mt * xrow * xe);
+    const int l16 = 16 * lane, n16 = 16 * (lane & 15), lx = 4 * lane * xe;
 
     // A-operand rows of lane group G: 4G + 2t + part (token 2 tp + t of MFMA set tp, hi /
     // lo part) over the k-group of sub-block 2G (low nibbles) or 2G + 1 (high nibbles);
     // other rows zero.  Four tokens take two sets of MFMAs over the same B operands.
     static_assert(MT == 1 || MT == 2 || MT == 4, "token rows");
     constexpr int NTP = (MT + 1) / 2;
+    // per wave: one buffer per unit of a pass [token, hi/lo][256] f16, each followed
+    // by 64 zero halves that the A operand of the rows without data reads
+    constexpr int kBuf = MT * 512 + 64;
+    __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][UPW][kBuf];
+    __shared__ float red[WAVES][MT][16];
     const int G = lane >> 4, n = lane & 15, i = n & 3;
-    int aoff[NTP];
-#pragma unroll
-    for (int tp = 0; tp < NTP; tp++) {
-        const bool own = G == (n >> 2) && 2 * tp + (i >> 1) < MT;
-        aoff[tp] = own ? ((2 * tp + (i >> 1)) * 2 + (i & 1)) * 256 + 64 * G : MT * 512;
-    }
-    const int mt = (int)a.m;  // tokens of the call (MT = 4 holds 3 or 4; the rows past mt are zero)
 
-    const int units = (int)a.nblk, k = (int)a.k, ntile = (int)a.ntile;
-    const uint8_t *qbase[R], *hbase[R];
+    float acc1[MT], acc2[MT];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int tile = min(tile0 + r, ntile - 1);  // a tail tile re-reads the last one
-        qbase[r] = a.qs + (size_t)tile * units * 2048 + 16 * lane;
-        hbase[r] = a.hdr + (size_t)tile * units * 256 + 16 * n;
-    }
-    constexpr int xe = XB ? 2 : 4;
-    const int xrow = XM == 2 ? 2 * k : k;  // elements per token row of x
-    const uint8_t *xbase = reinterpret_cast<const uint8_t *>(a.x) + 4 * lane * xe;
-    float acc1[R][MT], acc2[R][MT];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int t = 0; t < MT; t++) acc1[r][t] = acc2[r][t] = 0.f;
+    for (int t = 0; t < MT; t++) acc1[t] = acc2[t] = 0.f;
     int ub0 = 0;
-    do {  // passes over K (units >= 1: the host checks k >= 256)
+    do {  // passes over K
         // activation slices first (L2 hits), then the weights of every unit of the pass
         u32x4 xr[UPW][MT], xu[XM == 2 ? UPW : 1][MT];
-        UnitQ4K w[UPW][R];
+        UnitQ4K w[UPW];
+        int uo[UPW];
+#pragma unroll
+        for (int j = 0; j < UPW; j++) uo[j] = min(ub0 + wv + j * WAVES, units - 1);
 #pragma unroll
         for (int j = 0; j < UPW; j++) {
-            const uint32_t u = (uint32_t)min(ub0 + wv + j * WAVES, units - 1);
 #pragma unroll
             for (int t = 0; t < MT; t++) {
                 const int tr = t < mt ? t : 0;  // rows past the batch read row 0, staged as zeros
-                const uint8_t *p = xbase + (uint32_t)(tr * xrow + (int)u * 256) * (uint32_t)xe;
+                const int so = (tr * xrow + uo[j] * 256) * xe;
                 if (XB) {
-                    const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+                    const u32x2 w2 = gv_load2(rx, lx, so);
                     xr[j][t] = u32x4{w2[0], w2[1], 0u, 0u};
                 } else {
-                    xr[j][t] = *reinterpret_cast<const u32x4 *>(p);
+                    xr[j][t] = gv_load4<0>(rx, lx, so);
                 }
-                if constexpr (XM == 2) xu[j][t] = *reinterpret_cast<const u32x4 *>(p + (size_t)k * 4);
+                if constexpr (XM == 2) xu[j][t] = gv_load4<0>(rx, lx, so + k * 4);
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // keep this issue order
 #pragma unroll
         for (int j = 0; j < UPW; j++) {
-            const uint32_t u = (uint32_t)min(ub0 + wv + j * WAVES, units - 1);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                w[j][r].q0 = ldg128(qbase[r] + u * 2048u);
-                w[j][r].q1 = ldg128(qbase[r] + u * 2048u + 1024u);
-                w[j][r].h = ldg128(hbase[r] + u * 256u);
-            }
+            w[j].q0 = gv_load4<2>(rq, l16, uo[j] * 2048);
+            w[j].q1 = gv_load4<2>(rq, l16 + 1024, uo[j] * 2048);
+            w[j].h = gv_load4<2>(rh, n16, uo[j] * 256);
             __builtin_amdgcn_sched_barrier(0);
         }
+        if (ub0 == 0 && lane < 8 * UPW)  // the wave's own pads, read later only by lanes of this wave
+            *reinterpret_cast<u32x4 *>(&xbuf[wv][lane >> 3][MT * 512 + 8 * (lane & 7)]) = u32x4{0u, 0u, 0u, 0u};
         // every unit's activation slice is staged first: it needs only the activation
         // loads (issued before the weights), so it runs while the weights stream in
         XStat st_all[UPW][MT];
@@ -802,6 +808,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        int aoff[NTP];
+#pragma unroll
+        for (int tp = 0; tp < NTP; tp++) {
+            const bool own = G == (n >> 2) && 2 * tp + (i >> 1) < MT;
+            aoff[tp] = own ? ((2 * tp + (i >> 1)) * 2 + (i & 1)) * 256 + 64 * G : MT * 512;
+        }
 #pragma unroll
         for (int j = 0; j < UPW; j++) {
             if (ub0 + wv + j * WAVES >= units) break;  // wave-uniform
@@ -809,49 +821,46 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
             const uint16_t *ap[NTP];
 #pragma unroll
             for (int tp = 0; tp < NTP; tp++) ap[tp] = xbuf[wv][j] + aoff[tp];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K
-                // packing, get_scale_min_k4, crates/nn-core/src/layers/quantized/linear.rs:166-176)
-                const u32x4 &h = w[j][r].h;
-                const float d = f16_to_f32(h[0] & 0xFFFFu), dmin = f16_to_f32(h[0] >> 16);
-                const uint32_t S1 = h[1], S2 = h[2], S3 = h[3];
-                const uint32_t hsel = 0u - (uint32_t)(G >> 1);  // all ones for sub-blocks 4..7
-                const uint32_t scw =
-                    ((S1 & 0x3F3F3F3Fu) & ~hsel) | (((S3 & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) & hsel);
-                const uint32_t mnw =
-                    ((S2 & 0x3F3F3F3Fu) & ~hsel) | ((((S3 >> 4) & 0x0F0F0F0Fu) | ((S2 >> 2) & 0x30303030u)) & hsel);
-                const uint32_t scp = scw >> (16 * (G & 1)), mnp = mnw >> (16 * (G & 1));
-                const float sc_lo = (float)(scp & 0xFFu), sc_hi = 0.0625f * (float)((scp >> 8) & 0xFFu);
-                const float mn_lo = (float)(mnp & 0xFFu), mn_hi = (float)((mnp >> 8) & 0xFFu);
+            // header: d | dmin, scales[0..3], scales[4..7], scales[8..11] (BlockQ4K
+            // packing, get_scale_min_k4, crates/nn-core/src/layers/quantized/linear.rs:166-176)
+            const u32x4 &h = w[j].h;
+            const float d = f16_to_f32(h[0] & 0xFFFFu), dmin = f16_to_f32(h[0] >> 16);
+            const uint32_t S1 = h[1], S2 = h[2], S3 = h[3];
+            const uint32_t hsel = 0u - (uint32_t)(G >> 1);  // all ones for sub-blocks 4..7
+            const uint32_t scw =
+                ((S1 & 0x3F3F3F3Fu) & ~hsel) | (((S3 & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) & hsel);
+            const uint32_t mnw =
+                ((S2 & 0x3F3F3F3Fu) & ~hsel) | ((((S3 >> 4) & 0x0F0F0F0Fu) | ((S2 >> 2) & 0x30303030u)) & hsel);
+            const uint32_t scp = scw >> (16 * (G & 1)), mnp = mnw >> (16 * (G & 1));
+            const float sc_lo = (float)(scp & 0xFFu), sc_hi = 0.0625f * (float)((scp >> 8) & 0xFFu);
+            const float mn_lo = (float)(mnp & 0xFFu), mn_hi = (float)((mnp >> 8) & 0xFFu);
 
-                floatx4 clo[NTP], chi[NTP];
+            floatx4 clo[NTP], chi[NTP];
 #pragma unroll
-                for (int tp = 0; tp < NTP; tp++) clo[tp] = chi[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int tp = 0; tp < NTP; tp++) clo[tp] = chi[tp] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int q4 = 0; q4 < 4; q4++) {
-                    const u32x4 q = q4 < 2 ? w[j][r].q0 : w[j][r].q1;
-                    const uint32_t w0 = q[2 * (q4 & 1)], w1 = q[2 * (q4 & 1) + 1];
-                    const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
-                    const u32x4 blo = {w0 & 0x000F000Fu, w0s & 0x000F000Fu, w1 & 0x000F000Fu, w1s & 0x000F000Fu};
-                    const u32x4 bhi = {w0 & 0x00F000F0u, w0s & 0x00F000F0u, w1 & 0x00F000F0u, w1s & 0x00F000F0u};
+            for (int q4 = 0; q4 < 4; q4++) {
+                const u32x4 q = q4 < 2 ? w[j].q0 : w[j].q1;
+                const uint32_t w0 = q[2 * (q4 & 1)], w1 = q[2 * (q4 & 1) + 1];
+                const uint32_t w0s = w0 >> 8, w1s = w1 >> 8;
+                const u32x4 blo = {w0 & 0x000F000Fu, w0s & 0x000F000Fu, w1 & 0x000F000Fu, w1s & 0x000F000Fu};
+                const u32x4 bhi = {w0 & 0x00F000F0u, w0s & 0x00F000F0u, w1 & 0x00F000F0u, w1s & 0x00F000F0u};
 #pragma unroll
-                    for (int tp = 0; tp < NTP; tp++) {
-                        clo[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 8 * q4), blo, clo[tp]);
-                        chi[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 32 + 8 * q4), bhi, chi[tp]);
-                    }
+                for (int tp = 0; tp < NTP; tp++) {
+                    clo[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 8 * q4), blo, clo[tp]);
+                    chi[tp] = mfma16x16x32_f16(*reinterpret_cast<const u32x4 *>(ap[tp] + 32 + 8 * q4), bhi, chi[tp]);
                 }
-                // lane 16G + n now holds, for row n and sub-blocks 2G / 2G + 1, the
-                // (hi, lo) partial dot products of token 2 tp (entries 0, 1 of set tp) and
-                // token 2 tp + 1 (entries 2, 3)
+            }
+            // lane 16G + n now holds, for row n and sub-blocks 2G / 2G + 1, the
+            // (hi, lo) partial dot products of token 2 tp (entries 0, 1 of set tp) and
+            // token 2 tp + 1 (entries 2, 3)
 #pragma unroll
-                for (int t = 0; t < MT; t++) {
-                    const floatx4 &cl = clo[t >> 1], &ch = chi[t >> 1];
-                    const int e = 2 * (t & 1);
-                    const float T = (sc_lo * st[t].b_lo) * (cl[e] + cl[e + 1]) + (sc_hi * st[t].b_hi) * (ch[e] + ch[e + 1]);
-                    acc1[r][t] += d * T;
-                    acc2[r][t] += dmin * (mn_lo * st[t].xs_lo + mn_hi * st[t].xs_hi);
-                }
+            for (int t = 0; t < MT; t++) {
+                const floatx4 &cl = clo[t >> 1], &ch = chi[t >> 1];
+                const int e = 2 * (t & 1);
+                const float T = (sc_lo * st[t].b_lo) * (cl[e] + cl[e + 1]) + (sc_hi * st[t].b_hi) * (ch[e] + ch[e + 1]);
+                acc1[t] += d * T;
+                acc2[t] += dmin * (mn_lo * st[t].xs_lo + mn_hi * st[t].xs_hi);
             }
         }
         ub0 += WAVES * UPW;
@@ -859,20 +868,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
 
     // y = 2^24 * (code sums) - (min terms), summed over the lane groups, then the waves
 #pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int t = 0; t < MT; t++) {
-            const float v = sum_rows(acc1[r][t] * 16777216.0f - acc2[r][t]);
-            if (lane < 16) red[wv][r * MT + t][lane] = v;
-        }
+    for (int t = 0; t < MT; t++) {
+        const float v = sum_rows(acc1[t] * 16777216.0f - acc2[t]);
+        if (lane < 16) red[wv][t][lane] = v;
+    }
     __syncthreads();
-    if (tid < R * MT * 16) {
-        const int rt = tid >> 4, nn = tid & 15, t = rt % MT;
-        const int64_t tile = tile0 + rt / MT;  // rows of a tail tile fail row < n
+    if (tid < MT * 16) {
+        const int t = tid >> 4, nn = tid & 15;
         float y = 0.f;
 #pragma unroll
-        for (int w2 = 0; w2 < WAVES; w2++) y += red[w2][rt][nn];
-        const int64_t row = tile * 16 + nn;
+        for (int w2 = 0; w2 < WAVES; w2++) y += red[w2][t][nn];
+        const int64_t row = (int64_t)tile * 16 + nn;
         if (a.swiglu_out) {
             // rows nn < 8 are gate rows, nn + 8 their up rows (full tiles: n = 2 * inter, inter % 8 == 0)
             store_swiglu_pair(a, y, t, tile, nn, blockIdx.x == 0 && tid == 0);
@@ -891,7 +897,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_decode_kernel(GemvArgs a)
                 uint64_t other = __shfl_xor(key, o, 16);
                 key = other > key ? other : key;
             }
-            if (nn == 0 && tile < a.ntile) a.argmax_partial[tile] = key;
+            if (nn == 0) a.argmax_partial[tile] = key;
         }
     }
 }
@@ -2029,22 +2035,20 @@ static int launch_wave(const GemvArgs &a, int64_t units, void *stream) {
         return launch_q6k_decode(a, units, stream);
 }
 
-template <int WAVES, int UPW, int R, int XM>
-static int launch_q4k_decode_x(const GemvArgs &a, void *stream) {
-    const dim3 grid((unsigned)((a.ntile + R - 1) / R));
-    if (a.m == 1)
-        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, R, XM, 1>), grid, dim3(WAVES * 64), 0,
-                           (hipStream_t)stream, a);
-    else
-        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, R, XM, 2>), grid, dim3(WAVES * 64), 0,
-                           (hipStream_t)stream, a);
+template <int WAVES, int UPW, int XM, int MT>
+static int launch_q4k_decode_k(const GemvArgs &a, void *stream) {
+    hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, XM, MT>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
+                       (hipStream_t)stream, a.qs, a.hdr, a.x, (int)a.nblk, (int)a.m, a);
     return (int)hipGetLastError();
 }
-template <int WAVES, int UPW, int R>
+template <int WAVES, int UPW, int XM>
+static int launch_q4k_decode_x(const GemvArgs &a, void *stream) {
+    return a.m == 1 ? launch_q4k_decode_k<WAVES, UPW, XM, 1>(a, stream) : launch_q4k_decode_k<WAVES, UPW, XM, 2>(a, stream);
+}
+template <int WAVES, int UPW>
 static int launch_q4k_decode_t(const GemvArgs &a, void *stream) {
-    if (a.x_swiglu) return launch_q4k_decode_x<WAVES, UPW, R, 2>(a, stream);
-    return a.x_bf16 ? launch_q4k_decode_x<WAVES, UPW, R, 1>(a, stream)
-                    : launch_q4k_decode_x<WAVES, UPW, R, 0>(a, stream);
+    if (a.x_swiglu) return launch_q4k_decode_x<WAVES, UPW, 2>(a, stream);
+    return a.x_bf16 ? launch_q4k_decode_x<WAVES, UPW, 1>(a, stream) : launch_q4k_decode_x<WAVES, UPW, 0>(a, stream);
 }
 
 // Q4_K decode shapes, from sweeps on MI355X: K of up to 16 units takes 8 waves of
@@ -2057,12 +2061,7 @@ static int device_cus();
 // 4 tokens at 4096x12288 in 11.4 us (two passes of two: 15.0)
 template <int WAVES, int UPW>
 static int launch_q4k_batch_t(const GemvArgs &a, void *stream) {
-    const dim3 grid((unsigned)a.ntile);
-    if (a.x_bf16)
-        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, 1, 1, 4>), grid, dim3(WAVES * 64), 0, (hipStream_t)stream, a);
-    else
-        hipLaunchKernelGGL((gemv_q4k_decode_kernel<WAVES, UPW, 1, 0, 4>), grid, dim3(WAVES * 64), 0, (hipStream_t)stream, a);
-    return (int)hipGetLastError();
+    return a.x_bf16 ? launch_q4k_decode_k<WAVES, UPW, 1, 4>(a, stream) : launch_q4k_decode_k<WAVES, UPW, 0, 4>(a, stream);
 }
 
 static int launch_q4k_decode(const GemvArgs &a, void *stream) {
@@ -2094,13 +2093,13 @@ static int launch_q4k_decode(const GemvArgs &a, void *stream) {
             return (int)hipGetLastError();
         }
     }
-    if (units <= 4) return launch_q4k_decode_t<4, 1, 1>(a, stream);
-    if (units <= 8) return launch_q4k_decode_t<8, 1, 1>(a, stream);
-    if (units <= 16) return launch_q4k_decode_t<8, 2, 1>(a, stream);
+    if (units <= 4) return launch_q4k_decode_t<4, 1>(a, stream);
+    if (units <= 8) return launch_q4k_decode_t<8, 1>(a, stream);
+    if (units <= 16) return launch_q4k_decode_t<8, 2>(a, stream);
     const int64_t need = (units + 15) / 16;
-    if (need <= 2) return launch_q4k_decode_t<16, 2, 1>(a, stream);
-    if (need <= 3) return launch_q4k_decode_t<16, 3, 1>(a, stream);
-    return launch_q4k_decode_t<16, 4, 1>(a, stream);
+    if (need <= 2) return launch_q4k_decode_t<16, 2>(a, stream);
+    if (need <= 3) return launch_q4k_decode_t<16, 3>(a, stream);
+    return launch_q4k_decode_t<16, 4>(a, stream);
 }
 
 // tokens per launch: Q4_K and Q6_K up to 4, Q8_0 up to 8 (callers run passes)
