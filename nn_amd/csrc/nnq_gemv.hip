@@ -958,31 +958,31 @@ __device__ __forceinline__ float lane_value(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// XM: activation kind, 0 f32, 1 bf16, 2 f32 gate | up pairs (SwiGLU prologue)
+// XM: activation kind, 0 f32, 1 bf16, 2 f32 gate | up pairs (SwiGLU prologue).  Leading
+// scalar arguments preloaded into SGPRs and buffer loads, as gemv_q4k_decode_kernel.
 template <int WAVES, int UPW, int XM, int MT>
-__global__ __launch_bounds__(WAVES * 64) void gemv_q80_decode_kernel(GemvArgs a) {
+__global__ __launch_bounds__(WAVES * 64) void gemv_q80_decode_kernel(const uint8_t *qs, const uint8_t *hdr,
+                                                                    const void *x, int units, int k, int mt,
+                                                                    GemvArgs a) {
     constexpr bool XB = XM == 1;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tile = (int)blockIdx.x;
+    constexpr int xe = XB ? 2 : 4;
+    const int xrow = XM == 2 ? 2 * k : k;  // elements per token row of x
+    const __amdgpu_buffer_rsrc_t rq = gv_rsrc(qs + (size_t)tile * units * 4096, (int64_t)units * 4096);
+    const __amdgpu_buffer_rsrc_t rh = gv_rsrc(hdr + (size_t)tile * units * 256, (int64_t)units * 256);
+    const __amdgpu_buffer_rsrc_t rx = gv_rsrc(x, (int64_t)mt * xrow * xe);
+    const int l16 = 16 * lane, lx = 4 * lane * xe;
     // per wave and unit of a pass: [token, hi / lo][256] f16, then 256 zero halves
     constexpr int kBuf = MT * 512 + 256;
     __shared__ __attribute__((aligned(16))) uint16_t xbuf[WAVES][UPW][kBuf];
     __shared__ float red[WAVES][MT][16];
-#pragma unroll
-    for (int j = 0; j < UPW; j++)  // the wave's own pads, read later only by lanes of this wave
-        if (lane < 32) *reinterpret_cast<u32x4 *>(&xbuf[wv][j][MT * 512 + 8 * lane]) = u32x4{0u, 0u, 0u, 0u};
 
     // A-operand row of this lane: lane & 15 = 2t + part (token t, hi / lo part)
     const int r16 = lane & 15, kg = lane >> 4;
     const int aoff = (r16 >> 1) < MT ? r16 * 256 + 8 * kg : MT * 512 + 8 * kg;
 
-    const int units = (int)(a.nblk / 8), k = (int)a.k;
-    const uint8_t *qbase = a.qs + (size_t)tile * (size_t)(a.nblk / 2) * 1024 + 16 * lane;
-    const uint8_t *hbase = a.hdr + (size_t)tile * units * 256 + 16 * r16;
-    constexpr int xe = XB ? 2 : 4;
-    const int xrow = XM == 2 ? 2 * k : k;  // elements per token row of x
-    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x);
     float acc1[MT], acc2[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) acc1[t] = acc2[t] = 0.f;
@@ -991,32 +991,36 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q80_decode_kernel(GemvArgs a)
         // activation slices first (L2 hits), then the weights of every unit of the pass
         u32x4 xr[UPW][MT], xu[XM == 2 ? UPW : 1][MT];
         bool xin[UPW];
+        int uo[UPW];
 #pragma unroll
         for (int j = 0; j < UPW; j++) {
-            const int u = min(ub0 + wv + j * WAVES, units - 1);
-            const int kk = u * 256 + 4 * lane;
-            xin[j] = kk < k;
+            uo[j] = min(ub0 + wv + j * WAVES, units - 1);
+            xin[j] = uo[j] * 256 + 4 * lane < k;  // k beyond K in the last (padded) unit: staged as zeros
 #pragma unroll
             for (int t = 0; t < MT; t++) {
-                const uint8_t *p = xb + (size_t)(xin[j] ? t * xrow + kk : 0) * xe;  // out of range: x[0]
+                const int so = (t * xrow + uo[j] * 256) * xe;
                 if (XB) {
-                    const u32x2 w2 = *reinterpret_cast<const u32x2 *>(p);
+                    const u32x2 w2 = gv_load2(rx, lx, so);
                     xr[j][t] = u32x4{w2[0], w2[1], 0u, 0u};
                 } else {
-                    xr[j][t] = *reinterpret_cast<const u32x4 *>(p);
+                    xr[j][t] = gv_load4<0>(rx, lx, so);
                 }
-                if constexpr (XM == 2) xu[j][t] = *reinterpret_cast<const u32x4 *>(p + (size_t)k * 4);
+                if constexpr (XM == 2) xu[j][t] = gv_load4<0>(rx, lx, so + k * 4);
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // keep this issue order
         UnitQ80 w[UPW];
 #pragma unroll
         for (int j = 0; j < UPW; j++) {
-            const uint32_t u = (uint32_t)min(ub0 + wv + j * WAVES, units - 1);
 #pragma unroll
-            for (int i = 0; i < 4; i++) w[j].q[i] = ldg128(qbase + (size_t)(u * 4u + i) * 1024u);
-            w[j].h = ldg128(hbase + (size_t)u * 256u);
+            for (int i = 0; i < 4; i++) w[j].q[i] = gv_load4<2>(rq, l16 + 1024 * i, uo[j] * 4096);
+            w[j].h = gv_load4<2>(rh, 16 * r16, uo[j] * 256);
             __builtin_amdgcn_sched_barrier(0);
+        }
+        if (ub0 == 0) {  // the wave's own pads, read later only by lanes of this wave
+#pragma unroll
+            for (int j = 0; j < UPW; j++)
+                if (lane < 32) *reinterpret_cast<u32x4 *>(&xbuf[wv][j][MT * 512 + 8 * lane]) = u32x4{0u, 0u, 0u, 0u};
         }
         // staging needs only the activation loads, so it runs while the weights stream in
         float bk[UPW][MT], xs[UPW][MT];
@@ -1914,10 +1918,10 @@ template <int WAVES, int UPW, int XM>
 static int launch_q80_decode_x(const GemvArgs &a, void *stream) {
     if (a.m == 1)
         hipLaunchKernelGGL((gemv_q80_decode_kernel<WAVES, UPW, XM, 1>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
-                           (hipStream_t)stream, a);
+                           (hipStream_t)stream, a.qs, a.hdr, a.x, (int)(a.nblk / 8), (int)a.k, (int)a.m, a);
     else
         hipLaunchKernelGGL((gemv_q80_decode_kernel<WAVES, UPW, XM, 2>), dim3((unsigned)a.ntile), dim3(WAVES * 64), 0,
-                           (hipStream_t)stream, a);
+                           (hipStream_t)stream, a.qs, a.hdr, a.x, (int)(a.nblk / 8), (int)a.k, (int)a.m, a);
     return (int)hipGetLastError();
 }
 template <int WAVES, int UPW>
