@@ -286,7 +286,8 @@ int nnq_moe_destroy(nnq_moe *moe);
  * softmax -> top_k -> renormalise -> per expert clamp(silu(x@Wg+bg), -limit, limit)
  * * (x@Wu+bu) -> @Wd + bd -> weighted sum.  x: NNQ_F32 or NNQ_BF16, 16-byte aligned;
  * any number of tokens (batches beyond 16384 token-expert assignments run as token
- * chunks of that size, one after another on the stream), top_k <= 8.  Routing,
+ * chunks of that size, one after another on the stream), top_k from 1 to the number of
+ * experts (experts_per_token, crates/nn-gptoss/src/quantized_model.rs:92,141).  Routing,
  * permutation and combine run on the
  * device (no host synchronisation); the expert outputs are summed per token in
  * ascending expert order, as moe_forward's index_add does.

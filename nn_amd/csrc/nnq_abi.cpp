@@ -743,7 +743,7 @@ int nnq_moe_forward(const nnq_moe *m, const void *x, nnq_dtype x_dtype, int64_t 
                     int top_k, float swiglu_limit, float *y, uint32_t *topk_idx, float *topk_w, void *stream) {
     if (!m) return fail(NNQ_ERR_INVALID_ARGUMENT, "MoE handle is null");
     if (tokens < 0) return fail(NNQ_ERR_INVALID_ARGUMENT, "tokens < 0");
-    if (top_k <= 0 || top_k > m->d.E || top_k > 8)
+    if (top_k <= 0 || top_k > m->d.E)
         return fail(NNQ_ERR_INVALID_SHAPE, "topk k=%d out of range for %lld experts", top_k, (long long)m->d.E);
     if (x_dtype != NNQ_F32 && x_dtype != NNQ_BF16) return fail(NNQ_ERR_UNSUPPORTED, "input dtype %d", (int)x_dtype);
     if (tokens == 0) return NNQ_OK;
@@ -988,7 +988,7 @@ int nnq_moe_block_forward(const nnq_moe *m, const nnq_router *r, const void *x, 
     if (r->E != m->d.E || r->H != m->d.H)
         return fail(NNQ_ERR_SHAPE_MISMATCH, "router [%lld, %lld] does not match the MoE's %lld experts x hidden %lld",
                     (long long)r->E, (long long)r->H, (long long)m->d.E, (long long)m->d.H);
-    if (top_k <= 0 || top_k > m->d.E || top_k > 8)
+    if (top_k <= 0 || top_k > m->d.E)
         return fail(NNQ_ERR_INVALID_SHAPE, "topk k=%d out of range for %lld experts", top_k, (long long)m->d.E);
     if (tokens == 0) return NNQ_OK;
     if (!y) return fail(NNQ_ERR_INVALID_ARGUMENT, "y is null");

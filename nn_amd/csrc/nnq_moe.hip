@@ -233,9 +233,53 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *logits, int
         for (int j = 0; j < 4; j++) p[j] = p[j] / sum;
     }
     // top-k: descending by total order, ties to the lowest index (key = orderable value, ~index)
+    bool taken[4] = {false, false, false, false};
+    if (k > 8) {
+        // any k (up to E): each selection is written as it is made, its probability kept
+        // in the wave's LDS row (the softmax sum has been read from it already), and the
+        // weights normalised by the sum of the selected values in selection order
+        float ssum = -0.0f;
+        for (int s = 0; s < k; s++) {
+            uint64_t best = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int c = lane + 64 * j;
+                if (c < E && !taken[j]) {
+                    const uint32_t o = (uint32_t)total_key(p[j]) ^ 0x80000000u;
+                    const uint64_t key = ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)c);
+                    best = key > best ? key : best;
+                }
+            }
+            best = wave_max_u64(best);
+            const uint32_t c = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu);
+            float pv = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (lane + 64 * j == (int)c) {
+                    taken[j] = true;
+                    pv = p[j];
+                }
+            }
+            pv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), __builtin_amdgcn_readfirstlane((int)(c & 63))));
+            ssum = ssum + pv;
+            if (lane == 0) {
+                ex[wv][s] = pv;
+                ti[t * k + s] = c;
+                if (ti_out) ti_out[t * k + s] = c;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int s = lane; s < k; s += 64) {
+            const float w = ex[wv][s] / ssum;
+            tw[t * k + s] = w;
+            if (tw_out) tw_out[t * k + s] = w;
+        }
+        return;
+    }
     uint32_t idx[8];
     float val[8];
-    bool taken[4] = {false, false, false, false};
     for (int s = 0; s < k; s++) {
         uint64_t best = 0;
 #pragma unroll
@@ -290,7 +334,8 @@ __global__ __launch_bounds__(256) void moe_route_any_kernel(const float *logits,
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int64_t t = (int64_t)blockIdx.x * 4 + wv;
     if (t >= T) return;  // wave-uniform; no barrier below
-    float *v = rowbuf + (size_t)wv * E;
+    // per wave: E values (then keys), and for k > 8 the k selected values
+    float *v = rowbuf + (size_t)wv * (E + (k > 8 ? k : 0));
     uint32_t *key = reinterpret_cast<uint32_t *>(v);
     auto wave_sync = [] {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -326,6 +371,7 @@ __global__ __launch_bounds__(256) void moe_route_any_kernel(const float *logits,
     // replace the values in LDS (a chosen expert's key becomes 0)
     uint32_t idx[8];
     float val[8];
+    float ssum = -0.0f;
     for (int c = lane; c < E; c += 64) key[c] = (uint32_t)total_key(v[c]) ^ 0x80000000u;
     wave_sync();
     for (int s = 0; s < k; s++) {
@@ -339,14 +385,31 @@ __global__ __launch_bounds__(256) void moe_route_any_kernel(const float *logits,
         const uint32_t o = (uint32_t)(best >> 32) ^ 0x80000000u;  // back to the total-order key
         // the key -> float inverse of total_key
         const int32_t b = (int32_t)o;
-        idx[s] = c;
-        val[s] = __int_as_float(b ^ (int32_t)((uint32_t)(b >> 31) >> 1));
+        const float pv = __int_as_float(b ^ (int32_t)((uint32_t)(b >> 31) >> 1));
+        ssum = ssum + pv;  // the selected values summed in selection order
+        if (k > 8) {
+            // any k: written as selected, the values kept after the keys
+            if (lane == 0) {
+                v[E + s] = pv;
+                ti[t * k + s] = c;
+                if (ti_out) ti_out[t * k + s] = c;
+            }
+        } else {
+            idx[s] = c;
+            val[s] = pv;
+        }
         wave_sync();
         if (lane == 0) key[c] = 0u;
         wave_sync();
     }
-    float ssum = -0.0f;
-    for (int s = 0; s < k; s++) ssum = ssum + val[s];
+    if (k > 8) {
+        for (int s = lane; s < k; s += 64) {
+            const float w = v[E + s] / ssum;
+            tw[t * k + s] = w;
+            if (tw_out) tw_out[t * k + s] = w;
+        }
+        return;
+    }
     if (lane < k) {
         uint32_t ci = 0;
         float cv = 0.0f;
@@ -485,6 +548,96 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const uint32_t *ti, i
             }
         return;
     }
+    for (int64_t i = tid; i < T * k; i += 1024) {
+        const int32_t p = pos[i] + base[ti[i]];
+        pos[i] = p;
+        stok[p] = (int32_t)(i / k);
+    }
+}
+
+// moe_permute_kernel for any k (k > 8): the token's experts are read from ti inside the
+// expert loop instead of registers, and the ranks go through pos.
+__global__ __launch_bounds__(1024) void moe_permute_any_kernel(const uint32_t *ti, int64_t T, int E, int k,
+                                                               int32_t *off, int32_t *stok, int32_t *pos) {
+    __shared__ int32_t wcnt[16][256];
+    extern __shared__ int32_t base[];  // [E]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int e = tid; e < E; e += 1024) base[e] = 0;
+    __syncthreads();
+    for (int64_t t0 = 0; t0 < T; t0 += 1024) {
+        const int64_t t = t0 + tid;
+        for (int g0 = 0; g0 < E; g0 += 256) {
+            const int ge = min(256, E - g0);
+            const bool live = t0 + (int64_t)wv * 64 < T;  // wave-uniform
+            for (int e = 0; e < ge; e++) {
+                if (!live) {
+                    if (lane == 0) wcnt[wv][e] = 0;
+                    continue;
+                }
+                const uint32_t ee = (uint32_t)(g0 + e);
+                int sh = -1;  // the token routes to an expert at most once
+                if (t < T)
+                    for (int s = 0; s < k; s++)
+                        if (ti[t * k + s] == ee) sh = s;
+                const uint64_t m = __ballot(sh >= 0);
+                if (sh >= 0) pos[t * k + sh] = __popcll(m & lt);  // rank within the wave
+                if (lane == 0) wcnt[wv][e] = __popcll(m);
+            }
+            __syncthreads();
+            for (int e = tid; e < ge; e += 1024) {
+                int32_t c[16];
+#pragma unroll
+                for (int w = 0; w < 16; w++) c[w] = wcnt[w][e];
+                int32_t run = base[g0 + e];
+#pragma unroll
+                for (int w = 0; w < 16; w++) {
+                    wcnt[w][e] = run;
+                    run += c[w];
+                }
+                base[g0 + e] = run;
+            }
+            __syncthreads();
+            if (t < T)
+                for (int s = 0; s < k; s++) {
+                    const uint32_t ex = ti[t * k + s];
+                    if (ex >= (uint32_t)g0 && ex < (uint32_t)(g0 + ge)) pos[t * k + s] += wcnt[wv][ex - g0];
+                }
+            __syncthreads();
+        }
+    }
+    if (tid < 64) {
+        int32_t carry = 0;
+        for (int c0 = 0; c0 < E; c0 += 256) {
+            int32_t c[4], sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = c0 + 4 * tid + j;
+                c[j] = e < E ? base[e] : 0;
+                sum += c[j];
+            }
+            int32_t before = sum;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int32_t v = __shfl_up(before, o, 64);
+                if (tid >= o) before += v;
+            }
+            const int32_t total = __shfl(before, 63, 64);
+            before += carry - sum;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = c0 + 4 * tid + j;
+                if (e < E) {
+                    base[e] = before;
+                    off[e] = before;
+                }
+                before += c[j];
+            }
+            carry += total;
+        }
+        if (tid == 0) off[E] = carry;
+    }
+    __syncthreads();
     for (int64_t i = tid; i < T * k; i += 1024) {
         const int32_t p = pos[i] + base[ti[i]];
         pos[i] = p;
@@ -1019,6 +1172,48 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeScratch sc, int64_t
     if (status && __any(bad) && (threadIdx.x & 63) == 0) *status = NNQ_ERR_NON_FINITE;
 }
 
+// moe_combine_kernel for any k (k > 8): the token's (row, weight) pairs are put in
+// ascending expert order in LDS (an entry's place = the count of its smaller experts).
+template <bool V4>
+__global__ __launch_bounds__(256) void moe_combine_any_kernel(MoeScratch sc, int64_t H, int k, float *y,
+                                                              int32_t *status) {
+    extern __shared__ __attribute__((aligned(16))) int32_t cs[];  // [k] rows, then [k] weights
+    int32_t *ps = cs;
+    float *ws = reinterpret_cast<float *>(cs + k);
+    const int64_t t = blockIdx.x;
+    for (int s = threadIdx.x; s < k; s += 256) {
+        const uint32_t e = sc.ti[t * k + s];
+        int r = 0;
+        for (int q = 0; q < k; q++) r += sc.ti[t * k + q] < e ? 1 : 0;
+        ps[r] = sc.pos[t * k + s];
+        ws[r] = sc.tw[t * k + s];
+    }
+    __syncthreads();
+    bool bad = false;
+    if (V4) {
+        const int64_t H4 = H / 4;
+        for (int64_t c = threadIdx.x; c < H4; c += 256) {
+            floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int s = 0; s < k; s++) {
+                const floatx4 v = *reinterpret_cast<const floatx4 *>(sc.yb + (int64_t)ps[s] * H + 4 * c);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = acc[i] + v[i] * ws[s];
+            }
+            *reinterpret_cast<floatx4 *>(y + t * H + 4 * c) = acc;
+#pragma unroll
+            for (int i = 0; i < 4; i++) bad |= !(fabsf(acc[i]) <= 3.402823466e38f);
+        }
+    } else {
+        for (int64_t c = threadIdx.x; c < H; c += 256) {
+            float acc = 0.0f;
+            for (int s = 0; s < k; s++) acc = acc + sc.yb[(int64_t)ps[s] * H + c] * ws[s];
+            y[t * H + c] = acc;
+            bad |= !(fabsf(acc) <= 3.402823466e38f);
+        }
+    }
+    if (status && __any(bad) && (threadIdx.x & 63) == 0) *status = NNQ_ERR_NON_FINITE;
+}
+
 // ---------------------------------------------------------------------------------
 // bit-exact decode of one expert (Mxfp4Tensor::dequantize, crates/nn-gptoss/src/quantize.rs:167-188)
 // ---------------------------------------------------------------------------------
@@ -1134,8 +1329,9 @@ int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const floa
         hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, nsplit, bias, T,
                            (int)d.E, k, sc.ti, sc.tw, topk_idx, topk_w);
     else
-        hipLaunchKernelGGL(moe_route_any_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), (size_t)4 * d.E * 4, st,
-                           logits, nsplit, bias, T, (int)d.E, k, sc.ti, sc.tw, topk_idx, topk_w);
+        hipLaunchKernelGGL(moe_route_any_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256),
+                           (size_t)4 * (d.E + (k > 8 ? k : 0)) * 4, st, logits, nsplit, bias, T, (int)d.E, k, sc.ti,
+                           sc.tw, topk_idx, topk_w);
     if (!run.perm) switch (k) {
 #define NNQ_PERM(K)                                                                                              \
     case K:                                                                                                      \
@@ -1145,7 +1341,9 @@ int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const floa
         NNQ_PERM(1) NNQ_PERM(2) NNQ_PERM(3) NNQ_PERM(4) NNQ_PERM(5) NNQ_PERM(6) NNQ_PERM(7) NNQ_PERM(8)
 #undef NNQ_PERM
     default:
-        return (int)hipErrorInvalidValue;
+        hipLaunchKernelGGL(moe_permute_any_kernel, dim3(1), dim3(1024), (size_t)d.E * 4, st, sc.ti, T, (int)d.E, k,
+                           sc.off, sc.stok, sc.pos);
+        break;
     }
     if (x_bf16) {
         run.xa[0] = reinterpret_cast<const uint16_t *>(x);
@@ -1176,7 +1374,13 @@ int launch_moe(const MoeDev &d, const void *x, int x_bf16, int64_t T, const floa
         NNQ_COMB(1) NNQ_COMB(2) NNQ_COMB(3) NNQ_COMB(4) NNQ_COMB(5) NNQ_COMB(6) NNQ_COMB(7) NNQ_COMB(8)
 #undef NNQ_COMB
     default:
-        return (int)hipErrorInvalidValue;
+        if (v4)
+            hipLaunchKernelGGL((moe_combine_any_kernel<true>), dim3((unsigned)T), dim3(256), (size_t)k * 8, st, sc, d.H,
+                               k, y, status);
+        else
+            hipLaunchKernelGGL((moe_combine_any_kernel<false>), dim3((unsigned)T), dim3(256), (size_t)k * 8, st, sc, d.H,
+                               k, y, status);
+        break;
     }
     return (int)hipGetLastError();
 }

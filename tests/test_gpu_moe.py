@@ -269,6 +269,35 @@ def test_moe_block_vs_oracle(O, dev, E, H, I, T, k, xdt):
     check_close(ref, y.cpu().numpy(), f"moe block E={E} H={H} I={I} T={T} k={k} x={xdt}")
 
 
+# top_k above 8 (experts_per_token up to the expert count, quantized_model.rs:92,141):
+# the general routing path (E <= 256 and E > 256), the general permutation (batches over
+# 1024 tokens), the general combine, and k = E.
+@pytest.mark.parametrize("E,H,I,T,k,xdt", [(32, 96, 64, 40, 16, "bf16"), (24, 64, 64, 1100, 12, "f32"),
+                                          (300, 64, 64, 30, 20, "bf16"), (16, 64, 64, 50, 16, "f32")])
+def test_moe_top_k_above_8(O, dev, E, H, I, T, k, xdt):
+    import nn_amd
+    L = make_layer(E, H, I, seed=E * 5 + k)
+    rw, rb = make_router(E, H, seed=E + k)
+    moe = nn_amd.QuantizedMoE(E, H, I, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"],
+                              router_weight=rw, router_bias=rb)
+    x = torch.from_numpy(nn_amd.synth_normal(k + 3, 5, (T, H), 1.0)).to(dev)
+    if xdt == "bf16":
+        x = x.to(torch.bfloat16)
+    xf = x.float().cpu().numpy()
+    logits = torch.from_numpy(nn_amd.synth_normal(k + 3, 6, (T, E), 1.0)).to(dev)
+    y, ti, tw = moe.forward(x, logits, top_k=k, return_routing=True)
+    ref, rti, rtw = O.moe_forward(xf, logits.cpu().numpy(), k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    assert np.array_equal(ti.cpu().numpy().astype(np.uint32), rti), "routing differs"
+    assert np.allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    check_close(ref, y.cpu().numpy(), f"moe E={E} T={T} k={k} x={xdt}")
+    yb, tib, twb = moe.block_forward(x, top_k=k, return_routing=True)
+    lg = O.router_logits(xf, rw, rb)
+    refb, rtib, rtwb = O.moe_forward(xf, lg, k, L["gp"], L["gs"], L["gb"], L["dp"], L["ds"], L["db"], I)
+    assert np.array_equal(tib.cpu().numpy().astype(np.uint32), rtib), "block routing differs"
+    assert np.allclose(twb.cpu().numpy(), rtwb, rtol=1e-5, atol=1e-6)
+    check_close(refb, yb.cpu().numpy(), f"moe block E={E} T={T} k={k} x={xdt}")
+
+
 def test_moe_block_nonfinite_raises(O, dev):
     import nn_amd
     E, H, I, T = 4, 64, 64, 6
