@@ -34,7 +34,7 @@ HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_gemm_wi
 PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
 EXTRA_FLAGS = {"nnq_gemm_blk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "nnq_gemv.hip": PRELOAD,
                "nnq_probe.hip": PRELOAD}
-HOST_SOURCES = ["nnq_abi.cpp", "nnq_repack.cpp", "nnq_host.cpp", "nnq_gguf.cpp"]
+HOST_SOURCES = ["nnq_abi.cpp", "nnq_plan.cpp", "nnq_repack.cpp", "nnq_host.cpp", "nnq_gguf.cpp"]
 # measurement probes for bench.py (streaming-read floor, empty launch), a library of their own
 PROBE_SOURCES = ["nnq_probe.hip"]
 PROBE_LIB = os.path.join(HERE, "libnnq_probe.so")

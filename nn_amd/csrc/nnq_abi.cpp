@@ -63,14 +63,15 @@ int hip_fail(hipError_t e, const char *what) {
     return fail(NNQ_ERR_DISPATCH_FAILED, "%s: %s", what, hipGetErrorString(e));
 }
 
+// a workspace whose size does not fit size_t (absurd shapes)
+int size_fail() { return fail(NNQ_ERR_OUT_OF_MEMORY, "workspace size overflows"); }
+
 #define HIP_TRY(expr, what)                       \
     do {                                          \
         hipError_t _e = (expr);                   \
         if (_e != hipSuccess) return hip_fail(_e, what); \
     } while (0)
 
-// token-expert assignments per MoE launch sequence; longer batches run in token chunks
-constexpr int64_t kMoeChunkAssign = 16384;
 // experts of a MoE layer: the routing kernels keep a token's E probabilities (4 tokens per
 // workgroup) and the permutation its E running counts in LDS
 constexpr int kMoeMaxExperts = 4096;
@@ -277,7 +278,6 @@ struct Scratch {
     }
 };
 
-inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // The kernels load activations as 16-byte vectors and store outputs as 4-byte words (or
 // wider); an input or output at an address that does not allow that (a narrowed view)
@@ -500,9 +500,18 @@ static bool gemm_batch(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
     return m > (x_dtype == NNQ_BF16 ? 8 : 16);
 }
 
+// the prefill GEMM's scratch for m tokens run in launches of gemm_chunk_rows rows (the
+// first launch's rows, or the last, shorter one's when that plan needs more)
+static size_t gemm_call_scratch(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
+    const int64_t mc = gemm_chunk_rows(m, w->L.k), tail = m % mc;
+    size_t b = gemm_scratch_bytes(gemm_args(w, nullptr, x_dtype, mc, nullptr, nullptr, NNQ_F32));
+    if (tail) b = std::max(b, gemm_scratch_bytes(gemm_args(w, nullptr, x_dtype, tail, nullptr, nullptr, NNQ_F32)));
+    return b;
+}
+
 static size_t linear_scratch_bytes(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
     if (!gemm_batch(w, m, x_dtype)) return 0;
-    return gemm_scratch_bytes(gemm_args(w, nullptr, x_dtype, m, nullptr, nullptr, NNQ_F32));
+    return gemm_call_scratch(w, m, x_dtype);
 }
 
 static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m, const float *bias,
@@ -515,17 +524,24 @@ static int dispatch_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype
     const int64_t k = L.k;
     const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, ye = y_dtype == NNQ_BF16 ? 2 : 4;
     if (gemm_batch(w, m, x_dtype) && !x_swiglu) {
-        // prefill: MFMA GEMM (Q4_K: nnq_gemm*.hip; Q8_0 / Q6_K: nnq_gemm_blk.hip)
-        GemmArgs g = gemm_args(w, x, x_dtype, m, bias, y, y_dtype);
+        // prefill: MFMA GEMM (Q4_K: nnq_gemm*.hip; Q8_0 / Q6_K: nnq_gemm_blk.hip), in launches
+        // of gemm_chunk_rows rows (their 32-bit activation offsets; one launch up to ~43k
+        // rows at K = 12288), one after another on the stream sharing the scratch
+        const int64_t mc = gemm_chunk_rows(m, k);
         Scratch s;
-        if (ext_scratch)
-            g.scratch = ext_scratch;
-        else {
-            HIP_TRY(s.alloc(gemm_scratch_bytes(g), (hipStream_t)stream), "scratch alloc");
-            g.scratch = s.p;
+        void *scr = ext_scratch;
+        if (!scr) {
+            HIP_TRY(s.alloc(gemm_call_scratch(w, m, x_dtype), (hipStream_t)stream), "scratch alloc");
+            scr = s.p;
         }
-        int e = g.blk ? launch_gemm_blk(g, stream) : launch_gemm_q4k(g, stream);
-        if (e) return hip_fail((hipError_t)e, "gemm launch");
+        for (int64_t m0 = 0; m0 < m; m0 += mc) {
+            const int64_t rows = std::min(mc, m - m0);
+            GemmArgs g = gemm_args(w, (const uint8_t *)x + (size_t)m0 * k * xe, x_dtype, rows, bias,
+                                   (uint8_t *)y + (size_t)m0 * L.n * ye, y_dtype);
+            g.scratch = scr;
+            int e = g.blk ? launch_gemm_blk(g, stream) : launch_gemm_q4k(g, stream);
+            if (e) return hip_fail((hipError_t)e, "gemm launch");
+        }
         return NNQ_OK;
     }
     // tokens per GEMV pass: Q4_K and Q6_K up to 4 (their decode kernels with four token
@@ -568,17 +584,22 @@ int nnq_linear(const nnq_weight *w, const void *x, nnq_dtype x_dtype, int64_t m,
     const bool xm = misaligned_in(x), ym = misaligned_out(y);
     if (!xm && !ym) return dispatch_linear(w, x, x_dtype, m, bias, y, y_dtype, stream);
     const hipStream_t st = (hipStream_t)stream;
-    const size_t xbytes = (size_t)m * k * (x_dtype == NNQ_BF16 ? 2 : 4);
-    const size_t ybytes = (size_t)m * w->L.n * (y_dtype == NNQ_BF16 ? 2 : 4);
-    const size_t xb = xm ? al256(xbytes) : 0, yb = ym ? al256(ybytes) : 0, lb = linear_scratch_bytes(w, m, x_dtype);
+    // workspace: [staged x][y computed here][the GEMM's scratch]
+    size_t xbytes = 0, ybytes = 0, off[3], total = 0;
+    if (!array_bytes(m, k, x_dtype == NNQ_BF16 ? 2 : 4, &xbytes) ||
+        !array_bytes(m, w->L.n, y_dtype == NNQ_BF16 ? 2 : 4, &ybytes))
+        return size_fail();
+    const size_t lb = linear_scratch_bytes(w, m, x_dtype);
+    const size_t sizes[3] = {xm ? xbytes : 0, ym ? ybytes : 0, lb};
+    if (!plan_regions(sizes, 3, off, &total)) return size_fail();
     Scratch s;
-    HIP_TRY(s.alloc(xb + yb + lb, st), "scratch alloc");
+    HIP_TRY(s.alloc(total, st), "scratch alloc");
     uint8_t *base = reinterpret_cast<uint8_t *>(s.p);
-    if (xm) HIP_TRY(hipMemcpyAsync(base, x, xbytes, hipMemcpyDeviceToDevice, st), "stage x");
-    rc = dispatch_linear(w, xm ? base : x, x_dtype, m, bias, ym ? base + xb : y, y_dtype, stream, 0, nullptr, 0,
-                         lb ? base + xb + yb : nullptr);
+    if (xm) HIP_TRY(hipMemcpyAsync(base + off[0], x, xbytes, hipMemcpyDeviceToDevice, st), "stage x");
+    rc = dispatch_linear(w, xm ? base + off[0] : x, x_dtype, m, bias, ym ? base + off[1] : y, y_dtype, stream, 0,
+                         nullptr, 0, lb ? base + off[2] : nullptr);
     if (rc) return rc;
-    if (ym) HIP_TRY(hipMemcpyAsync(y, base + xb, ybytes, hipMemcpyDeviceToDevice, st), "copy y out");
+    if (ym) HIP_TRY(hipMemcpyAsync(y, base + off[1], ybytes, hipMemcpyDeviceToDevice, st), "copy y out");
     return NNQ_OK;
 }
 
@@ -601,15 +622,18 @@ int nnq_linear_argmax(const nnq_weight *w, const float *x, int64_t k, const floa
     if (!idx) return fail(NNQ_ERR_INVALID_ARGUMENT, "idx is null");
     if (misaligned_out(logits)) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits must be 4-byte aligned");
     const Layout &L = w->L;
-    const size_t kb = al256((size_t)L.ntile * sizeof(unsigned long long));
     const bool xm = misaligned_in(x);
+    // workspace: [per-tile argmax keys][staged x]
+    const size_t sizes[2] = {(size_t)L.ntile * sizeof(unsigned long long), xm ? (size_t)k * 4 : 0};
+    size_t off[2], total = 0;
+    if (!plan_regions(sizes, 2, off, &total)) return size_fail();
     Scratch s;
-    HIP_TRY(s.alloc(kb + (xm ? (size_t)k * 4 : 0), (hipStream_t)stream), "scratch alloc");
+    HIP_TRY(s.alloc(total, (hipStream_t)stream), "scratch alloc");
     if (xm) {
-        HIP_TRY(hipMemcpyAsync(reinterpret_cast<uint8_t *>(s.p) + kb, x, (size_t)k * 4, hipMemcpyDeviceToDevice,
+        HIP_TRY(hipMemcpyAsync(reinterpret_cast<uint8_t *>(s.p) + off[1], x, (size_t)k * 4, hipMemcpyDeviceToDevice,
                                (hipStream_t)stream),
                 "stage x");
-        x = reinterpret_cast<const float *>(reinterpret_cast<uint8_t *>(s.p) + kb);
+        x = reinterpret_cast<const float *>(reinterpret_cast<uint8_t *>(s.p) + off[1]);
     }
     GemvArgs a{};
     a.qs = w->dev;
@@ -752,17 +776,23 @@ int nnq_moe_forward(const nnq_moe *m, const void *x, nnq_dtype x_dtype, int64_t 
         return fail(NNQ_ERR_INVALID_ARGUMENT, "y and router_logits must be 4-byte aligned");
     // tokens are routed independently, so a long batch runs as chunks of at most
     // kMoeChunkAssign token-expert assignments, one after another on the stream
-    const int64_t tc = std::min<int64_t>(tokens, kMoeChunkAssign / top_k);
-    const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, xbytes = (size_t)tokens * m->d.H * xe;
-    const size_t msb = al256(moe_scratch_bytes(tc, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16));
+    const int64_t tc = moe_chunk_tokens(tokens, top_k);
+    const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4;
+    size_t xbytes = 0;
+    if (!array_bytes(tokens, m->d.H, xe, &xbytes)) return size_fail();
     const bool xm = misaligned_in(x);
+    // workspace: [the MoE launches' scratch][staged x]
+    const size_t sizes[2] = {moe_scratch_bytes(tc, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16),
+                             xm ? xbytes : 0};
+    size_t off[2], total = 0;
+    if (!plan_regions(sizes, 2, off, &total)) return size_fail();
     Scratch s;
-    HIP_TRY(s.alloc(msb + (xm ? xbytes : 0), (hipStream_t)stream), "scratch alloc");
+    HIP_TRY(s.alloc(total, (hipStream_t)stream), "scratch alloc");
     if (xm) {
-        HIP_TRY(hipMemcpyAsync(reinterpret_cast<uint8_t *>(s.p) + msb, x, xbytes, hipMemcpyDeviceToDevice,
+        HIP_TRY(hipMemcpyAsync(reinterpret_cast<uint8_t *>(s.p) + off[1], x, xbytes, hipMemcpyDeviceToDevice,
                                (hipStream_t)stream),
                 "stage x");
-        x = reinterpret_cast<uint8_t *>(s.p) + msb;
+        x = reinterpret_cast<uint8_t *>(s.p) + off[1];
     }
     for (int64_t t0 = 0; t0 < tokens; t0 += tc) {
         const int64_t n = std::min(tc, tokens - t0);
@@ -871,32 +901,34 @@ int nnq_mlp_forward(const nnq_mlp *p, const void *x, nnq_dtype x_dtype, int64_t 
     if (rc) return rc;
     if (m == 0) return NNQ_OK;
     const int64_t I = p->inter;
-    auto al = [](size_t v) { return al256(v); };
     // m <= 2: interleaved Q4_K gate | up -> the GEMV writes h = silu(gate) * up and the
     // down GEMV reads h; otherwise the down GEMV takes gate | up and applies SwiGLU while
     // staging.  m > 2: linear, swiglu_kernel, linear.
     const bool fused = m <= 2, hout = fused && p->interleaved8;
-    // one scratch: gate | up [m, 2I] f32 (h [m, I] when hout), h [m, I] f32, then the GEMM
-    // scratch of either linear
-    const size_t gu_bytes = al((size_t)m * (hout ? 1 : 2) * I * 4), h_bytes = fused ? 0 : al((size_t)m * I * 4);
+    // one workspace: gate | up [m, 2I] f32 (h [m, I] when hout), h [m, I] f32, the GEMM
+    // scratch of either linear, then a misaligned x or y staged
+    size_t gu_bytes = 0, h_bytes = 0, xbytes = 0, ybytes = 0;
+    if (!array_bytes(m, (hout ? 1 : 2) * I, 4, &gu_bytes) || !array_bytes(m, fused ? 0 : I, 4, &h_bytes) ||
+        !array_bytes(m, k, x_dtype == NNQ_BF16 ? 2 : 4, &xbytes) ||
+        !array_bytes(m, p->hidden, y_dtype == NNQ_BF16 ? 2 : 4, &ybytes))
+        return size_fail();
     const size_t lin_bytes =
         std::max(linear_scratch_bytes(p->gu, m, x_dtype), fused ? 0 : linear_scratch_bytes(p->down, m, NNQ_F32));
-    // a misaligned x or y goes through the workspace (after the other regions)
-    const size_t xbytes = (size_t)m * k * (x_dtype == NNQ_BF16 ? 2 : 4);
-    const size_t ybytes = (size_t)m * p->hidden * (y_dtype == NNQ_BF16 ? 2 : 4);
     const bool xm = misaligned_in(x), ym = misaligned_out(y);
-    const size_t main_bytes = gu_bytes + h_bytes + al256(lin_bytes);
+    const size_t sizes[5] = {gu_bytes, h_bytes, lin_bytes, xm ? xbytes : 0, ym ? ybytes : 0};
+    size_t off[5], total = 0;
+    if (!plan_regions(sizes, 5, off, &total)) return size_fail();
     Scratch s;
-    HIP_TRY(s.alloc(main_bytes + (xm ? al256(xbytes) : 0) + (ym ? ybytes : 0), (hipStream_t)stream), "scratch alloc");
+    HIP_TRY(s.alloc(total, (hipStream_t)stream), "scratch alloc");
     uint8_t *base = reinterpret_cast<uint8_t *>(s.p);
-    void *lin = lin_bytes ? base + gu_bytes + h_bytes : nullptr;
+    void *lin = lin_bytes ? base + off[2] : nullptr;
     void *const y_user = y;
     if (xm) {
-        HIP_TRY(hipMemcpyAsync(base + main_bytes, x, xbytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "stage x");
-        x = base + main_bytes;
+        HIP_TRY(hipMemcpyAsync(base + off[3], x, xbytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "stage x");
+        x = base + off[3];
     }
-    if (ym) y = base + main_bytes + (xm ? al256(xbytes) : 0);
-    rc = mlp_run(p, x, x_dtype, m, y, y_dtype, status_dev, stream, base, gu_bytes, lin, fused, hout);
+    if (ym) y = base + off[4];
+    rc = mlp_run(p, x, x_dtype, m, y, y_dtype, status_dev, stream, base, off[1], lin, fused, hout);
     if (rc) return rc;
     if (ym) HIP_TRY(hipMemcpyAsync(y_user, y, ybytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "copy y out");
     return NNQ_OK;
@@ -963,11 +995,16 @@ int nnq_router_logits(const nnq_router *r, const void *x, nnq_dtype x_dtype, int
     if (!logits) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits is null");
     if (misaligned_out(logits)) return fail(NNQ_ERR_INVALID_ARGUMENT, "logits must be 4-byte aligned");
     const size_t pb = router_partial_bytes(tokens, r->H, (int)r->E);
-    const size_t xbytes = (size_t)tokens * r->H * (x_dtype == NNQ_BF16 ? 2 : 4);
+    size_t xbytes = 0;
+    if (!array_bytes(tokens, r->H, x_dtype == NNQ_BF16 ? 2 : 4, &xbytes)) return size_fail();
     const bool xm = misaligned_in(x);
+    // workspace (when needed): [K-part slabs][staged x]
+    const size_t sizes[2] = {pb, xm ? xbytes : 0};
+    size_t off[2], total = 0;
+    if (!plan_regions(sizes, 2, off, &total)) return size_fail();
     Scratch s;
-    if (pb || xm) HIP_TRY(s.alloc(al256(pb) + (xm ? xbytes : 0), (hipStream_t)stream), "scratch alloc");
-    if (xm && (rc = stage_tokens(&x, xbytes, reinterpret_cast<uint8_t *>(s.p) + al256(pb), stream))) return rc;
+    if (total) HIP_TRY(s.alloc(total, (hipStream_t)stream), "scratch alloc");
+    if (xm && (rc = stage_tokens(&x, xbytes, reinterpret_cast<uint8_t *>(s.p) + off[1], stream))) return rc;
     int ks = 1;
     int e = launch_router_logits(x, x_dtype == NNQ_BF16, tokens, r->H, r->w, r->b, (int)r->E,
                                  pb ? reinterpret_cast<float *>(s.p) : logits, &ks, nullptr, stream);
@@ -994,14 +1031,20 @@ int nnq_moe_block_forward(const nnq_moe *m, const nnq_router *r, const void *x, 
     if (!y) return fail(NNQ_ERR_INVALID_ARGUMENT, "y is null");
     if (misaligned_out(y)) return fail(NNQ_ERR_INVALID_ARGUMENT, "y must be 4-byte aligned");
     // chunks of at most kMoeChunkAssign token-expert assignments (tokens are independent)
-    const int64_t tc = std::min<int64_t>(tokens, kMoeChunkAssign / top_k);
-    const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4, xbytes = (size_t)tokens * m->d.H * xe;
-    const size_t lg_bytes = al256(std::max(router_partial_bytes(tc, r->H, (int)r->E), (size_t)tc * m->d.E * 4));
-    const size_t msb = al256(moe_scratch_bytes(tc, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16));
+    const int64_t tc = moe_chunk_tokens(tokens, top_k);
+    const size_t xe = x_dtype == NNQ_BF16 ? 2 : 4;
+    size_t xbytes = 0;
+    if (!array_bytes(tokens, m->d.H, xe, &xbytes)) return size_fail();
     const bool xm = misaligned_in(x);
+    // workspace: [a chunk's router logits or K-part slabs][the MoE launches' scratch][staged x]
+    const size_t sizes[3] = {std::max(router_partial_bytes(tc, r->H, (int)r->E), (size_t)tc * m->d.E * 4),
+                             moe_scratch_bytes(tc, m->d.E, m->d.H, m->d.I, top_k, x_dtype == NNQ_BF16),
+                             xm ? xbytes : 0};
+    size_t off[3], total = 0;
+    if (!plan_regions(sizes, 3, off, &total)) return size_fail();
     Scratch s;
-    HIP_TRY(s.alloc(lg_bytes + msb + (xm ? xbytes : 0), (hipStream_t)stream), "scratch alloc");
-    if (xm && (rc = stage_tokens(&x, xbytes, reinterpret_cast<uint8_t *>(s.p) + lg_bytes + msb, stream))) return rc;
+    HIP_TRY(s.alloc(total, (hipStream_t)stream), "scratch alloc");
+    if (xm && (rc = stage_tokens(&x, xbytes, reinterpret_cast<uint8_t *>(s.p) + off[2], stream))) return rc;
     float *logits = reinterpret_cast<float *>(s.p);
     for (int64_t t0 = 0; t0 < tokens; t0 += tc) {
         const int64_t n = std::min(tc, tokens - t0);
@@ -1017,7 +1060,7 @@ int nnq_moe_block_forward(const nnq_moe *m, const nnq_router *r, const void *x, 
         e = launch_moe(m->d, xc, x_dtype == NNQ_BF16, n, logits, ks, ks > 1 ? r->b : nullptr, top_k, swiglu_limit,
                        y + t0 * m->d.H, topk_idx ? topk_idx + t0 * top_k : nullptr,
                        topk_w ? topk_w + t0 * top_k : nullptr, status_dev,
-                       reinterpret_cast<uint8_t *>(s.p) + lg_bytes, stream);
+                       reinterpret_cast<uint8_t *>(s.p) + off[1], stream);
         if (e) return hip_fail((hipError_t)e, "moe launch");
     }
     return NNQ_OK;

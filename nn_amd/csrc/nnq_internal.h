@@ -59,6 +59,21 @@ void q4k_aux_plane(const uint8_t *hdr, const Layout &L, uint8_t *aux, int64_t t0
 // the calling thread's last-error message (nnq_last_error); returns `code`
 int set_error(int code, const char *msg);
 
+// ---- host arithmetic of the ABI calls (nnq_plan.cpp) -------------------------------
+// token-expert assignments per MoE launch sequence; longer batches run in token chunks
+constexpr int64_t kMoeChunkAssign = 16384;
+size_t align256(size_t v);
+// rows * cols * elem bytes; false when negative or beyond size_t
+bool array_bytes(int64_t rows, int64_t cols, size_t elem, size_t *out);
+// regions one after another, each at a 256-byte boundary (a zero size takes no space):
+// offsets[i] and the total; false on size_t overflow
+bool plan_regions(const size_t *sizes, int n, size_t *offsets, size_t *total);
+// tokens per MoE launch sequence (at most kMoeChunkAssign / top_k, at least 1)
+int64_t moe_chunk_tokens(int64_t tokens, int top_k);
+// rows per prefill-GEMM launch: the kernels' 32-bit activation offsets need
+// 4 * rows * k < 2^31
+int64_t gemm_chunk_rows(int64_t m, int64_t k);
+
 // ---- kernel launch parameters ------------------------------------------------------
 struct GemvArgs {
     const uint8_t *qs;    // quant plane

@@ -1,13 +1,15 @@
 // Host code of the nnq library and the CPU oracle under AddressSanitizer and
-// UndefinedBehaviorSanitizer (built by tests/sanitize/Makefile with g++ alone; no HIP).
+// UndefinedBehaviorSanitizer (built by tests/sanitize/Makefile with ROCm's clang as a
+// plain host compiler; no device code is built or run).
 //
 // Covered: the GGUF reader on a valid file and on thousands of mutated copies of it
 // (bit flips, byte overwrites with extreme values, truncations, grown length fields),
 // including tensor-data lookups and the device-weight path up to the repack; the repacks
 // of every weight format and layout over random bytes and ragged shapes; the host
-// encoders over random, zero, tiny, huge and non-finite inputs; and the oracle's
-// decoders, linears, MoE and sampling on small random cases.  Any sanitizer report
-// aborts the run (exit code != 0).
+// encoders over random, zero, tiny, huge and non-finite inputs; the ABI calls' size,
+// workspace-layout and chunking arithmetic (nnq_plan.cpp) over random and extreme
+// shapes; and the oracle's decoders, linears, MoE and sampling on small random cases.
+// Any sanitizer report aborts the run (exit code != 0).
 //
 // nnq_abi.cpp (HIP) is not linked: this file provides the two symbols the host sources
 // take from it, with nnq_weight_create validating as the library does and then running
@@ -329,12 +331,92 @@ static int oracle() {
     return 0;
 }
 
+
+// nnq_plan.cpp: array sizes, workspace regions, MoE token chunks and GEMM row chunks, as
+// the ABI calls use them, over random and extreme shapes (UBSan checks the signed
+// arithmetic; the properties below check the results)
+static int plans() {
+    auto bad = [](const char *what, long long a, long long b) {
+        std::fprintf(stderr, "plan check failed: %s (%lld, %lld)\n", what, a, b);
+        return 1;
+    };
+    const int64_t edge[] = {0, 1, 2, 3, 15, 16, 17, 255, 256, 4095, 4096, 12288, 65535, (int64_t)1 << 31,
+                            ((int64_t)1 << 32) + 7, (int64_t)1 << 40, INT64_MAX / 2, INT64_MAX};
+    std::uniform_int_distribution<int64_t> small(0, 1 << 20);
+    for (int it = 0; it < 20000; it++) {
+        const int64_t r = it < 400 ? edge[it % 18] : small(rng), c = it < 400 ? edge[(it / 18) % 18] : small(rng);
+        const size_t el = (size_t)1 << (it % 4);
+        size_t got = 0;
+        const bool ok = nnq::array_bytes(r, c, el, &got);
+        const unsigned __int128 exact = (unsigned __int128)(uint64_t)r * (uint64_t)c * el;
+        if (ok != (exact <= SIZE_MAX)) return bad("array_bytes overflow flag", r, c);
+        if (ok && got != (size_t)exact) return bad("array_bytes value", r, c);
+        if (nnq::array_bytes(-1 - r, c, el, &got)) return bad("array_bytes negative", r, c);
+    }
+    std::uniform_int_distribution<int> nreg(1, 6);
+    for (int it = 0; it < 20000; it++) {
+        size_t sz[6], off[6], total = 0;
+        const int n = nreg(rng);
+        for (int i = 0; i < n; i++) {
+            const int kind = (int)(rng() % 5);
+            sz[i] = kind == 0 ? 0 : kind == 1 ? rng() % 512 : kind == 2 ? rng() % (1u << 30)
+                  : kind == 3 ? (size_t)(rng() % 4096) * 256 : SIZE_MAX - rng() % 1024;
+        }
+        unsigned __int128 at = 0;
+        bool fits = true;
+        for (int i = 0; i < n; i++) {
+            if (sz[i] == 0) continue;
+            at = (at + sz[i] + 255) / 256 * 256;
+            if (at > SIZE_MAX) fits = false;
+        }
+        const bool ok = nnq::plan_regions(sz, n, off, &total);
+        if (ok != fits) return bad("plan_regions overflow flag", n, (long long)fits);
+        if (!ok) continue;
+        size_t end = 0;
+        for (int i = 0; i < n; i++) {
+            if (off[i] % 256) return bad("region alignment", i, (long long)off[i]);
+            if (sz[i] == 0) continue;
+            if (off[i] < end) return bad("regions overlap", i, (long long)off[i]);
+            end = off[i] + sz[i];
+            if (end > total) return bad("region past the total", i, (long long)end);
+        }
+    }
+    for (int64_t T : {(int64_t)0, (int64_t)1, (int64_t)7, (int64_t)4095, (int64_t)4096, (int64_t)4097,
+                      (int64_t)100000, (int64_t)1 << 40}) {
+        for (int k : {1, 2, 3, 4, 8, 9, 16, 100, 4096, 16384, 16385, 1 << 20}) {
+            const int64_t tc = nnq::moe_chunk_tokens(T, k);
+            if (T == 0) {
+                if (tc != 0) return bad("moe chunk of no tokens", T, k);
+                continue;
+            }
+            if (tc < 1 || tc > T) return bad("moe chunk range", T, k);
+            if (k <= nnq::kMoeChunkAssign && tc * k > nnq::kMoeChunkAssign) return bad("moe chunk assignments", T, k);
+            int64_t covered = 0, launches = 0;
+            for (int64_t t0 = 0; t0 < T && launches < 3; t0 += tc, launches++) covered = std::min(T, t0 + tc);
+            if (launches < 3 && covered != T) return bad("moe chunks cover the batch", T, k);
+        }
+    }
+    for (int64_t K : {(int64_t)32, (int64_t)256, (int64_t)4096, (int64_t)12288, (int64_t)32768, (int64_t)1 << 20,
+                      (int64_t)1 << 26, (int64_t)1 << 30}) {
+        for (int64_t m : {(int64_t)1, (int64_t)9, (int64_t)512, (int64_t)43690, (int64_t)43691, (int64_t)200000,
+                          (int64_t)1 << 35}) {
+            const int64_t mc = nnq::gemm_chunk_rows(m, K);
+            if (mc < 1 || mc > m) return bad("gemm chunk range", m, K);
+            if (4 * mc * K >= ((int64_t)1 << 31) && mc > 1) return bad("gemm chunk 32-bit offsets", m, K);
+            if (mc < m && mc >= 256 && mc % 256) return bad("gemm chunk whole tiles", m, K);
+        }
+    }
+    std::printf("plans: done\n");
+    return 0;
+}
+
 int main(int argc, char **argv) {
     const int iters = argc > 1 ? std::atoi(argv[1]) : 3000;
     const char *dir = argc > 2 ? argv[2] : "/tmp";
     int rc = fuzz_gguf(iters, dir);
     if (!rc) rc = repacks();
     if (!rc) rc = encoders();
+    if (!rc) rc = plans();
     if (!rc) rc = oracle();
     std::printf("%s\n", rc ? "FAILED" : "OK");
     return rc;

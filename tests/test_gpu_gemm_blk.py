@@ -133,3 +133,22 @@ def test_gemm_blk_baseline_shapes(O, dev, fmt, n, k, m):
     w = make_weight(fmt, b, n, k)
     xf, y = run(w, nn_amd.synth_normal(m, 9, (m, k), 1.0), dev, "bf16")
     check_close(oracle_linear(O, fmt, b, n, k, xf), y.cpu().numpy(), f"{fmt} {n}x{k} m={m}")
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_k"])
+def test_gemm_row_chunks(O, dev, fmt):
+    """A batch whose f32 activations pass 2^31 bytes per two planes (17000 x 32768) runs as
+    launches of gemm_chunk_rows rows (16128 here) that share one scratch: rows at the
+    start, across the chunk boundary and at the end match the oracle."""
+    import nn_amd
+    m, n, k = 17000, 64, 32768
+    b = quantized_weight_bytes(fmt, n, k, seed=97, O=O)
+    w = make_weight(fmt, b, n, k)
+    g = torch.Generator(device=dev).manual_seed(97)
+    x = torch.randn((m, k), device=dev, generator=g)
+    y = nn_amd.quantized_linear(x, w).cpu().numpy()
+    for r0 in (0, 16100, m - 64):
+        xs = x[r0:r0 + 64].cpu().numpy()
+        check_close(oracle_linear(O, fmt, b, n, k, xs), y[r0:r0 + 64], f"{fmt} rows {r0}..{r0 + 63} of {m}")
+    del x
+    torch.cuda.empty_cache()
