@@ -82,7 +82,10 @@ def check_close(ref, got, what):
     peak = float(np.abs(ref).max())
     m = Ox.compare(ref, got, abs_tol=ABS_TOL_FRAC * peak)
     cos = Ox.row_cosines(ref, got)
-    print(f"{what}: normwise={m['normwise']:.2e} max_rel={m['max_rel']:.2e} min_row_cos={cos.min():.8f}")
+    # the share of outputs below the elementwise bar's floor (normwise and cosine cover them)
+    skipped = float((np.abs(ref) < ABS_TOL_FRAC * peak).mean())
+    print(f"{what}: normwise={m['normwise']:.2e} max_rel={m['max_rel']:.2e} min_row_cos={cos.min():.8f} "
+          f"elementwise-skipped={skipped:.2%}")
     assert np.isfinite(got).all(), what
     assert m["normwise"] <= REL_TOL, what
     assert m["max_rel"] <= REL_TOL, what
