@@ -53,6 +53,12 @@ GemmScratch gemm_carve(void *base, const GemmArgs &a, size_t *bytes) {
         if (bytes) *bytes = off;
         return s;
     }
+    if (gemm_wide8_plan(a, nullptr)) {
+        GemmScratch s{};
+        const size_t off = gemm_wide8_scratch(a, &s, b);
+        if (bytes) *bytes = off;
+        return s;
+    }
     size_t off = 0;
     GemmScratch s;
     s.xh = reinterpret_cast<uint16_t *>(b + off);

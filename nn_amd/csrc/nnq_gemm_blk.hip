@@ -413,6 +413,7 @@ int launch_gemm_blk(const GemmArgs &a, void *stream) {
     if (a.m <= 0) return 0;
     if (a.blk != NNQ_FMT_Q8_0 && a.blk != NNQ_FMT_Q6_K) return (int)hipErrorInvalidValue;
     const GemmScratch sc = gemm_carve(a.scratch, a, nullptr);
+    if (gemm_wide8_plan(a, nullptr)) return launch_gemm_wide8(a, sc, stream);  // Q8_0, bf16, M > 128
     hipStream_t st = (hipStream_t)stream;
     int e = launch_gemm_prep(a, sc, st);
     if (e) return e;

@@ -545,7 +545,7 @@ __global__ __launch_bounds__(W * 64) void gemm_q4k_skinny_kernel(WideArgs a) {
 // -2^-8 * sum(x * 2^s_row) over the row's eight 32-element sub-blocks.  Rows past M
 // (padding to 16) are written as zeros.
 // ---------------------------------------------------------------------------------
-template <int NG>
+template <int NG, bool XS>
 __global__ __launch_bounds__(512) void gemm_stage_wide_kernel(const uint16_t *x, int64_t m, int64_t k, u32x4 *xa,
                                                               u32x4 *xs, float *rowback) {
     const int64_t row = blockIdx.x;
@@ -596,6 +596,7 @@ __global__ __launch_bounds__(512) void gemm_stage_wide_kernel(const uint16_t *x,
             }
         }
     }
+    if constexpr (!XS) return;  // no min-term operands (Q8_0)
     __syncthreads();
     // min-term fragments: lane group G of super-block b: part G & 1 of -2^-8 * sum, 8 sub-blocks
     const int64_t nsb = k / 256;
@@ -729,6 +730,25 @@ static int launch_skinny_r(const WideArgs &w, hipStream_t st) {
     return (int)hipErrorInvalidValue;
 }
 
+int launch_stage_wide(const uint16_t *x, int64_t m, int64_t k, void *xa, void *xs, float *rowback, void *stream) {
+    const dim3 sg((unsigned)((m + 15) / 16 * 16));
+    hipStream_t st = (hipStream_t)stream;
+    auto fa = reinterpret_cast<u32x4 *>(xa), fs = reinterpret_cast<u32x4 *>(xs);
+    if (k > 4096 * 3 || k % 256) return (int)hipErrorInvalidValue;
+    if (k <= 4096) {
+        if (xs)
+            hipLaunchKernelGGL((gemm_stage_wide_kernel<1, true>), sg, dim3(512), 0, st, x, m, k, fa, fs, rowback);
+        else
+            hipLaunchKernelGGL((gemm_stage_wide_kernel<1, false>), sg, dim3(512), 0, st, x, m, k, fa, fs, rowback);
+    } else {
+        if (xs)
+            hipLaunchKernelGGL((gemm_stage_wide_kernel<3, true>), sg, dim3(512), 0, st, x, m, k, fa, fs, rowback);
+        else
+            hipLaunchKernelGGL((gemm_stage_wide_kernel<3, false>), sg, dim3(512), 0, st, x, m, k, fa, fs, rowback);
+    }
+    return (int)hipGetLastError();
+}
+
 int launch_gemm_wide(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     int ks = 0, sr = 0, sw = 0;
     const bool skinny = gemm_skinny_plan(a, &sr, &sw);
@@ -739,12 +759,7 @@ int launch_gemm_wide(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     auto xa = reinterpret_cast<u32x4 *>(sc.xh);
     auto xs = reinterpret_cast<u32x4 *>(sc.xs);
     auto xin = reinterpret_cast<const uint16_t *>(a.x);
-    const dim3 sg((unsigned)(nrg * 16));
-    if (a.k <= 4096)
-        hipLaunchKernelGGL(gemm_stage_wide_kernel<1>, sg, dim3(512), 0, st, xin, a.m, a.k, xa, xs, sc.rowback);
-    else
-        hipLaunchKernelGGL(gemm_stage_wide_kernel<3>, sg, dim3(512), 0, st, xin, a.m, a.k, xa, xs, sc.rowback);
-    int e = (int)hipGetLastError();
+    int e = launch_stage_wide(xin, a.m, a.k, xa, xs, sc.rowback, stream);
     if (e) return e;
     WideArgs w{};
     w.qs = a.qs;

@@ -171,6 +171,14 @@ int gemm_wide_plan(const GemmArgs &a, int *ks);
 int gemm_skinny_plan(const GemmArgs &a, int *R, int *W);
 size_t gemm_wide_scratch(const GemmArgs &a, GemmScratch *s, uint8_t *base);
 int launch_gemm_wide(const GemmArgs &a, const GemmScratch &sc, void *stream);
+// the wide kernels' activation staging (bf16 x, K a multiple of 256 up to 12288): f16 of
+// x * 2^s_row in fragment order, 2^-s_row per row, and (xs given) the Q4_K min-term operands
+int launch_stage_wide(const uint16_t *x, int64_t m, int64_t k, void *xa, void *xs, float *rowback, void *stream);
+// Q8_0 wide kernel (nnq_gemm_wide8.hip): column tiles per workgroup (0: not its shape) and
+// K split; its scratch; the staging and the kernel (and the slab sum with a split)
+int gemm_wide8_plan(const GemmArgs &a, int *ks);
+size_t gemm_wide8_scratch(const GemmArgs &a, GemmScratch *s, uint8_t *base);
+int launch_gemm_wide8(const GemmArgs &a, const GemmScratch &sc, void *stream);
 // split-K result: ks f32 slabs [m][n] summed in order, plus the bias, to f32 or bf16 (n % 4 == 0)
 int launch_gemm_finalize(const float *ys, int ks, const float *bias, void *y, int y_bf16, int64_t m, int64_t n,
                          void *stream);

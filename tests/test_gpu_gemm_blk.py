@@ -152,3 +152,24 @@ def test_gemm_row_chunks(O, dev, fmt):
         check_close(oracle_linear(O, fmt, b, n, k, xs), y[r0:r0 + 64], f"{fmt} rows {r0}..{r0 + 63} of {m}")
     del x
     torch.cuda.empty_cache()
+
+
+# The Q8_0 wide kernel (nnq_gemm_wide8.hip: bf16 activations, more than 128 rows, K a
+# multiple of 256): 2 or 4 column tiles per workgroup, the K range split in two (slab sum)
+# when the workgroups alone would leave CUs idle, partial row tiles, random block bytes.
+@pytest.mark.parametrize("m,n,k", [(300, 4096, 4096), (512, 4096, 4096), (700, 1024, 2048), (129, 2048, 12288),
+                                   (1000, 768, 256), (260, 12288, 4096), (1100, 320, 1024)])
+def test_gemm_q80_wide(O, dev, m, n, k):
+    import nn_amd
+    b = rand_bytes("q8_0", n, k, seed=m + n + k)
+    w = make_weight("q8_0", b, n, k)
+    x = nn_amd.synth_normal(m + 5, 2, (m, k), 1.0)
+    bias = torch.from_numpy(nn_amd.synth_normal(m, 3, (n,), 0.5)).to(dev)
+    xt = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    y = nn_amd.quantized_linear(xt, w, bias)
+    assert torch.equal(y, nn_amd.quantized_linear(xt, w, bias)), "not deterministic"
+    ref = oracle_linear(O, "q8_0", b, n, k, xt.float().cpu().numpy()) + bias.cpu().numpy()
+    check_close(ref, y.cpu().numpy(), f"q8_0 wide {m}x{n}x{k}")
+    # the bf16 output is the f32 result rounded once
+    yb = nn_amd.quantized_linear(xt, w, bias, out_dtype=torch.bfloat16)
+    assert torch.equal(yb, y.to(torch.bfloat16)), "bf16 output is not the f32 result rounded once"
