@@ -50,6 +50,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 MFMA16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 METRIC = "Q4_K GEMV GB/s (% HBM peak) at 4096x12288; prefill TFLOP/s at M=512"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+TRAFFIC_FILE_REL = "profiles/traffic.json"
 PROBE_LIB = os.path.join(ROOT, "nn_amd", "libnnq_probe.so")
 
 
@@ -191,11 +192,37 @@ def windows_for(steps, per_call_s, budget_s=0.5, lo=5, hi=40):
     return int(max(lo, min(hi, budget_s / max(steps * per_call_s, 1e-9))))
 
 
+def trace_fields(tr, algo_bytes, st):
+    """The roofline's profile-derived figures for a config of profiles/traffic.json: the
+    fraction from the rocprofv3 kernel trace taken at the bench's own cadence (the same
+    launches, eager windows of --steps 20), the traced empty kernel of the same run, and
+    where the traffic figure comes from."""
+    if not tr:
+        return {}
+    out = {"traffic_source": f"{TRAFFIC_FILE_REL} configs.{tr['name']}: FETCH_SIZE and WRITE_SIZE per dispatch "
+                             f"(the table of {tr['source']}, one counter per rocprofv3 run) scaled by a 256 MiB "
+                             f"device copy under the same counters"}
+    t = tr.get("trace")
+    if t:
+        out["frac_trace"] = round(algo_bytes / (t["avg_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        out["trace"] = {"kernel_avg_us": t["avg_us"], "kernel_median_us": t["median_us"],
+                        "kernel_p10_us": t["p10_us"], "kernel_p90_us": t["p90_us"], "dispatches": t["dispatches"],
+                        "empty_kernel_avg_us": t["empty_avg_us"],
+                        "event_us_per_step_p10_p90": [round(st["p10"] * 1e6, 3), round(st["p90"] * 1e6, 3)],
+                        "source": f"{t['source']} ({t['command']})",
+                        "note": "traced kernel durations run from each dispatch's start to its end, so they "
+                                "leave out the gaps between launches that the event-timed value includes; the "
+                                "empty kernel of the same traced run shows what a dispatch that does nothing "
+                                "takes under the tracer"}
+    return out
+
+
 def traffic_record(name):
     if not os.path.exists(TRAFFIC_FILE):
         return None
     with open(TRAFFIC_FILE) as fh:
-        return json.load(fh).get("configs", {}).get(name)
+        rec = json.load(fh).get("configs", {}).get(name)
+    return dict(rec, name=name) if rec else None
 
 
 # ---------------------------------------------------------------------------------
@@ -757,7 +784,8 @@ def main():
                       if "st_long" in r else {})},
         "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": tr["traffic_bytes_per_launch"] if tr else None},
+                     "traffic": tr["traffic_bytes_per_launch"] if tr else None,
+                     **trace_fields(tr, r["algo_bytes"], r["st"])},
         "cpu_baseline": cpu,
         "configs": configs or None,
     }
