@@ -570,13 +570,18 @@ def cpu_baselines(head, lm, gemms, mi, budget):
     # 32 experts on every expert call, sampled over 2 expert calls and scaled
     if mi is not None:
         args = (mi["x"], mi["lg"], mi["K"], mi["gp"], mi["gs"], mi["gb"], mi["dp"], mi["ds"], mi["db"], mi["I"])
-        both("mxfp4_moe_decode_once", lambda th: (lambda: CB.moe_forward(*args, threads=th)), budget / 2)
+        E, H = mi["lg"].shape[1], mi["x"].shape[1]
+        once = CB.moe_buffers(E, H, mi["I"])
+        both("mxfp4_moe_decode_once", lambda th: (lambda: CB.moe_forward(*args, threads=th, bufs=once)), budget / 2)
+        del once
         used = mi.get("experts_used", 32)
         r = {}
+        every = CB.moe_buffers(E, H, mi["I"], faithful=True)
         for th in (1, allt):
             with CB.blas_threads(th):
+                CB.moe_forward(*args, faithful=True, expert_limit=1, threads=th, bufs=every)  # first touch
                 t0 = time.perf_counter()
-                _, ran = CB.moe_forward(*args, faithful=True, expert_limit=2, threads=th)
+                _, ran = CB.moe_forward(*args, faithful=True, expert_limit=2, threads=th, bufs=every)
                 dt = (time.perf_counter() - t0) / ran * used
             r[f"t{th}"] = {"sec": dt, "calls": 1, "sample": f"{ran} of {used} expert calls, scaled by {used}/{ran}"}
             log(f"  cpu mxfp4_moe_faithful threads={th}: {dt * 1e3:.1f} ms/call (sampled)")

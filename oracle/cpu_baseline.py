@@ -128,15 +128,23 @@ def argmax(v) -> int:
     return int(lib().cb_argmax(_p(v, _f32p), v.size))
 
 
+def moe_buffers(E, H, inter, faithful=False):
+    """moe_forward's decode buffers (gate_up, down), allocated once by the caller so that
+    no timed call pays first-touch page faults"""
+    n = E if faithful else 1
+    return np.empty(n * H * 2 * inter, np.float32), np.empty(n * inter * H, np.float32)
+
+
 def moe_forward(x, logits, top_k, gp, gs, gb, dp, ds, db, inter, limit=7.0, faithful=False, expert_limit=0,
-                threads=1):
+                threads=1, bufs=None):
     """QuantizedDecoderLayer::moe_forward with router logits given
     (crates/nn-gptoss/src/quantized_model.rs:132-194): softmax, top-k, renormalise, then per
     expert in ascending order over its tokens: x @ Wgu + b, clamp(silu(gate)) * up,
     @ Wd + b, weighted index_add.  faithful: every expert call decodes all experts'
     weights (expert_forward, :107, :123), as the reference does; otherwise only the expert
     in use.  expert_limit > 0 runs only that many experts that have tokens (a bounded
-    sample).  Returns (y, experts run).  Call inside blas_threads(threads)."""
+    sample).  bufs: moe_buffers(...) of the same form, else allocated here.  Returns (y,
+    experts run).  Call inside blas_threads(threads)."""
     x = np.asarray(x, np.float32)
     logits = np.asarray(logits, np.float32)
     T, H = x.shape
@@ -150,8 +158,7 @@ def moe_forward(x, logits, top_k, gp, gs, gb, dp, ds, db, inter, limit=7.0, fait
     tw = np.take_along_axis(p, ti, axis=1)
     tw = tw / tw.sum(axis=1, keepdims=True)
     y = np.zeros((T, H), np.float32)
-    wgu = np.empty((E if faithful else 1) * gu_per, np.float32)
-    wdn = np.empty((E if faithful else 1) * dn_per, np.float32)
+    wgu, wdn = bufs if bufs is not None else moe_buffers(E, H, I, faithful)
     ran = 0
     for e in range(E):
         rows, slots = np.nonzero(ti == e)
