@@ -71,7 +71,8 @@ def build(verbose: bool = False) -> str:
     nlib = len(HIP_SOURCES) + len(HOST_SOURCES)
     for out, parts in ((LIB, objs[:nlib]), (PROBE_LIB, objs[nlib:])):
         tmp = out + ".tmp"
-        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *parts, "-lpthread"])
+        # -z defs: a kernel whose launch stub the host pass dropped fails here, not at load time
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *parts, "-lpthread"])
         os.replace(tmp, out)
         if verbose:
             print(f"built {out}")

@@ -801,6 +801,15 @@ constexpr size_t moe_lds(int64_t KB) {
 // and r + 2 .. r + 6 land in different banks; the xor stays inside aligned groups of 4
 __device__ __forceinline__ int moe_slot(int kc, int r) { return kc ^ ((r >> 1) & 3); }
 
+// One 16-byte-per-lane copy from a buffer resource straight into LDS (the wave's 64
+// granules land contiguously at `lds`); an offset past the resource's range copies zeros.
+// (The host pass has no such builtin and would drop the kernels' launch stubs.)
+__device__ inline void moe_copy16_lds(__amdgpu_buffer_rsrc_t r, unsigned char *lds, uint32_t voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
+#endif
+}
+
 __host__ __device__ constexpr int moe_streams(bool gu, int64_t H, int64_t I) { return (int)(gu ? I / 32 : H / 32); }
 
 template <int P, bool GU, int CKB, bool SL>
@@ -893,6 +902,16 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
         // the host keeps them under 4 GB), so a copy address costs one VGPR, not two
         const unsigned char *abase = reinterpret_cast<const unsigned char *>(GU ? run.xa[0] : sc.hb);
         const int64_t pstride = GU ? (run.xa[1] ? run.xa[1] - run.xa[0] : 0) : run.A * I;  // elements per plane
+        // the copies go through a buffer resource over the activation's planes: a granule of a
+        // row tile with no live rows gets an offset past the range, so its copy instruction is
+        // still issued (every wave issues the same batches: the vmcnt waits below count them)
+        // but reads nothing and writes zeros that no MFMA reads
+        // (the planes span at most 2^31 bytes under the size limits and token chunking, so
+        // live offsets stay below the record count and 2^31 plus the chunk's scalar offset
+        // is past it without wrapping)
+        const int64_t abytes = 2 * ((int64_t)(P - 1) * pstride + (GU ? run.T * H : run.A * I));
+        const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned char *>(abase), 0, (int)(uint32_t)min(abytes, (int64_t)0x80000000), 0x00020000);
         uint32_t aoff[LPA];
 #pragma unroll
         for (int j = 0; j < LPA; j++) {
@@ -902,17 +921,15 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_stream_kernel(MoeDev d, Mo
             const int kc = moe_slot(slot, r);  // the row's 16-byte granule held at this slot
             const int32_t rr = r0 + m0 + min(r, ne - m0 - 1);  // rows past the expert repeat its last row
             const int64_t tok = GU ? (run.perm ? tok_s[rr - r0] : sc.stok[rr]) : 0;
-            aoff[j] = (uint32_t)(2 * ((int64_t)pl * pstride + (GU ? tok * H : (int64_t)rr * I) + 8 * kc));
+            aoff[j] = r < 16 * mtn ? (uint32_t)(2 * ((int64_t)pl * pstride + (GU ? tok * H : (int64_t)rr * I) + 8 * kc))
+                                   : 0x80000000u;
         }
         auto issue = [&](int ch) {
             const int cv = min(ch, nch - 1);  // past the end: re-copy the last chunk
             unsigned char *buf = smem + (size_t)(ch % NBUF) * C::BUF;
-            const unsigned char *cb = abase + (size_t)cv * CKB * 64;
 #pragma unroll
             for (int j = 0; j < LPA; j++)
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(cb + aoff[j]),
-                                                 (__attribute__((address_space(3))) void *)(buf + (size_t)(j * NTH + wv * 64) * 16),
-                                                 16, 0, 0);
+                moe_copy16_lds(ars, buf + (size_t)(j * NTH + wv * 64) * 16, aoff[j], cv * CKB * 64);
         };
         const int nround = (s_hi - s_lo + kMoeWaves - 1) / kMoeWaves;
         for (int rd = 0; rd < nround; rd++) {
