@@ -24,7 +24,7 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 
 HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_gemm_wide.hip", "nnq_gemm_wide8.hip",
-               "nnq_gemm_blk.hip", "nnq_moe.hip", "nnq_sample.hip"]
+               "nnq_gemm_thin.hip", "nnq_gemm_blk.hip", "nnq_moe.hip", "nnq_sample.hip"]
 # per-file device flags: the block-scaled GEMM's MFMAs write their partials to VGPRs (the
 # FMAs that scale them read VGPRs only; with the default accumulator registers every
 # partial costs four extra register reads)
@@ -33,7 +33,8 @@ HIP_SOURCES = ["nnq_gemv.hip", "nnq_gemm.hip", "nnq_gemm_ring.hip", "nnq_gemm_wi
 # kernel-argument fetch: at 4096x12288 the GEMV is launch- and latency-bound at ~7 us.
 PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
 VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
-EXTRA_FLAGS = {"nnq_gemm_blk.hip": VGPR_MFMA, "nnq_gemm_wide8.hip": VGPR_MFMA, "nnq_gemv.hip": PRELOAD,
+EXTRA_FLAGS = {"nnq_gemm_blk.hip": VGPR_MFMA, "nnq_gemm_wide8.hip": VGPR_MFMA, "nnq_gemm_thin.hip": VGPR_MFMA,
+               "nnq_gemv.hip": PRELOAD,
                "nnq_probe.hip": PRELOAD}
 HOST_SOURCES = ["nnq_abi.cpp", "nnq_plan.cpp", "nnq_repack.cpp", "nnq_host.cpp", "nnq_gguf.cpp"]
 # measurement probes for bench.py (streaming-read floor, empty launch), a library of their own

@@ -47,6 +47,10 @@ bool use_ring(const GemmArgs &a) { return !a.blk && gemm_ring_plan(a, nullptr) >
 GemmScratch gemm_carve(void *base, const GemmArgs &a, size_t *bytes) {
     const int P = a.x_bf16 ? 1 : 2;
     uint8_t *b = reinterpret_cast<uint8_t *>(base);
+    if (gemm_thin_plan(a, nullptr, nullptr)) {
+        if (bytes) *bytes = 0;
+        return GemmScratch{};
+    }
     if (!a.blk && (gemm_skinny_plan(a, nullptr, nullptr) || gemm_wide_plan(a, nullptr))) {
         GemmScratch s{};
         const size_t off = gemm_wide_scratch(a, &s, b);
@@ -526,6 +530,7 @@ int launch_gemm_prep(const GemmArgs &a, const GemmScratch &sc, void *stream) {
 
 int launch_gemm_q4k(const GemmArgs &a, void *stream) {
     if (a.m <= 0) return 0;
+    if (gemm_thin_plan(a, nullptr, nullptr)) return launch_gemm_thin(a, stream);
     const GemmScratch sc = gemm_carve(a.scratch, a, nullptr);
     if (gemm_skinny_plan(a, nullptr, nullptr) || gemm_wide_plan(a, nullptr)) return launch_gemm_wide(a, sc, stream);
     hipStream_t st = (hipStream_t)stream;

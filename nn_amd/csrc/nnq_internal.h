@@ -144,6 +144,10 @@ struct GemmArgs {
     int blk;  // 0: Q4_K; NNQ_FMT_Q8_0 / NNQ_FMT_Q6_K: the block-scaled GEMM (nnq_gemm_blk.hip)
 };
 int launch_gemm_q4k(const GemmArgs &a, void *stream);
+// one-launch Q4_K GEMM for a few bf16 token rows (nnq_gemm_thin.hip): whether it takes
+// the shape (R, W: tiles per workgroup and waves), and its launch; no scratch
+int gemm_thin_plan(const GemmArgs &a, int *R, int *W);
+int launch_gemm_thin(const GemmArgs &a, void *stream);
 // Q8_0 / Q6_K prefill GEMM (M > 8): the activation staging below, then one kernel
 int launch_gemm_blk(const GemmArgs &a, void *stream);
 // its K split (and tile height and width, when bm / bn are given)

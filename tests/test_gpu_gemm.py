@@ -50,6 +50,29 @@ def test_gemm_small_vs_oracle(O, dev, m, n, k, xdt):
     check_close(ref, y, f"gemm m={m} n={n} k={k} x={xdt}")
 
 
+@pytest.mark.parametrize("m,n,k", [
+    (16, 9216, 4096),  # three tiles per workgroup, sixteen waves, one super-block each
+    (11, 9216, 6144),  # three tiles, eight waves over 24 super-blocks: three per wave
+    (5, 4096, 12288),  # one tile, sixteen waves over 48 super-blocks
+    (13, 256, 512),    # one tile, two super-blocks: fourteen waves without one
+    (7, 100, 768),     # N not a multiple of 16 (the last tile's extra columns unwritten)
+])
+def test_gemm_thin_configs(O, dev, m, n, k):
+    """The one-launch kernel for 5..16 bf16 token rows (nnq_gemm_thin.hip) in each of its
+    launch configurations, on random block bytes (arbitrary finite d, dmin, scales), with
+    a bias, f32 and bf16 outputs (bf16: the f32 result rounded once)."""
+    import nn_amd
+    b = rand_bytes("q4_k", n, k, seed=1000 + m + n)
+    w = make_weight("q4_k", b, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(m, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    bias = torch.from_numpy(nn_amd.synth_normal(m + 1, 3, (n,), 0.5)).to(dev)
+    y32 = nn_amd.quantized_linear(x, w, bias)
+    yb = nn_amd.quantized_linear(x, w, bias, out_dtype=torch.bfloat16)
+    ref = ref_f64(O, b, n, k, x.float().cpu().numpy()) + bias.cpu().numpy()
+    check_close(ref, y32.cpu().numpy(), f"thin m={m} n={n} k={k}")
+    assert torch.equal(yb, y32.to(torch.bfloat16)), "bf16 output is the f32 result rounded once"
+
+
 def test_gemm_legacy_random_blocks(O, dev):
     """nn-gguf layout with random block bytes (arbitrary finite d / dmin / scales)."""
     import nn_amd
