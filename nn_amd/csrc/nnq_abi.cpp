@@ -489,13 +489,14 @@ static GemmArgs gemm_args(const nnq_weight *w, const void *x, nnq_dtype x_dtype,
 
 // scratch a linear call of m tokens needs (the prefill GEMM's staging and split-K slabs)
 // MFMA GEMM or GEMV passes (of up to 8 tokens for Q8_0, 4 otherwise), by the measured
-// crossover on MI355X: Q4_K from 5 tokens with bf16 activations (8 tokens at 4096x12288:
-// 23.6 us as two GEMV passes, 20.7 as GEMM) and from 9 with f32 ones (23.6 against 28.4
-// at 8), Q6_K from 9 (8 tokens at 4096x12288: two batched passes 27 us, GEMM 36.8), Q8_0
+// crossover on MI355X: Q4_K from 3 tokens with bf16 activations (the one-launch thin
+// GEMM: 3 and 4 tokens at 12288x4096 in 8.8 / 8.9 us against 10.3 / 10.5 as a GEMV pass,
+// level at 4096x12288; 2 tokens: 8.7 against 7.7) and from 9 with f32 ones (23.6 against
+// 28.4 at 8), Q6_K from 9 (8 tokens at 4096x12288: two batched passes 27 us, GEMM 36.8), Q8_0
 // from 9 with bf16 activations and from 17 with f32 ones (8 tokens in one batched GEMV
 // pass: 7.9 us at 4096x4096, 17.9 at 4096x12288; 9 f32 tokens as GEMM: 20.9 and 39.2 us)
 static bool gemm_batch(const nnq_weight *w, int64_t m, nnq_dtype x_dtype) {
-    if (w->L.fmt == NNQ_FMT_Q4_K) return m > (x_dtype == NNQ_BF16 ? 4 : 8);
+    if (w->L.fmt == NNQ_FMT_Q4_K) return m > (x_dtype == NNQ_BF16 ? 2 : 8);
     if (w->L.fmt == NNQ_FMT_Q6_K) return m > 8;
     return m > (x_dtype == NNQ_BF16 ? 8 : 16);
 }

@@ -1,4 +1,4 @@
-// Prefill GEMM for Q4_K weights at 5 .. 16 bf16 token rows on gfx950, in one launch:
+// Prefill GEMM for Q4_K weights at 3 .. 16 bf16 token rows on gfx950, in one launch:
 // Y[m, n] = X[m, k] . W[n, k]^T (+ bias), the arithmetic of QLinear::forward with a few
 // tokens (crates/nn-core/src/layers/quantized/linear.rs:366-400; the bf16 result dtype of
 // crates/nn-core/src/dyn_tensor/ops/matmul.rs:37-38).
@@ -219,14 +219,14 @@ int launch_thin_cfg(const ThinArgs &t, hipStream_t st) {
 
 }  // namespace
 
-// The thin kernel's shape rules: Q4_K, bf16 activations, 5 to 16 rows.  R = 3 tiles per
+// The thin kernel's shape rules: Q4_K, bf16 activations, 3 to 16 rows.  R = 3 tiles per
 // workgroup when that gives at least 192 workgroups, else 1 (two tiles on 128 workgroups
 // measured slower: every workgroup reads the whole activation, but half the CUs stream
 // the weight).  Sixteen waves, except three tiles over more than 16 units (eight: the
 // double-buffered loads of three tiles take 199 registers).  Returns 1 when it takes the
 // shape (and R, W: tiles per workgroup and waves).
 int gemm_thin_plan(const GemmArgs &a, int *R, int *W) {
-    if (a.blk || !a.x_bf16 || a.m <= 4 || a.m > 16 || a.k % 256 || (int64_t)a.m * a.k > (int64_t)1 << 29) return 0;
+    if (a.blk || !a.x_bf16 || a.m <= 2 || a.m > 16 || a.k % 256 || (int64_t)a.m * a.k > (int64_t)1 << 29) return 0;
     const int r = (a.ntile % 3 == 0 && a.ntile / 3 >= 192) ? 3 : 1;
     if (R) *R = r;
     if (W) *W = (r == 3 && a.nblk > 16) ? 8 : 16;

@@ -342,14 +342,14 @@ __global__ __launch_bounds__(NTH, 1) void gemm_q4k_wide_kernel(WideArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// Skinny GEMM (5 .. 32 rows, bf16 activations): the weight is streamed once, like a decode
-// GEMV.  One workgroup per R consecutive weight tiles (16 columns each); its W waves split
+// Skinny GEMM (17 .. 32 rows, bf16 activations; up to 16 rows take the one-launch thin
+// kernel of nnq_gemm_thin.hip): the weight is streamed once, like a decode GEMV.  One workgroup per R consecutive weight tiles (16 columns each); its W waves split
 // K by units of 256 (unit u to wave u % W).  Each wave runs all MT row tiles of the batch
 // against its R tiles: it dequantizes its B fragments in registers straight from the tile16
 // bytes (the wide kernel's exact sc * q operands, here without any LDS or barrier in the
 // loop), shares every A fragment (the same staged activation planes) across the R tiles,
 // and keeps the d-scaled totals and the min term as the wide kernel does.  The raw bytes of
-// a wave's next D units are loaded while it computes the current one.  At the end the waves'
+// a wave's next unit are loaded while it computes the current one.  At the end the waves'
 // totals meet in LDS and the workgroup writes its M x 16 R outputs.
 // ---------------------------------------------------------------------------------
 template <int R, int MT, int W>
@@ -357,9 +357,7 @@ struct Skinny {
     static constexpr int LDS = W * R * MT * 1024;  // every wave's totals, f32
 };
 
-// D = 0: a wave's next unit's raw bytes load during the current one and each step loads its
-// A fragments; D = 1: the burst schedule (A fragments one unit ahead, raw bytes two)
-template <int R, int MT, int W, int D>
+template <int R, int MT, int W>
 __global__ __launch_bounds__(W * 64) void gemm_q4k_skinny_kernel(WideArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -409,9 +407,8 @@ __global__ __launch_bounds__(W * 64) void gemm_q4k_skinny_kernel(WideArgs a) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) tot[r][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // the unit body: unit u from ring slot `cur`; with apre, its A fragments were loaded
-    // one unit ahead (ap[step][mt]), else each step loads its own
-    auto unit = [&](int u, const Raw &cur, const u32x4 (*apre)[MT]) {
+    // the unit body: unit u from the raw bytes `cur`; each step loads its A fragments
+    auto unit = [&](int u, const Raw &cur) {
         u32x4 xsf[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) xsf[mt] = bload4(rxs[mt], loff, u * 1024);
@@ -437,7 +434,7 @@ __global__ __launch_bounds__(W * 64) void gemm_q4k_skinny_kernel(WideArgs a) {
         for (int s = 0; s < 8; s++) {
             const int p = s >> 1;
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) af[mt] = apre ? apre[s][mt] : bload4(ra[mt], loff, (u * 8 + s) * 1024);
+            for (int mt = 0; mt < MT; mt++) af[mt] = bload4(ra[mt], loff, (u * 8 + s) * 1024);
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const uint32_t w0 = cur.q[r][p][0], w1 = cur.q[r][p][1], w0s = w0 >> 8, w1s = w1 >> 8;
@@ -466,41 +463,13 @@ __global__ __launch_bounds__(W * 64) void gemm_q4k_skinny_kernel(WideArgs a) {
     };
     // this wave's units wv, wv + W, ...
     const int nu = nblk > wv ? (nblk - wv + W - 1) / W : 0;
-    if constexpr (D == 0) {
-        // one unit's raw bytes ahead, A fragments loaded by each step
-        Raw cur, nxt;
-        if (nu > 0) load_raw(wv, cur);
-        for (int i = 0; i < nu; i++) {
-            if (i + 1 < nu) load_raw(wv + (i + 1) * W, nxt);
-            unit(wv + i * W, cur, nullptr);
-            if (i + 1 < nu) cur = nxt;
-        }
-    } else {
-        // Loads in bursts, because the vector memory counter retires loads in issue order:
-        // at the start of unit i come all A fragments of unit i + 1, then the raw bytes of
-        // unit i + 2, so every wait inside unit i is on loads issued a unit or more before
-        // (the HBM-latency raw loads never hold up an A fragment needed soon).
-        Raw rw[3];
-        u32x4 ab[2][8][MT];
-        auto load_a = [&](int i, u32x4 (*dst)[MT]) {
-#pragma unroll
-            for (int s = 0; s < 8; s++)
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) dst[s][mt] = bload4(ra[mt], loff, ((wv + i * W) * 8 + s) * 1024);
-        };
-        if (nu > 0) load_raw(wv, rw[0]);
-        if (nu > 0) load_a(0, ab[0]);
-        if (nu > 1) load_raw(wv + W, rw[1]);
-        for (int i0 = 0; i0 < nu; i0 += 6) {
-#pragma unroll
-            for (int j = 0; j < 6; j++) {
-                const int i = i0 + j;
-                if (i >= nu) break;
-                if (i + 1 < nu) load_a(i + 1, ab[(j + 1) & 1]);
-                if (i + 2 < nu) load_raw(wv + (i + 2) * W, rw[(j + 2) % 3]);
-                unit(wv + i * W, rw[j % 3], ab[j & 1]);
-            }
-        }
+    // one unit's raw bytes ahead
+    Raw cur, nxt;
+    if (nu > 0) load_raw(wv, cur);
+    for (int i = 0; i < nu; i++) {
+        if (i + 1 < nu) load_raw(wv + (i + 1) * W, nxt);
+        unit(wv + i * W, cur);
+        if (i + 1 < nu) cur = nxt;
     }
     // the waves' totals meet in LDS: [W][R][MT][64 lanes] floatx4
 #pragma unroll
@@ -649,18 +618,16 @@ int gemm_wide_plan(const GemmArgs &a, int *ks) {
     return 0;
 }
 
-// The skinny kernel's shape rules: bf16 activations, 5 to 32 rows, K <= 4096 * 3 (the
-// staging), whole groups of R tiles.  R = 3 tiles per workgroup when that gives at least
-// 192 workgroups, else 1; with one tile per workgroup only up to 16 rows (every workgroup
-// reads the whole staged activation: from 17 rows on, and at 48 and 64 rows for either R,
-// the ring kernel measured as fast or faster on MI355X).  W = 8 waves over K (measured
-// against 4).  Returns 1 when the kernel takes the shape.
+// The skinny kernel's shape rules: bf16 activations, 17 to 32 rows (fewer: the thin
+// kernel), K <= 4096 * 3 (the staging), R = 3 tiles per workgroup giving at least 192
+// workgroups (with one tile per workgroup every workgroup reads the whole staged
+// activation: there, and at 48 and 64 rows, the ring kernel measured as fast or faster
+// on MI355X).  W = 8 waves over K (measured against 4).  Returns 1 when the kernel takes
+// the shape.
 int gemm_skinny_plan(const GemmArgs &a, int *R, int *W) {
-    if (a.blk || !a.x_bf16 || a.m <= 4 || a.m > 32 || a.k > 4096 * 3) return 0;
-    const int mt = (int)((a.m + 15) / 16);
-    const int r = (a.ntile % 3 == 0 && a.ntile / 3 >= 192) ? 3 : 1;
-    if (mt == 2 && r == 1) return 0;  // 17 to 32 rows over one tile per workgroup: the ring kernel is as fast
-    if (R) *R = r;
+    if (a.blk || !a.x_bf16 || a.m <= 16 || a.m > 32 || a.k > 4096 * 3) return 0;
+    if (a.ntile % 3 != 0 || a.ntile / 3 < 192) return 0;
+    if (R) *R = 3;
     if (W) *W = 8;
     return 1;
 }
@@ -706,28 +673,15 @@ static int launch_wide_nt(const WideArgs &w, hipStream_t st) {
 template <int R, int MT, int W>
 static int launch_skinny_cfg(const WideArgs &w, hipStream_t st) {
     using C = Skinny<R, MT, W>;
-    constexpr int D = (R == 1 && MT <= 2) ? 1 : 0;  // the burst schedule where the registers allow
     static bool attr_set = false;  // idempotent attribute write; races only repeat it
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_skinny_kernel<R, MT, W, D>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_q4k_skinny_kernel<R, MT, W>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((gemm_q4k_skinny_kernel<R, MT, W, D>), dim3((unsigned)(w.ntile / R)), dim3(W * 64), C::LDS, st,
-                       w);
+    hipLaunchKernelGGL((gemm_q4k_skinny_kernel<R, MT, W>), dim3((unsigned)(w.ntile / R)), dim3(W * 64), C::LDS, st, w);
     return (int)hipGetLastError();
-}
-
-template <int R, int W>
-static int launch_skinny_r(const WideArgs &w, hipStream_t st) {
-    switch ((w.m + 15) / 16) {
-        case 1: return launch_skinny_cfg<R, 1, W>(w, st);
-        case 2: return launch_skinny_cfg<R, 2, W>(w, st);
-        case 3: if constexpr (R == 1) return launch_skinny_cfg<R, 3, W>(w, st); break;
-        case 4: if constexpr (R == 1) return launch_skinny_cfg<R, 4, W>(w, st); break;
-    }
-    return (int)hipErrorInvalidValue;
 }
 
 int launch_stage_wide(const uint16_t *x, int64_t m, int64_t k, void *xa, void *xs, float *rowback, void *stream) {
@@ -779,7 +733,7 @@ int launch_gemm_wide(const GemmArgs &a, const GemmScratch &sc, void *stream) {
     w.ks = skinny ? 1 : ks;
     w.nrg = (int)nrg;
     if (skinny) {
-        return sr == 3 ? launch_skinny_r<3, 8>(w, st) : launch_skinny_r<1, 8>(w, st);
+        return launch_skinny_cfg<3, 2, 8>(w, st);  // the plan: 17 to 32 rows, three tiles, eight waves
     }
     e = nt == 6 ? launch_wide_nt<6>(w, st) : launch_wide_nt<4>(w, st);
     if (e || ks == 1) return e;

@@ -116,12 +116,13 @@ def test_gemm_bias_bf16_out_and_nan_row(O, dev):
     assert np.isnan(yn[5]).all() and np.isfinite(np.delete(yn, 5, axis=0)).all()
 
 
-@pytest.mark.parametrize("m,xdt", [(16, "bf16"), (64, "bf16"), (128, "bf16"), (512, "bf16"), (64, "f32"), (5, "bf16")])
+@pytest.mark.parametrize("m,xdt", [(16, "bf16"), (64, "bf16"), (128, "bf16"), (512, "bf16"), (64, "f32"), (5, "bf16"),
+                                   (3, "bf16")])
 @pytest.mark.parametrize("n,k", [(12288, 4096), (4096, 12288)])
 def test_gemm_baseline_shapes(O, dev, m, n, k, xdt):
     """Config 4: both Qwen3-8B MLP matrices at M = 16, 64, 128 (the GEMV-to-GEMM
     crossover) and 512, bf16 activations, f32 and bf16 outputs; also f32 activations
-    and a 5-token batch (the smallest that runs the GEMM)."""
+    and 5- and 3-token batches (3: the smallest that runs the GEMM)."""
     import nn_amd
     wb = q4k_bytes(n, k, seed=4000 + k)
     w = make_weight("q4_k", wb, n, k)

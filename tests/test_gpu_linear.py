@@ -200,12 +200,13 @@ def test_q4k_decode_launch_shapes(O, dev, k, m, xdt):
 
 
 @pytest.mark.parametrize("fmt,m,xdt", [("q4_k", 5, "bf16"), ("q4_k", 6, "bf16"), ("q4_k", 8, "bf16"), ("q4_k", 6, "f32"),
-                                       ("q4_k", 7, "f32"), ("q4_k", 9, "f32"), ("q4_k", 4, "bf16"),
+                                       ("q4_k", 7, "f32"), ("q4_k", 9, "f32"), ("q4_k", 4, "bf16"), ("q4_k", 3, "bf16"),
+                                       ("q4_k", 2, "bf16"),
                                        ("q6_k", 6, "f32"), ("q6_k", 7, "bf16"), ("q6_k", 8, "f32"), ("q8_0", 8, "bf16"),
                                        ("q8_0", 12, "f32"), ("q8_0", 16, "f32"), ("q8_0", 17, "f32"), ("q8_0", 5, "bf16"),
                                        ("q6_k", 3, "bf16"), ("q6_k", 9, "bf16"), ("q6_k", 5, "f32")])
 def test_linear_gemm_crossover(O, dev, fmt, m, xdt):
-    """Batches on both sides of each format's GEMV-to-GEMM crossover (Q4_K from 5 tokens
+    """Batches on both sides of each format's GEMV-to-GEMM crossover (Q4_K from 3 tokens
     with bf16 activations and from 9 with f32 ones, Q6_K from 9, Q8_0 from 9 with bf16
     and from 17 with f32 ones; smaller Q8_0 and Q6_K batches run the batched decode
     kernels in passes of 8 and 4 tokens), with a ragged tile."""
