@@ -88,16 +88,19 @@ __global__ __launch_bounds__(W * 64) void gemm_q4k_thin_kernel(ThinArgs a) {
         u32x2 q[R][4];
         u32x4 h[R];
     };
+    // issue order = use order (loads retire in order): the headers, then per pair of steps
+    // their A fragments and the tiles' codes, so a step waits only for its own loads
     auto load = [&](int u, Raw &w) {
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
+        for (int r = 0; r < R; r++) w.h[r] = thin_load4_nt(rh, hoff, (r * nblk + u) * 256);
 #pragma unroll
-            for (int s = 0; s < 8; s++) w.x[mt][s] = thin_load4(rx, xoff[mt], (u * 256 + 32 * s) * 2);
+        for (int p = 0; p < 4; p++) {
 #pragma unroll
-        for (int r = 0; r < R; r++) {
+            for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int p = 0; p < 4; p++) w.q[r][p] = thin_load2_nt(rq, qoff + 256 * p, (r * nblk + u) * 2048);
-            w.h[r] = thin_load4_nt(rh, hoff, (r * nblk + u) * 256);
+                for (int s = 2 * p; s < 2 * p + 2; s++) w.x[mt][s] = thin_load4(rx, xoff[mt], (u * 256 + 32 * s) * 2);
+#pragma unroll
+            for (int r = 0; r < R; r++) w.q[r][p] = thin_load2_nt(rq, qoff + 256 * p, (r * nblk + u) * 2048);
         }
     };
 
