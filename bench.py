@@ -23,8 +23,8 @@ torch's f16 GEMM at the prefill shapes), the other benchmark configs (Q8_0 GEMV 
 own streaming-read floor, Q4_K
 gate+up GEMV, MLP decode, the Q6_K LM head with argmax and sampling, the Q4_K prefill
 GEMMs at M = 16, 64, 128, 512, the MXFP4 MoE), and the CPU baseline: the reference's
-flow (the oracle's block decoders and a blocked f32 product, OpenMP; numpy BLAS for the
-MoE's products) on this host, one thread and all threads, with the host's core count.
+flow (the oracle's block decoders and blocked f32 products, OpenMP) on this host, one
+thread and all threads, with the host's core count.
 
 Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 200] [--windows 25]
        python bench.py --only headline --no-single    (one kernel population, for rocprofv3)

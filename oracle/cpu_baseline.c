@@ -124,6 +124,57 @@ void cb_matmul_xwt(const float *x, int64_t m, const float *w, int64_t n, int64_t
     for (int64_t jb = 0; jb < nblk; jb++) matmul_cols(x, m, w, n, k, y, jb * NC, jb * NC + NC < n ? jb * NC + NC : n);
 }
 
+/* ---- f32 product y[m][n] = x[m][k] . w[k][n] (w row-major, as the MoE experts' f32
+ * weights are laid out after decoding) ------------------------------------------------
+ * Column strips of 4 VW, rows 4 at a time: the strip's accumulators stay in registers
+ * over a k block of 256 while each row of w contributes one broadcast FMA per vector. */
+__attribute__((target_clones("avx512f", "avx2", "default"))) static void matmul_xw_cols(
+    const float *x, int64_t m, const float *w, int64_t k, int64_t n, float *y, int64_t j0, int64_t j1) {
+    const int64_t KC = 256;
+    for (int64_t i = 0; i < m; i++) memset(y + i * n + j0, 0, (size_t)(j1 - j0) * sizeof(float));
+    for (int64_t k0 = 0; k0 < k; k0 += KC) {
+        const int64_t k1 = k0 + KC < k ? k0 + KC : k;
+        for (int64_t i0 = 0; i0 < m; i0 += 4) {
+            const int64_t rows = m - i0 < 4 ? m - i0 : 4;
+            int64_t j = j0;
+            for (; j + 4 * VW <= j1; j += 4 * VW) {
+                vf acc[4][4];
+                for (int r = 0; r < 4; r++)
+                    for (int c = 0; c < 4; c++) acc[r][c] = (vf){0};
+                for (int64_t kk = k0; kk < k1; kk++) {
+                    vf wv[4];
+                    for (int c = 0; c < 4; c++) wv[c] = ldv(w + kk * n + j + c * VW);
+                    for (int r = 0; r < 4; r++) {
+                        if (r >= rows) break;
+                        const float xs = x[(i0 + r) * k + kk];
+                        for (int c = 0; c < 4; c++) acc[r][c] += xs * wv[c];
+                    }
+                }
+                for (int r = 0; r < rows; r++)
+                    for (int c = 0; c < 4; c++) {
+                        float *yp = y + (i0 + r) * n + j + c * VW;
+                        vf yv = ldv(yp);
+                        yv += acc[r][c];
+                        memcpy(yp, &yv, sizeof yv);
+                    }
+            }
+            for (; j < j1; j++)  /* scalar columns past the last whole strip */
+                for (int64_t r = 0; r < rows; r++) {
+                    float s = 0.0f;
+                    for (int64_t kk = k0; kk < k1; kk++) s += x[(i0 + r) * k + kk] * w[kk * n + j];
+                    y[(i0 + r) * n + j] += s;
+                }
+        }
+    }
+}
+
+/* columns split over the threads in blocks of 256 */
+void cb_matmul_xw(const float *x, int64_t m, const float *w, int64_t k, int64_t n, float *y, int threads) {
+    const int64_t NC = 256, nblk = (n + NC - 1) / NC;
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (int64_t jb = 0; jb < nblk; jb++) matmul_xw_cols(x, m, w, k, n, y, jb * NC, jb * NC + NC < n ? jb * NC + NC : n);
+}
+
 /* QLinear::forward with a Q4_K weight, as the reference runs it: decode all of W into the
  * caller's f32 buffer (allocated once by the caller), then y = x . W^T */
 void cb_q4k_qlinear(const uint8_t *wb, int64_t n, int64_t k, const float *x, int64_t m, float *wbuf, float *y,

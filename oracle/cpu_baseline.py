@@ -5,10 +5,12 @@ crates/nn-core/src/dyn_tensor/ops/matmul.rs:18-52).
 Benchmark infrastructure: bench.py's cpu_baseline leg and the tests that check it
 load this module; no product code does.  libcpu_baseline.so (cpu_baseline.c) holds the
 oracle's own decoders built at -O3 and run over block ranges under OpenMP, and a
-cache-blocked f32 product (x . W^T) with the columns split over OpenMP threads.  The
-MoE's products (x . W with W stored [in, out]) use numpy's BLAS, its thread count set
-through threadpoolctl.  Decoded values are bit-identical to the oracle's; products agree
-with it to f32 rounding only, so this is a speed baseline, never a parity reference.
+cache-blocked f32 product (x . W^T) with the columns split over OpenMP threads, and its
+x . W form for the MoE's experts (W stored [in, out]).  Every product runs on the same
+OpenMP threads as the decoders: with numpy's BLAS beside them, the decoders' idle OpenMP
+threads spun through the BLAS calls and all-thread runs were slower than one thread.
+Decoded values are bit-identical to the oracle's; products agree with it to f32 rounding
+only, so this is a speed baseline, never a parity reference.
 """
 from __future__ import annotations
 
@@ -40,6 +42,7 @@ def lib():
             getattr(L, name).argtypes = [_u8p, _sz, _f32p, _int]
         L.cb_dequant_mxfp4.argtypes = [_u8p, _u8p, _sz, _f32p, _int]
         L.cb_matmul_xwt.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _f32p, _int]
+        L.cb_matmul_xw.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _f32p, _int]
         L.cb_q4k_qlinear.argtypes = [_u8p, _i64, _i64, _f32p, _i64, _f32p, _f32p, _int]
         L.cb_argmax.argtypes = [_f32p, _i64]
         L.cb_argmax.restype = _i64
@@ -115,6 +118,17 @@ def matmul_xwt(x, w, threads=1, out=None):
     return out
 
 
+def matmul_xw(x, w, threads=1, out=None):
+    """y = x . w for w [k, n] row-major (f32; OpenMP over column blocks)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    m, k = x.shape
+    n = w.shape[1]
+    out = np.empty((m, n), np.float32) if out is None else out
+    lib().cb_matmul_xw(_p(x, _f32p), m, _p(w, _f32p), k, n, _p(out, _f32p), threads)
+    return out
+
+
 def q4k_qlinear(wb, n, k, x, wbuf, out, threads=1):
     """QLinear::forward with a Q4_K weight: decode all of W into wbuf (allocated once by
     the caller), then out = x . W^T."""
@@ -144,7 +158,7 @@ def moe_forward(x, logits, top_k, gp, gs, gb, dp, ds, db, inter, limit=7.0, fait
     weights (expert_forward, :107, :123), as the reference does; otherwise only the expert
     in use.  expert_limit > 0 runs only that many experts that have tokens (a bounded
     sample).  bufs: moe_buffers(...) of the same form, else allocated here.  Returns (y,
-    experts run).  Call inside blas_threads(threads)."""
+    experts run).  Decoders and products run on `threads` OpenMP threads."""
     x = np.asarray(x, np.float32)
     logits = np.asarray(logits, np.float32)
     T, H = x.shape
@@ -179,9 +193,9 @@ def moe_forward(x, logits, top_k, gp, gs, gb, dp, ds, db, inter, limit=7.0, fait
                           dn_per, threads, wdn)
             Wg = wgu.reshape(H, 2 * I)
             Wd = wdn.reshape(I, H)
-        gu = x[rows] @ Wg + gb[e]
+        gu = matmul_xw(x[rows], Wg, threads) + gb[e]
         g, u = gu[:, :I], gu[:, I:]
         h = np.clip(g / (1.0 + np.exp(-g)), -limit, limit) * u
-        yo = h @ Wd + db[e]
+        yo = matmul_xw(h, Wd, threads) + db[e]
         y[rows] += yo * tw[rows, slots][:, None]  # a token meets an expert at most once
     return y, ran

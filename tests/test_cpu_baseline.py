@@ -50,8 +50,8 @@ def test_moe_matches_oracle(O, faithful):
 
 @pytest.mark.parametrize("m,n,k", [(1, 37, 300), (5, 70, 1040), (8, 130, 2048)])
 def test_matmul_and_qlinear_match_oracle(O, m, n, k):
-    """The blocked f32 product (any m, n, k: register-block and vector tails) equals an f64
-    product to f32 rounding, at one and several threads; QLinear::forward's flow (decode,
+    """The blocked f32 products (x . W^T and x . W; any m, n, k: register-block and vector
+    tails) equal an f64 product to f32 rounding, at one and several threads; QLinear::forward's flow (decode,
     then the product) matches the oracle's decode followed by the same product."""
     rng = np.random.default_rng(m * 1000 + n)
     x = rng.standard_normal((m, k), dtype=np.float32)
@@ -60,6 +60,10 @@ def test_matmul_and_qlinear_match_oracle(O, m, n, k):
     for th in (1, 3):
         y = CB.matmul_xwt(x, w, th)
         assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max() * np.sqrt(k)
+        # the MoE experts' product x . W with W stored [k, n] (column strips of 64 and a
+        # scalar tail, rows in fours and a ragged last group)
+        y2 = CB.matmul_xw(x, np.ascontiguousarray(w.T), th)
+        assert np.abs(y2 - ref).max() <= 1e-5 * np.abs(ref).max() * np.sqrt(k)
     if k % 256 == 0:
         import nn_amd
         wb = O.quantize_q4_k(nn_amd.synth_normal(7, 1, (n, k), 0.02))
