@@ -385,7 +385,7 @@ def bench_lm_head(steps, warmup, seed=3):
                 wbytes=wb, x=x)
 
 
-def bench_gemm(m, n, k, steps, warmup, min_bytes=256 << 20, fmt="q4_k"):
+def bench_gemm(m, n, k, steps, warmup, min_bytes=512 << 20, fmt="q4_k"):
     """Config 4: X [m, k] bf16 ~ N(0,1) times Q4_K W [n, k]^T -> Y [m, n] bf16, f32 accumulate
     (fmt q8_0 / q6_k: the same product over those formats' prefill GEMM)."""
     import torch
