@@ -229,7 +229,11 @@ int launch_thin_cfg(const ThinArgs &t, hipStream_t st) {
 // double-buffered loads of three tiles take 199 registers).  Returns 1 when it takes the
 // shape (and R, W: tiles per workgroup and waves).
 int gemm_thin_plan(const GemmArgs &a, int *R, int *W) {
-    if (a.blk || !a.x_bf16 || a.m <= 2 || a.m > 16 || a.k % 256 || (int64_t)a.m * a.k > (int64_t)1 << 29) return 0;
+    // (32-bit buffer offsets: the activation's m * k * 2 bytes and three tiles' codes,
+    // 3 * nblk * 2048 bytes, stay below 2^31)
+    if (a.blk || !a.x_bf16 || a.m <= 2 || a.m > 16 || a.k % 256 || (int64_t)a.m * a.k > (int64_t)1 << 29 ||
+        a.nblk > 65536)
+        return 0;
     const int r = (a.ntile % 3 == 0 && a.ntile / 3 >= 192) ? 3 : 1;
     if (R) *R = r;
     if (W) *W = (r == 3 && a.nblk > 16) ? 8 : 16;
