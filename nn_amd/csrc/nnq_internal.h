@@ -170,7 +170,7 @@ int launch_gemm_ring(const GemmArgs &a, const GemmScratch &sc, void *stream);
 // fragment-major staged activation in xh, min-term operands in xs, rowback, split slabs;
 // s null: sizes only) and its launch (staging, kernel, and with a K split the slab sum)
 int gemm_wide_plan(const GemmArgs &a, int *ks);
-// the skinny kernel (same file and staging; bf16 activations, 5 to 32 rows): whether it
+// the skinny kernel (same file and staging; bf16 activations, 17 to 32 rows): whether it
 // takes the shape, with its tiles per workgroup R and waves W
 int gemm_skinny_plan(const GemmArgs &a, int *R, int *W);
 size_t gemm_wide_scratch(const GemmArgs &a, GemmScratch *s, uint8_t *base);

@@ -1,11 +1,12 @@
-"""GPU parity for the Q4_K prefill GEMMs of nnq_gemm_wide.hip (bf16 activations): the
-wide-wave-tile kernel (more than 128 rows) and the skinny kernel (5 to 64 rows), against
-the oracle's bit-exact decode followed by an f64 product (tolerances as in
-test_gpu_linear).  Shapes cover both wide column-tile widths (96 columns, and 64 with the
-K range split in two), the skinny kernel's 1 and 3 tiles per workgroup, 4 and 8 waves
-over K and 1 to 4 row tiles, ragged row tiles (the last tile partly past M, a row group
-partly past M), random block bytes (arbitrary finite d / dmin / scales, with d = 0
-super-blocks), bias, f32 and bf16 outputs, and repeated calls agreeing bit for bit."""
+"""GPU parity for the Q4_K prefill GEMMs of bf16 activations at every batch size the
+random-byte shapes below reach: the wide-wave-tile kernel (more than 128 rows), the
+skinny kernel (17 to 32 rows over three tiles per workgroup), the one-launch thin kernel
+(up to 16 rows) and the ring kernel between them, against the oracle's bit-exact decode
+followed by an f64 product (tolerances as in test_gpu_linear).  Shapes cover both wide
+column-tile widths (96 columns, and 64 with the K range split in two), ragged row tiles
+(the last tile partly past M, a row group partly past M), random block bytes (arbitrary
+finite d / dmin / scales, with d = 0 super-blocks), bias, f32 and bf16 outputs, and
+repeated calls agreeing bit for bit."""
 import numpy as np
 import pytest
 import torch
