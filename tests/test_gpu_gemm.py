@@ -73,6 +73,25 @@ def test_gemm_thin_configs(O, dev, m, n, k):
     assert torch.equal(yb, y32.to(torch.bfloat16)), "bf16 output is the f32 result rounded once"
 
 
+def test_gemm_thin_nonfinite_rows(O, dev):
+    """The thin kernel (7 bf16 rows): a NaN in one token's activation and an infinity in
+    another's make all of those tokens' outputs NaN (the infinity meets the offset term's
+    opposite infinity), as the staged GEMMs' per-row scale does; the other rows stay
+    within the bars."""
+    import nn_amd
+    m, n, k = 7, 96, 1024
+    wb = q4k_bytes(n, k, seed=17)
+    w = make_weight("q4_k", wb, n, k)
+    x = torch.from_numpy(nn_amd.synth_normal(17, 2, (m, k), 1.0)).to(dev).to(torch.bfloat16)
+    ref = ref_f64(O, wb, n, k, x.float().cpu().numpy())
+    x[2, 300] = float("nan")
+    x[5, 17] = float("inf")
+    y = nn_amd.quantized_linear(x, w).cpu().numpy()
+    assert np.isnan(y[2]).all() and np.isnan(y[5]).all()
+    keep = [0, 1, 3, 4, 6]
+    check_close(ref[keep], y[keep], "thin finite rows")
+
+
 def test_gemm_legacy_random_blocks(O, dev):
     """nn-gguf layout with random block bytes (arbitrary finite d / dmin / scales)."""
     import nn_amd
